@@ -1,0 +1,54 @@
+// Internal helpers shared by the khrt translation units (not installed).
+#pragma once
+
+#include "khrt.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <map>
+#include <string>
+#include <vector>
+
+namespace khrt {
+
+// Thread-local last-error message (khrt_last_error).
+void set_error(const std::string &msg);
+void clear_error();
+
+// Records `msg` (plus the HIP error string when code is a hipError_t) and
+// returns code, so call sites read `return fail(code, "...")`.
+int fail(int code, const std::string &msg);
+int fail_hip(hipError_t e, const char *what);
+
+// Ensures a device is current (ordinal 0 unless khrt_init_device chose one).
+int ensure_device();
+int current_device();
+
+// "k=v,k=v" -> map; false on any malformed segment (main.cpp:242-266).
+bool parse_shape(const std::string &text, std::map<std::string, int64_t> &out);
+
+// Verified launch used by both khrt_kernel_launch and the kh_* entry points.
+int verified_launch(void *function, khrt_dim3 grid, khrt_dim3 block, size_t shared, void *stream,
+                    void **params, size_t nparams);
+
+// Packs memref descriptors into 8-byte slots (LaunchArgs::add_memref).
+class LaunchArgs {
+ public:
+  void add_memref(const void *ptr, std::vector<int64_t> shape);
+  void add_scalar_bytes(const void *value, size_t bytes);
+  void **params();
+  size_t count() const { return slots_.size(); }
+  const std::vector<uint64_t> &slots() const { return slots_; }
+
+ private:
+  std::vector<uint64_t> slots_;
+  std::vector<void *> params_;
+};
+
+// Prelude registry: functions that need another kernel of their module
+// launched first with the same parameters (scan -> scan_reset).
+void register_prelude(void *function, void *prelude);
+void *prelude_for(void *function);
+
+}  // namespace khrt

@@ -1,0 +1,81 @@
+// fused_gelu for gfx950: out = gelu_tanh(1.5 x + 0.5), fp32, HBM-bound
+// (read x, write out: 8 B/element).
+//
+// Symbol and memref arguments follow the reference template
+// (lib/dsl/kernels/fused_gelu.cpp:73-160): x, tmp, out, rank-1 [n], 15
+// parameters. After the reference's fuse pass the producer's store to `tmp`
+// is gone (lib/passes/fusion.cpp:331-333), so `tmp` is a dead argument here
+// too: it is never read or written.
+//
+// Arithmetic (fused_gelu.cpp:113-119, 137-156):
+//   t = 1.5 x + 0.5
+//   z = 0.7978845608 (t + 0.044715 t^3)
+//   out = 0.5 t (1 + tanh z)
+// tanh is evaluated from the identity 1 + tanh z = 2 - 2 / (1 + e^{2z}),
+// with e^{2z} = 2^{2 z log2 e} on v_exp_f32 and an IEEE reciprocal-based
+// division; e^{2z} overflowing to +inf gives exactly 2, underflowing to 0
+// gives exactly 0, so the formula is finite for every finite input. The
+// absolute error of out is a few fp32 ulps of |t|, far inside the 1e-4
+// fp64-reference tolerance (e2e_fused_gelu_test.cpp:63).
+#include "kh_device.h"
+
+#ifndef KH_UNROLL
+#define KH_UNROLL 4
+#endif
+
+namespace {
+
+__device__ __forceinline__ float gelu_affine(float x) {
+  const float t = fmaf(1.5f, x, 0.5f);
+  const float t3 = t * t * t;
+  const float z = 0.7978845608f * fmaf(0.044715f, t3, t);
+  const float e = kh::exp2_hw(z * (2.0f * kh::kLog2e));
+  const float one_plus_tanh = 2.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
+  return 0.5f * t * one_plus_tanh;
+}
+
+__device__ __forceinline__ float4 gelu4(float4 v) {
+  float4 r;
+  r.x = gelu_affine(v.x);
+  r.y = gelu_affine(v.y);
+  r.z = gelu_affine(v.z);
+  r.w = gelu_affine(v.w);
+  return r;
+}
+
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(256)
+fused_gelu(KH_MEMREF1(const float, x), KH_MEMREF1(float, tmp), KH_MEMREF1(float, out)) {
+  (void)tmp_alloc;
+  (void)tmp_base;
+  const float *__restrict__ X = KH_PTR(x);
+  float *__restrict__ O = KH_PTR(out);
+  const int64_t n = out_n0;
+  const int64_t tid = threadIdx.x;
+  const int64_t nthreads = (int64_t)blockDim.x * gridDim.x;
+
+  if (kh::aligned16(X) && kh::aligned16(O)) {
+    const int64_t n4 = n >> 2;
+    const float4 *__restrict__ X4 = reinterpret_cast<const float4 *>(X);
+    float4 *__restrict__ O4 = reinterpret_cast<float4 *>(O);
+    const int64_t step = nthreads * KH_UNROLL;
+    int64_t i = (int64_t)blockIdx.x * blockDim.x * KH_UNROLL + tid;
+    for (; i + (KH_UNROLL - 1) * (int64_t)blockDim.x < n4; i += step) {
+      float4 v[KH_UNROLL];
+#pragma unroll
+      for (int u = 0; u < KH_UNROLL; ++u) v[u] = X4[i + u * (int64_t)blockDim.x];
+#pragma unroll
+      for (int u = 0; u < KH_UNROLL; ++u) O4[i + u * (int64_t)blockDim.x] = gelu4(v[u]);
+    }
+    for (int u = 0; u < KH_UNROLL; ++u) {
+      const int64_t j = i + u * (int64_t)blockDim.x;
+      if (j < n4) O4[j] = gelu4(X4[j]);
+    }
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + tid;
+    const int64_t t = (n4 << 2) + gid;
+    if (t < n) O[t] = gelu_affine(X[t]);
+  } else {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + tid; i < n; i += nthreads) O[i] = gelu_affine(X[i]);
+  }
+}

@@ -1,0 +1,77 @@
+// Shared device-side helpers for the gfx950 (CDNA4, wave64) kernel.h
+// templates: memref-descriptor parameter lists and wavefront reductions.
+//
+// Kernel ABI. Every buffer argument arrives as the expanded MLIR memref
+// descriptor the reference emitter produces (lib/compiler/emitter.cpp:
+// 713-727; lib/runtime/descriptor_packing.cpp:3-39): 2N+3 eight-byte kernel
+// parameters {allocated ptr, aligned ptr, offset, sizes[N], strides[N]}.
+// Element (i0..iN-1) lives at aligned + offset + sum(ik * stride_k). The
+// launcher always packs contiguous row-major descriptors with offset 0, and
+// the kernels honour the offset and the outer strides.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define KH_MEMREF1(T, name) \
+  T *__restrict__ name##_alloc, T *__restrict__ name##_base, int64_t name##_off, int64_t name##_n0, int64_t name##_s0
+
+#define KH_MEMREF2(T, name)                                                                 \
+  T *__restrict__ name##_alloc, T *__restrict__ name##_base, int64_t name##_off, int64_t name##_n0, \
+      int64_t name##_n1, int64_t name##_s0, int64_t name##_s1
+
+#define KH_MEMREF4(T, name)                                                                 \
+  T *__restrict__ name##_alloc, T *__restrict__ name##_base, int64_t name##_off, int64_t name##_n0, \
+      int64_t name##_n1, int64_t name##_n2, int64_t name##_n3, int64_t name##_s0, int64_t name##_s1, \
+      int64_t name##_s2, int64_t name##_s3
+
+// Element pointer of a descriptor (aligned pointer + offset).
+#define KH_PTR(name) (name##_base + name##_off)
+
+namespace kh {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ bool aligned16(const void *p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// DPP row_ror:n (rotate right by n within each 16-lane row), gfx9 encoding
+// 0x120 + n. All rows and banks enabled; rotation never leaves the row.
+template <int N>
+__device__ __forceinline__ float ror(float v) {
+  static_assert(N >= 1 && N <= 15, "row_ror range");
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x120 + N, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float readlane(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Wavefront all-reduce: a rotate-and-combine butterfly inside each 16-lane
+// row (every lane ends with its row's total), then the four row totals are
+// read into scalar registers and combined. The result is wave-uniform.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += ror<8>(v);
+  v += ror<4>(v);
+  v += ror<2>(v);
+  v += ror<1>(v);
+  return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, ror<8>(v));
+  v = fmaxf(v, ror<4>(v));
+  v = fmaxf(v, ror<2>(v));
+  v = fmaxf(v, ror<1>(v));
+  return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)), fmaxf(readlane(v, 32), readlane(v, 48)));
+}
+
+// 2^x on the hardware transcendental unit (v_exp_f32).
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+}  // namespace kh

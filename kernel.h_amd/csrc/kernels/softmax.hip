@@ -1,0 +1,123 @@
+// Row-wise safe softmax for gfx950: y[r,:] = exp(x[r,:] - max) / sum.
+//
+// Symbol and memref arguments follow the reference template
+// (lib/dsl/kernels/softmax.cpp:68-165): x, y rank-2 [rows, cols], 14
+// parameters. The reference runs an online max/sum recurrence serially in
+// every thread of a row's block (softmax.cpp:121-145), reading the row 256
+// times. Here ONE wavefront owns a row: the row is read once with dwordx4
+// loads into registers (cols <= 64 lanes x 4 x KH_SM_MAXV floats), reduced
+// with DPP row rotations + readlane (max, then the sum of exponentials),
+// and written once: 8 B of HBM traffic per element.
+//
+// Rows wider than the register path fall back to a two-sweep form (an online
+// per-lane (max, sum) pass, then a write pass that re-reads the row). Rows
+// are grid-strided over wavefronts, so any launch with a multiple of 64
+// threads per block is correct, including the reference's
+// rows x min(cols, 256) geometry (kernelh_backend.cpp:256-257).
+//
+// exp(x - m) is evaluated as 2^(x*log2e - m*log2e) with one fma on
+// v_exp_f32; y = e * (1/s) with an IEEE reciprocal of s.
+#include "kh_device.h"
+
+#ifndef KH_SM_MAXV
+#define KH_SM_MAXV 8  // float4 per lane on the register path: cols <= 2048
+#endif
+
+namespace {
+
+template <int V>
+__device__ __forceinline__ void softmax_row_regs(const float *__restrict__ xr, float *__restrict__ yr,
+                                                 int64_t cols, int lane) {
+  float4 v[V];
+  const float ninf = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int64_t c = (int64_t)(lane + j * kh::kWave) * 4;
+    if (c < cols) {
+      v[j] = *reinterpret_cast<const float4 *>(xr + c);
+    } else {
+      v[j] = make_float4(ninf, ninf, ninf, ninf);
+    }
+  }
+  float m = ninf;
+#pragma unroll
+  for (int j = 0; j < V; ++j) m = fmaxf(m, fmaxf(fmaxf(v[j].x, v[j].y), fmaxf(v[j].z, v[j].w)));
+  m = kh::wave_max(m);
+  const float mb = -m * kh::kLog2e;
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    v[j].x = kh::exp2_hw(fmaf(v[j].x, kh::kLog2e, mb));
+    v[j].y = kh::exp2_hw(fmaf(v[j].y, kh::kLog2e, mb));
+    v[j].z = kh::exp2_hw(fmaf(v[j].z, kh::kLog2e, mb));
+    v[j].w = kh::exp2_hw(fmaf(v[j].w, kh::kLog2e, mb));
+    s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  }
+  s = kh::wave_sum(s);
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int64_t c = (int64_t)(lane + j * kh::kWave) * 4;
+    if (c < cols) {
+      float4 o;
+      o.x = v[j].x * inv;
+      o.y = v[j].y * inv;
+      o.z = v[j].z * inv;
+      o.w = v[j].w * inv;
+      *reinterpret_cast<float4 *>(yr + c) = o;
+    }
+  }
+}
+
+// Any cols, any alignment: per-lane online (max, sum) over a strided sweep,
+// merged across the wave, then a second sweep writes the outputs.
+__device__ __forceinline__ void softmax_row_stream(const float *__restrict__ xr, float *__restrict__ yr,
+                                                   int64_t cols, int lane) {
+  float m = -__builtin_inff(), s = 0.0f;
+  for (int64_t c = lane; c < cols; c += kh::kWave) {
+    const float x = xr[c];
+    const float mn = fmaxf(m, x);
+    s = s * kh::exp2_hw((m - mn) * kh::kLog2e) + kh::exp2_hw((x - mn) * kh::kLog2e);
+    m = mn;
+  }
+  const float gm = kh::wave_max(m);
+  // Lanes that saw no element carry m = -inf, s = 0: contribute 0.
+  s = (s == 0.0f) ? 0.0f : s * kh::exp2_hw((m - gm) * kh::kLog2e);
+  const float gs = kh::wave_sum(s);
+  const float inv = 1.0f / gs;
+  const float mb = -gm * kh::kLog2e;
+  for (int64_t c = lane; c < cols; c += kh::kWave) yr[c] = kh::exp2_hw(fmaf(xr[c], kh::kLog2e, mb)) * inv;
+}
+
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(256)
+softmax(KH_MEMREF2(const float, x), KH_MEMREF2(float, y)) {
+  const float *__restrict__ X = KH_PTR(x);
+  float *__restrict__ Y = KH_PTR(y);
+  const int64_t rows = x_n0, cols = x_n1;
+  const int64_t xs = x_s0, ys = y_s0;
+  const int lane = kh::lane_id();
+  const int64_t waves_per_block = blockDim.x / kh::kWave;
+  const int64_t wave = threadIdx.x / kh::kWave;
+  const int64_t nwaves = waves_per_block * gridDim.x;
+
+  const bool vec = ((cols & 3) == 0) && ((xs & 3) == 0) && ((ys & 3) == 0) && kh::aligned16(X) &&
+                   kh::aligned16(Y);
+  const int64_t v4 = (cols + 255) / 256;  // float4 per lane needed
+  for (int64_t r = blockIdx.x * waves_per_block + wave; r < rows; r += nwaves) {
+    const float *xr = X + r * xs;
+    float *yr = Y + r * ys;
+    if (vec && v4 <= 1) {
+      softmax_row_regs<1>(xr, yr, cols, lane);
+    } else if (vec && v4 <= 2) {
+      softmax_row_regs<2>(xr, yr, cols, lane);
+    } else if (vec && v4 <= 4) {
+      softmax_row_regs<4>(xr, yr, cols, lane);
+    } else if (vec && v4 <= KH_SM_MAXV) {
+      softmax_row_regs<KH_SM_MAXV>(xr, yr, cols, lane);
+    } else {
+      softmax_row_stream(xr, yr, cols, lane);
+    }
+  }
+}

@@ -1,0 +1,382 @@
+// The seven kernel.h templates behind the C-ABI: embedded gfx950 code
+// objects, the registry, the launcher-owned geometry and one entry point per
+// template.
+//
+// Replaces the reference's name -> template dispatch (lib/dsl/registry.cpp:
+// 23-36, lib/dsl/program.cpp:17-51) and the per-kernel launch code its
+// callers repeat (bench/harness/kernelh_backend.cpp:205-436,
+// test/unit/e2e_*_test.cpp). The reference callers own grid/block; here the
+// launcher owns geometry per kernel (the kernels stay correct under the
+// reference's geometry too), while the memref argument lists, symbol names
+// and the hipModuleLoadData / hipModuleLaunchKernel path are unchanged.
+#include "kernelh/khrt_internal.hpp"
+#include "kh_tiles.h"
+
+#include <algorithm>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+// Code objects linked into the library by kh_embed.S (generated at build).
+#define KH_DECLARE_CO(name)              \
+  extern "C" const unsigned char kh_co_##name[]; \
+  extern "C" const unsigned char kh_co_##name##_end[];
+KH_DECLARE_CO(vecadd)
+KH_DECLARE_CO(fused_gelu)
+KH_DECLARE_CO(softmax)
+KH_DECLARE_CO(layernorm)
+KH_DECLARE_CO(scan)
+KH_DECLARE_CO(gemm)
+KH_DECLARE_CO(attention)
+KH_DECLARE_CO(util)
+
+namespace {
+
+struct CodeObject {
+  const char *name;
+  const unsigned char *begin;
+  const unsigned char *end;
+};
+
+const CodeObject kCodeObjects[] = {
+    {"vecadd", kh_co_vecadd, kh_co_vecadd_end},       {"fused_gelu", kh_co_fused_gelu, kh_co_fused_gelu_end},
+    {"softmax", kh_co_softmax, kh_co_softmax_end},    {"layernorm", kh_co_layernorm, kh_co_layernorm_end},
+    {"scan", kh_co_scan, kh_co_scan_end},             {"gemm", kh_co_gemm, kh_co_gemm_end},
+    {"attention", kh_co_attention, kh_co_attention_end}, {"util", kh_co_util, kh_co_util_end},
+};
+
+struct KernelResources {
+  const char *symbol;
+  khrt_kernel_resources r;
+};
+
+// Resource notes of every kernel symbol, generated from the code objects.
+const KernelResources kResources[] = {
+#include "kh_resources.inc"
+};
+
+struct Template {
+  const char *name;  // template name == kernel symbol
+  const char *co;    // code object holding the symbol
+};
+
+// Registry order follows the reference's registration (registry.cpp:23-36).
+const Template kTemplates[] = {
+    {"vecadd", "vecadd"}, {"gemm", "gemm"},         {"softmax", "softmax"},       {"layernorm", "layernorm"},
+    {"scan", "scan"},     {"scan_totals", "scan"}, {"fused_gelu", "fused_gelu"}, {"attention", "attention"},
+};
+
+const CodeObject *find_co(const char *name) {
+  for (const auto &c : kCodeObjects) {
+    if (std::strcmp(c.name, name) == 0) return &c;
+  }
+  return nullptr;
+}
+
+const Template *find_template(const char *name) {
+  if (name == nullptr) return nullptr;
+  for (const auto &t : kTemplates) {
+    if (std::strcmp(t.name, name) == 0) return &t;
+  }
+  return nullptr;
+}
+
+std::string registered_list() {
+  std::string s;
+  for (const auto &t : kTemplates) {
+    if (!s.empty()) s += ", ";
+    s += t.name;
+  }
+  return s;
+}
+
+int unknown_template(const char *name) {
+  return khrt::fail(KHRT_E_INVALID, "unknown kernel '" + std::string(name ? name : "(null)") +
+                                        "'; registered kernels: " + registered_list());
+}
+
+// Per-device module cache: code object name -> loaded module; symbol ->
+// function. Loaded once, kept for the process lifetime.
+struct LoadedModule {
+  int device;
+  std::string co;
+  void *module;
+};
+struct LoadedFunction {
+  int device;
+  std::string symbol;
+  void *function;
+};
+std::mutex g_mu;
+std::vector<LoadedModule> g_modules;
+std::vector<LoadedFunction> g_functions;
+
+int get_function(const char *co_name, const char *symbol, void **out) {
+  if (int rc = khrt::ensure_device()) return rc;
+  const int dev = khrt::current_device();
+  std::lock_guard<std::mutex> lock(g_mu);
+  for (const auto &f : g_functions) {
+    if (f.device == dev && f.symbol == symbol) {
+      *out = f.function;
+      return 0;
+    }
+  }
+  void *module = nullptr;
+  for (const auto &m : g_modules) {
+    if (m.device == dev && m.co == co_name) module = m.module;
+  }
+  if (module == nullptr) {
+    const CodeObject *co = find_co(co_name);
+    if (co == nullptr) return khrt::fail(KHRT_E_INVALID, std::string("no code object '") + co_name + "'");
+    const size_t size = static_cast<size_t>(co->end - co->begin);
+    if (size < 64) {
+      return khrt::fail(KHRT_E_INVALID, std::string("code object '") + co_name + "' is not part of this build");
+    }
+    if (int rc = khrt_module_load_data(&module, co->begin, size)) return rc;
+    g_modules.push_back({dev, co_name, module});
+  }
+  void *fn = nullptr;
+  if (int rc = khrt_module_get_function(&fn, module, symbol)) return rc;
+  g_functions.push_back({dev, symbol, fn});
+  *out = fn;
+  return 0;
+}
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+unsigned clamp_grid(int64_t g) { return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(g, 1 << 20))); }
+
+using Shape = std::map<std::string, int64_t>;
+
+bool need(const Shape &s, const char *key, int64_t &v) {
+  auto it = s.find(key);
+  if (it == s.end() || it->second <= 0) return false;
+  v = it->second;
+  return true;
+}
+
+// Launcher-owned geometry per template (see each kernel's header comment).
+int geometry(const char *name, const Shape &s, khrt_dim3 &grid, khrt_dim3 &block) {
+  block = {256, 1, 1};
+  grid = {1, 1, 1};
+  int64_t n = 0, rows = 0, cols = 0, m = 0, k = 0, b = 0, h = 0, seq = 0, d = 0;
+  const std::string t = name;
+  if (t == "vecadd" || t == "fused_gelu") {
+    if (!need(s, "n", n)) {
+      if (t == "fused_gelu" && need(s, "rows", rows) && need(s, "cols", cols)) {
+        n = rows * cols;
+      } else {
+        return khrt::fail(KHRT_E_INVALID, t + ": shape attribute 'n' is required and must be positive");
+      }
+    }
+    grid.x = clamp_grid(ceil_div(ceil_div(n, 4), 256LL * KH_EW_UNROLL));
+  } else if (t == "softmax" || t == "layernorm") {
+    if (!need(s, "rows", rows) || !need(s, "cols", cols)) {
+      return khrt::fail(KHRT_E_INVALID, t + ": shape attributes 'rows' and 'cols' are required and must be positive");
+    }
+    grid.x = clamp_grid(ceil_div(rows, 4));
+  } else if (t == "scan" || t == "scan_totals") {
+    if (!need(s, "n", n)) return khrt::fail(KHRT_E_INVALID, t + ": shape attribute 'n' is required and must be positive");
+    if (t == "scan") {
+      grid.x = clamp_grid(ceil_div(n, KH_SCAN_TILE));
+    } else {
+      grid.x = clamp_grid(std::min<int64_t>(ceil_div(ceil_div(n, 256) + 1, 256), 1024));
+    }
+  } else if (t == "gemm") {
+    if (!need(s, "m", m) || !need(s, "n", n) || !need(s, "k", k)) {
+      return khrt::fail(KHRT_E_INVALID, "gemm: shape attributes 'm', 'n' and 'k' are required and must be positive");
+    }
+    grid.x = clamp_grid(ceil_div(m, KH_GEMM_BM) * ceil_div(n, KH_GEMM_BN));
+  } else if (t == "attention") {
+    if (!need(s, "batch", b) || !need(s, "heads", h) || !need(s, "seq", seq) || !need(s, "head_dim", d)) {
+      return khrt::fail(KHRT_E_INVALID,
+                        "attention: shape attributes 'batch', 'heads', 'seq' and 'head_dim' are required and "
+                        "must be positive");
+    }
+    if (d != 64) {
+      return khrt::fail(KHRT_E_INVALID, "attention: the kernel is pinned to head_dim = 64 (got head_dim = " +
+                                            std::to_string(d) + ")");
+    }
+    grid = {static_cast<unsigned>(ceil_div(seq, KH_ATTN_BLOCK_Q)), static_cast<unsigned>(h),
+            static_cast<unsigned>(b)};
+  } else {
+    return unknown_template(name);
+  }
+  return 0;
+}
+
+// Packs, verifies and launches template `name`.
+int launch_template(const char *name, khrt::LaunchArgs &args, const Shape &shape, void *stream) {
+  const Template *t = find_template(name);
+  if (t == nullptr) return unknown_template(name);
+  khrt_dim3 grid, block;
+  if (int rc = geometry(name, shape, grid, block)) return rc;
+  void *fn = nullptr;
+  if (int rc = get_function(t->co, t->name, &fn)) return rc;
+  return khrt::verified_launch(fn, grid, block, 0, stream, args.params(), args.count());
+}
+
+int bad(const char *what) { return khrt::fail(KHRT_E_INVALID, what); }
+
+}  // namespace
+
+extern "C" {
+
+int khrt_template_count(void) { return static_cast<int>(sizeof(kTemplates) / sizeof(kTemplates[0])); }
+
+const char *khrt_template_name(int i) {
+  if (i < 0 || i >= khrt_template_count()) return nullptr;
+  return kTemplates[i].name;
+}
+
+int khrt_template_code_object(const char *name, const void **image, size_t *size) {
+  if (image == nullptr || size == nullptr) return bad("khrt_template_code_object: null output");
+  const Template *t = find_template(name);
+  if (t == nullptr) return unknown_template(name);
+  const CodeObject *co = find_co(t->co);
+  *image = co->begin;
+  *size = static_cast<size_t>(co->end - co->begin);
+  if (*size < 64) return khrt::fail(KHRT_E_INVALID, std::string("code object for '") + name + "' is not part of this build");
+  return 0;
+}
+
+int khrt_template_resources(const char *name, khrt_kernel_resources *out) {
+  if (out == nullptr) return bad("khrt_template_resources: null output");
+  if (name == nullptr) return unknown_template(name);
+  for (const auto &r : kResources) {
+    if (std::strcmp(r.symbol, name) == 0) {
+      *out = r.r;
+      return 0;
+    }
+  }
+  return unknown_template(name);
+}
+
+int khrt_template_geometry(const char *name, const char *shape, khrt_dim3 *grid, khrt_dim3 *block) {
+  if (grid == nullptr || block == nullptr || shape == nullptr) return bad("khrt_template_geometry: null argument");
+  if (find_template(name) == nullptr) return unknown_template(name);
+  Shape s;
+  if (!khrt::parse_shape(shape, s)) return khrt::fail(KHRT_E_INVALID, std::string("malformed shape '") + shape + "'");
+  return geometry(name, s, *grid, *block);
+}
+
+int khrt_template_function(const char *name, void **function) {
+  if (function == nullptr) return bad("khrt_template_function: null output");
+  const Template *t = find_template(name);
+  if (t == nullptr) return unknown_template(name);
+  return get_function(t->co, t->name, function);
+}
+
+int khrt_fill_f32(void *dst, float value, size_t count, void *stream) {
+  if (count == 0) return 0;
+  if (dst == nullptr) return bad("khrt_fill_f32: null destination");
+  void *fn = nullptr;
+  if (int rc = get_function("util", "kh_fill_f32", &fn)) return rc;
+  khrt::LaunchArgs a;
+  a.add_memref(dst, {static_cast<int64_t>(count)});
+  a.add_scalar_bytes(&value, sizeof(value));
+  const unsigned grid = clamp_grid(ceil_div(static_cast<int64_t>(count), 256 * 4));
+  return khrt_launch_raw(fn, khrt_dim3{grid, 1, 1}, khrt_dim3{256, 1, 1}, 0, stream, a.params());
+}
+
+int kh_vecadd(const float *a, const float *b, float *c, int64_t n, void *stream) {
+  if (n <= 0) return bad("vecadd: n must be positive");
+  if (!a || !b || !c) return bad("vecadd: null buffer");
+  khrt::LaunchArgs args;
+  args.add_memref(a, {n});
+  args.add_memref(b, {n});
+  args.add_memref(c, {n});
+  return launch_template("vecadd", args, {{"n", n}}, stream);
+}
+
+int kh_fused_gelu(const float *x, float *tmp, float *out, int64_t n, void *stream) {
+  if (n <= 0) return bad("fused_gelu: n must be positive");
+  if (!x || !out) return bad("fused_gelu: null buffer");
+  khrt::LaunchArgs args;
+  args.add_memref(x, {n});
+  args.add_memref(tmp, {n});
+  args.add_memref(out, {n});
+  return launch_template("fused_gelu", args, {{"n", n}}, stream);
+}
+
+int kh_softmax(const float *x, float *y, int64_t rows, int64_t cols, void *stream) {
+  if (rows <= 0 || cols <= 0) return bad("softmax: rows and cols must be positive");
+  if (!x || !y) return bad("softmax: null buffer");
+  khrt::LaunchArgs args;
+  args.add_memref(x, {rows, cols});
+  args.add_memref(y, {rows, cols});
+  return launch_template("softmax", args, {{"rows", rows}, {"cols", cols}}, stream);
+}
+
+int kh_layernorm(const float *x, const float *gamma, const float *beta, float *y, int64_t rows, int64_t cols,
+                 void *stream) {
+  if (rows <= 0 || cols <= 0) return bad("layernorm: rows and cols must be positive");
+  if (!x || !gamma || !beta || !y) return bad("layernorm: null buffer");
+  khrt::LaunchArgs args;
+  args.add_memref(x, {rows, cols});
+  args.add_memref(gamma, {cols});
+  args.add_memref(beta, {cols});
+  args.add_memref(y, {rows, cols});
+  return launch_template("layernorm", args, {{"rows", rows}, {"cols", cols}}, stream);
+}
+
+int kh_scan(const float *x, float *y, float *y_lo, float *totals_hi, float *totals_lo, int64_t n, void *stream) {
+  if (n <= 0) return bad("scan: n must be positive");
+  if (!x || !y || !totals_hi || !totals_lo) return bad("scan: null buffer");
+  const int64_t T = ceil_div(n, 256);
+  const int64_t tiles = ceil_div(n, KH_SCAN_TILE);
+  if (tiles > 1 && (reinterpret_cast<uintptr_t>(totals_hi) & 7u) != 0) {
+    return bad("scan: totals_hi must be 8-byte aligned (it holds the fp64 look-back values)");
+  }
+  if (tiles > 1 && (T < tiles + 1 || T < 4 * tiles)) return bad("scan: totals buffers too small for the look-back state");
+  khrt::LaunchArgs args;
+  args.add_memref(x, {n});
+  args.add_memref(y, {n});
+  args.add_memref(y_lo, {n});
+  args.add_memref(totals_hi, {T});
+  args.add_memref(totals_lo, {T});
+  return launch_template("scan", args, {{"n", n}}, stream);
+}
+
+int kh_scan_totals(const float *totals_hi, const float *totals_lo, float *off_hi, float *off_lo, float *off_lo2,
+                   float *y, float *y_lo, int64_t n, void *stream) {
+  if (n <= 0) return bad("scan_totals: n must be positive");
+  if (!totals_hi || !totals_lo || !off_hi || !off_lo || !off_lo2 || !y) return bad("scan_totals: null buffer");
+  const int64_t T = ceil_div(n, 256);
+  khrt::LaunchArgs args;
+  args.add_memref(totals_hi, {T});
+  args.add_memref(totals_lo, {T});
+  args.add_memref(off_hi, {T});
+  args.add_memref(off_lo, {T});
+  args.add_memref(off_lo2, {T});
+  args.add_memref(y, {n});
+  args.add_memref(y_lo, {n});
+  return launch_template("scan_totals", args, {{"n", n}}, stream);
+}
+
+int kh_gemm(const float *A, const float *B, float *C, int64_t m, int64_t n, int64_t k, void *stream) {
+  if (m <= 0 || n <= 0 || k <= 0) return bad("gemm: m, n and k must be positive");
+  if (!A || !B || !C) return bad("gemm: null buffer");
+  khrt::LaunchArgs args;
+  args.add_memref(A, {m, k});
+  args.add_memref(B, {k, n});
+  args.add_memref(C, {m, n});
+  return launch_template("gemm", args, {{"m", m}, {"n", n}, {"k", k}}, stream);
+}
+
+int kh_attention(const float *Q, const float *K, const float *V, float *O, int64_t batch, int64_t heads, int64_t seq,
+                 int64_t head_dim, void *stream) {
+  if (batch <= 0 || heads <= 0 || seq <= 0 || head_dim <= 0) return bad("attention: all extents must be positive");
+  if (!Q || !K || !V || !O) return bad("attention: null buffer");
+  if (heads > 65535 || batch > 65535) return bad("attention: heads and batch must be <= 65535 (grid y/z)");
+  khrt::LaunchArgs args;
+  args.add_memref(Q, {batch, heads, seq, head_dim});
+  args.add_memref(K, {batch, heads, seq, head_dim});
+  args.add_memref(V, {batch, heads, seq, head_dim});
+  args.add_memref(O, {batch, heads, seq, head_dim});
+  return launch_template("attention", args,
+                         {{"batch", batch}, {"heads", heads}, {"seq", seq}, {"head_dim", head_dim}}, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,298 @@
+"""Host-side boundary of the khrt C-ABI, no GPU needed.
+
+Mirrors the reference's CPU unit tests for the same pieces:
+  descriptor packing   test/unit/runtime_descriptor_test.cpp:22-117
+  device limits        test/unit/device_limits_test.cpp:157-216
+  launch verifier      test/unit/launch_verifier_test.cpp:165-259
+  occupancy            test/unit/occupancy_test.cpp:160-300
+plus the C-ABI itself: libkhrt.so loads and exports every symbol that
+include/khrt.h declares, and the embedded code objects are gfx950 wave64
+ELF objects carrying each template's kernel symbol with the reference's
+kernel-parameter count (2N+3 slots per memref).
+"""
+import ctypes
+import os
+import re
+import struct
+import subprocess
+
+import numpy as np
+import pytest
+
+import kernelh as kh
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+# ------------------------------------------------------------------ C-ABI exports
+
+def _declared_functions():
+    text = open(os.path.join(REPO, "include", "khrt.h")).read()
+    return re.findall(r"KHRT_API\s+[\w\s\*]+?\b(\w+)\s*\(", text)
+
+
+def test_library_exports_every_declared_symbol():
+    names = _declared_functions()
+    assert len(names) >= 45
+    L = ctypes.CDLL(kh.LIB_PATH)
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, f"declared in include/khrt.h but not exported: {missing}"
+    # And the Python binding covers each of them.
+    assert set(names) <= set(kh.SIGNATURES), set(names) - set(kh.SIGNATURES)
+
+
+def test_error_strings_and_version():
+    assert kh.lib.khrt_error_string(kh.KHRT_E_REFUSED).decode().startswith("launch refused")
+    assert kh.lib.khrt_error_string(kh.KHRT_E_SKIP).decode() == "skipped"
+    assert b"gfx950" in kh.lib.khrt_version()
+
+
+# ------------------------------------------------------------------ descriptors
+
+def test_descriptor_1d_byte_layout():
+    a = kh.LaunchArgs().add_memref(0x12340000, [1024])
+    assert a.slots == [0x12340000, 0x12340000, 0, 1024, 1]
+
+
+def test_descriptor_2d_byte_layout():
+    a = kh.LaunchArgs().add_memref(0x00AABBCC, [16, 8])
+    assert a.slots == [0x00AABBCC, 0x00AABBCC, 0, 16, 8, 8, 1]
+
+
+def test_descriptor_4d_layout_attention():
+    a = kh.LaunchArgs().add_memref(0x1000, [4, 16, 1024, 64])
+    assert a.slots == [0x1000, 0x1000, 0, 4, 16, 1024, 64, 16 * 1024 * 64, 1024 * 64, 64, 1]
+
+
+def test_descriptor_scalars_after_descriptors():
+    a = kh.LaunchArgs().add_memref(0x1000, [256])
+    a.add_scalar_bytes(struct.pack("<i", 42)).add_scalar_bytes(struct.pack("<d", 3.5))
+    assert a.param_count() == 7
+    assert a.slots[5] == 42
+    assert a.slots[6] == 0x400C000000000000
+
+
+def test_descriptor_pair_10_params_and_param_pointers():
+    a = kh.LaunchArgs().add_memref(0x1000, [4096]).add_memref(0x2000, [4096])
+    assert a.slots == [0x1000, 0x1000, 0, 4096, 1, 0x2000, 0x2000, 0, 4096, 1]
+    arr, store = a.params()
+    base = ctypes.addressof(store)
+    assert [arr[i] for i in range(10)] == [base + 8 * i for i in range(10)]
+
+
+@pytest.mark.parametrize("name,ranks,count", [
+    ("vecadd", [1, 1, 1], 15), ("fused_gelu", [1, 1, 1], 15), ("softmax", [2, 2], 14),
+    ("layernorm", [2, 1, 1, 2], 24), ("scan", [1] * 5, 25), ("scan_totals", [1] * 7, 35),
+    ("gemm", [2, 2, 2], 21), ("attention", [4, 4, 4, 4], 44)])
+def test_reference_parameter_counts(name, ranks, count):
+    # The 2N+3 slot counts the reference's e2e tests assert
+    # (e.g. e2e_scan_test.cpp:145, 158; e2e_softmax_test.cpp:153).
+    assert sum(kh.lib.khrt_memref_slot_count(r) for r in ranks) == count
+
+
+def test_pack_memref_capacity_error():
+    buf = (ctypes.c_uint64 * 4)()
+    shp = (ctypes.c_int64 * 1)(8)
+    rc = kh.lib.khrt_pack_memref(buf, 4, 0x10, 1, shp)
+    assert rc == kh.KHRT_E_INVALID and "capacity" in kh.last_error()
+
+
+# ------------------------------------------------------------------ device limits
+
+def test_gfx950_limits_exact_values():
+    l = kh.device_limits_for("gfx950")
+    assert l.lds_bytes_per_workgroup == 163840
+    assert l.wavefront_size == 64
+    assert l.max_threads_per_workgroup == 1024
+    assert list(l.max_grid_dim) == [2147483647, 65535, 65535]
+    assert l.waves_per_cu == 32
+    assert l.reg_file_per_cu == 131072
+    assert l.cu_count == 0
+    assert l.name == b"AMD Instinct MI355X (gfx950)"
+
+
+def test_reference_entries_kept():
+    g = kh.device_limits_for("gfx1101")
+    assert (g.lds_bytes_per_workgroup, g.wavefront_size, g.waves_per_cu, g.reg_file_per_cu) == (65536, 32, 32, 6144)
+    s = kh.device_limits_for("sm_80")
+    assert (s.lds_bytes_per_workgroup, s.waves_per_cu, s.reg_file_per_cu) == (49152, 64, 65536)
+
+
+@pytest.mark.parametrize("bad", ["gfx90a", "", "GFX950", None])
+def test_unknown_target_lists_known_tokens(bad):
+    with pytest.raises(kh.KhrtError) as e:
+        kh.device_limits_for(bad)
+    assert e.value.code == kh.KHRT_E_UNKNOWN_TARGET
+    assert "known targets: gfx950, gfx1101, sm_80" in e.value.message
+    assert (f'"{bad}"' if bad is not None else '"(null)"') in e.value.message
+
+
+def test_query_cu_count_falls_back_to_table_without_device():
+    if kh.device_count() > 0:
+        pytest.skip("a device is visible; the fallback path is for device-less hosts")
+    l = kh.device_limits_for("gfx950")
+    assert kh.lib.khrt_query_cu_count(ctypes.byref(l)) == 0
+
+
+# ------------------------------------------------------------------ launch verifier
+
+def test_verifier_shared_over_lds():
+    d = kh.verify_launch(256, (1, 1, 1), 170000)
+    assert "shared memory 170000 bytes exceeds the 163840-byte LDS limit" in d
+    assert "AMD Instinct MI355X (gfx950)" in d
+
+
+def test_verifier_threads_over_max():
+    assert "threads per workgroup 2048 exceeds the max 1024" in kh.verify_launch(2048)
+
+
+def test_verifier_wave64_multiple():
+    # wave32-sized workgroups that the reference accepted on gfx1101 are
+    # refused on gfx950 (launch_verifier.cpp:135-143 with wavefront 64).
+    assert "threads per workgroup 96 is not a multiple of the wavefront size 64" in kh.verify_launch(96)
+    assert kh.verify_launch(96, limits=kh.device_limits_for("gfx1101")) == ""
+
+
+def test_verifier_grid_over_limit():
+    assert "grid dim (1,1,70000) exceeds the target grid limits" in kh.verify_launch(256, (1, 1, 70000))
+
+
+def test_verifier_occupancy_zero_analytic():
+    low = kh.device_limits_for("gfx950")
+    low.waves_per_cu = 2
+    d = kh.verify_launch(256, limits=low)
+    assert "occupancy would be 0 on target 'AMD Instinct MI355X (gfx950)'" in d
+    assert "needs 4 wavefronts" in d
+    assert kh.verify_launch(128, limits=low) == ""
+
+
+def test_verifier_all_rules_reported_one_per_line():
+    d = kh.verify_launch(4100, (1, 1, 70000), 170000)
+    lines = d.split("\n")
+    assert len(lines) == 5
+    assert "shared memory" in lines[0] and "exceeds the max 1024" in lines[1]
+    assert "not a multiple of the wavefront size 64" in lines[2]
+    assert "grid dim" in lines[3] and "occupancy would be 0" in lines[4]
+
+
+def test_verifier_accepts_template_launches():
+    for name, shape in [("vecadd", "n=16777216"), ("softmax", "rows=4096,cols=1024"),
+                        ("layernorm", "rows=4096,cols=1024"), ("scan", "n=67108864"),
+                        ("fused_gelu", "n=67108864"), ("gemm", "m=8192,n=8192,k=8192"),
+                        ("attention", "batch=4,heads=16,seq=4096,head_dim=64")]:
+        grid, block = kh.geometry(name, shape)
+        res = kh.resources(name) if name not in ("gemm", "attention") else {"lds_bytes": 0}
+        assert kh.verify_launch(block[0] * block[1] * block[2], grid, res["lds_bytes"]) == "", name
+
+
+# ------------------------------------------------------------------ occupancy
+
+@pytest.mark.parametrize("vgpr,lds,threads,exp", [
+    # (vgpr_waves, lds_blocks, thread_blocks, achieved, limiter, pct) on gfx1101,
+    # the reference's hand computations (occupancy_test.cpp:160-235).
+    (32, 16384, 256, (6, 4, 4, 4, 2, 12.5)),
+    (64, 32768, 128, (3, 2, 8, 2, 2, 6.25)),
+    (48, 8192, 512, (4, 8, 2, 2, 3, 6.25)),
+    (128, 8192, 128, (1, 8, 8, 1, 1, 3.125)),
+    (64, 65536, 256, (3, 1, 4, 1, 2, 3.125)),
+    (0, 16384, 256, (0, 4, 4, 4, 2, 12.5)),
+])
+def test_occupancy_reference_hand_computations(vgpr, lds, threads, exp):
+    r = kh.occupancy(vgpr, lds, threads, limits=kh.device_limits_for("gfx1101"))
+    assert (r.vgpr_limited_waves, r.lds_limited_blocks, r.thread_limited_blocks, r.achieved_waves,
+            r.limiter) == exp[:5]
+    assert r.theoretical_pct == pytest.approx(exp[5])
+
+
+@pytest.mark.parametrize("vgpr,lds,threads,exp", [
+    # gfx950: R = 131072, wave 64, waves_per_cu 32, LDS 163840, 1024 threads.
+    (128, 32768, 256, (16, 5, 4, 4, 3, 12.5)),    # 131072/(128*64)=16; 163840/32768=5; 1024/256=4
+    (256, 65536, 256, (8, 2, 4, 2, 2, 6.25)),     # LDS-limited
+    (512, 0, 64, (4, 0, 16, 4, 1, 12.5)),         # VGPR-limited, no LDS
+    (8, 0, 64, (32, 0, 16, 16, 3, 50.0)),         # 256 waves capped at 32; thread bound 16
+])
+def test_occupancy_gfx950_hand_computations(vgpr, lds, threads, exp):
+    r = kh.occupancy(vgpr, lds, threads)
+    assert (r.vgpr_limited_waves, r.lds_limited_blocks, r.thread_limited_blocks, r.achieved_waves,
+            r.limiter) == exp[:5]
+    assert r.theoretical_pct == pytest.approx(exp[5])
+    assert r.measured_blocks == -1 and b"analytic only" in r.measured_note
+
+
+# ------------------------------------------------------------------ templates & code objects
+
+def test_registry_names_and_unknown_kernel():
+    assert kh.template_names() == list(kh.TEMPLATES)
+    with pytest.raises(kh.KhrtError) as e:
+        kh.code_object("matmul")
+    assert "registered kernels: vecadd, gemm, softmax, layernorm, scan, scan_totals, fused_gelu, attention" \
+        in e.value.message
+
+
+@pytest.mark.parametrize("name", ["vecadd", "fused_gelu", "softmax", "layernorm", "scan", "scan_totals"])
+def test_code_objects_are_gfx950_wave64_elf(name):
+    blob = kh.code_object(name)
+    assert blob[:4] == b"\x7fELF"
+    assert struct.unpack_from("<H", blob, 18)[0] == 0xE0  # EM_AMDGPU
+    assert b"gfx950" in blob
+    assert name.encode() + b".kd" in blob  # the kernel descriptor symbol
+    r = kh.resources(name)
+    assert r["wavefront_size"] == 64
+    assert r["private_segment_bytes"] == 0  # no scratch spills
+    assert r["max_flat_workgroup_size"] >= 256
+
+
+@pytest.mark.parametrize("name,nslots", [("vecadd", 15), ("fused_gelu", 15), ("softmax", 14),
+                                         ("layernorm", 24), ("scan", 25), ("scan_totals", 35)])
+def test_kernarg_segment_is_2n_plus_3_slots(name, nslots):
+    import json
+    co = {"scan_totals": "scan"}.get(name, name)
+    notes = json.load(open(os.path.join(kh.CO_DIR, co + ".notes.json")))
+    k = [x for x in notes if x["name"] == name][0]
+    # Every explicit parameter is one 8-byte slot, nslots of them.
+    assert k["explicit_args"] == [8] * nslots
+
+
+@pytest.mark.parametrize("name,shape,grid,block", [
+    ("vecadd", "n=16777216", (4096, 1, 1), (256, 1, 1)),
+    ("vecadd", "n=1", (1, 1, 1), (256, 1, 1)),
+    ("fused_gelu", "rows=4096,cols=1024", (1024, 1, 1), (256, 1, 1)),
+    ("softmax", "rows=4096,cols=1024", (1024, 1, 1), (256, 1, 1)),
+    ("layernorm", "rows=4097,cols=1024", (1025, 1, 1), (256, 1, 1)),
+    ("scan", "n=1000000", (245, 1, 1), (256, 1, 1)),
+    ("scan", "n=67108864", (16384, 1, 1), (256, 1, 1)),
+    ("gemm", "m=8192,n=8192,k=8192", (4096, 1, 1), (256, 1, 1)),
+    ("attention", "batch=4,heads=16,seq=4096,head_dim=64", (32, 16, 4), (256, 1, 1)),
+])
+def test_launcher_geometry(name, shape, grid, block):
+    assert kh.geometry(name, shape) == (grid, block)
+
+
+@pytest.mark.parametrize("name,shape,msg", [
+    ("softmax", "rows=4096", "'rows' and 'cols' are required"),
+    ("attention", "batch=1,heads=1,seq=64,head_dim=32", "pinned to head_dim = 64"),
+    ("gemm", "m=1,n=1,k=0", "'m', 'n' and 'k' are required and must be positive"),
+    ("vecadd", "n=abc", "malformed shape"),
+])
+def test_geometry_errors(name, shape, msg):
+    with pytest.raises(kh.KhrtError) as e:
+        kh.geometry(name, shape)
+    assert msg in e.value.message
+
+
+def test_entry_points_validate_before_touching_a_device():
+    with pytest.raises(kh.KhrtError) as e:
+        kh.softmax(0x1000, 0x2000, 0, 16)
+    assert "rows and cols must be positive" in e.value.message
+    with pytest.raises(kh.KhrtError) as e:
+        kh.vecadd(None, 0x10, 0x20, 16)
+    assert "null buffer" in e.value.message
+    with pytest.raises(kh.KhrtError) as e:
+        kh.scan(0x1000, 0x2000, 0x3000, 0x4004, 0x5000, 1 << 20)
+    assert "8-byte aligned" in e.value.message
+
+
+def test_corrupt_image_is_a_typed_error():
+    with pytest.raises(kh.KhrtError) as e:
+        kh.GpuModule(b"\x00" * 128)
+    assert e.value.code == kh.KHRT_E_INVALID and "not an ELF" in e.value.message
