@@ -46,6 +46,10 @@ class LaunchArgs {
   std::vector<void *> params_;
 };
 
+// "" when b[0..size) is a structurally sound 64-bit AMDGPU ELF image whose
+// tables and sections all lie inside it; otherwise the reason.
+std::string check_elf_image(const unsigned char *b, size_t size);
+
 // Prelude registry: functions that need another kernel of their module
 // launched first with the same parameters (scan -> scan_reset).
 void register_prelude(void *function, void *prelude);

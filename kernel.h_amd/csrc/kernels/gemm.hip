@@ -1,0 +1,192 @@
+// fp32 GEMM for gfx950 on the matrix cores: C[m,n] = A[m,k] B[k,n],
+// row-major, v_mfma_f32_32x32x2f32.
+//
+// Symbol and memref arguments follow the reference template
+// (lib/dsl/kernels/gemm.cpp:116-296): A [m,k], B [k,n], C [m,n], rank 2,
+// 21 parameters. The reference computes one element per lane with scalar
+// FMAs out of an 8 KiB LDS tile (gemm.cpp:265-296). Here:
+//
+//   * Workgroup = 256 threads (4 wave64s) computing a 128x128 tile of C;
+//     each wave owns a 64x64 quarter as 2x2 MFMA 32x32 accumulators
+//     (64 accumulator registers per lane).
+//   * K advances in 32-wide slabs staged through LDS, double-buffered: the
+//     next slab's global loads are in flight while the current slab feeds
+//     the MFMAs, one barrier per slab.
+//   * LDS holds A as [m][k] (rows padded to 36 floats: one ds_read_b128 per
+//     lane delivers four k values, every 8-lane group on distinct banks) and
+//     B as [k][n] (rows padded to 132 floats; a half-wave reads 32
+//     consecutive n with ds_read_b32). Both slabs arrive as dwordx4 loads.
+//   * K order inside an MFMA: the instruction sums k over its two lane
+//     halves, and any permutation of k applied to both operands gives the
+//     same product. Lane half h reads k = 8c + 4h + {0..3}; MFMA step s of
+//     chunk c consumes k = 8c + s (half 0) and 8c + 4 + s (half 1).
+//   * Tiles are ordered for the 8 XCDs (each with its own L2): consecutive
+//     workgroups go round-robin to XCDs, so the launch index is remapped to
+//     give every XCD a contiguous range of tiles, grouped 8 tile-rows deep
+//     so neighbouring workgroups share A rows and B columns in L2.
+//
+// Tails in m, n and k are zero-filled on load and guarded on store, so any
+// shape is correct; tiles are grid-strided so any grid is correct, including
+// the reference's ceil(m/32) x 256 geometry (kernelh_backend.cpp:225).
+// Accumulation is fp32 throughout (the MFMA accumulates in fp32).
+#include "kh_device.h"
+#include "kh_tiles.h"
+
+namespace {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int BM = KH_GEMM_BM;  // 128
+constexpr int BN = KH_GEMM_BN;  // 128
+constexpr int BK = 32;
+constexpr int LDA = BK + 4;     // A in LDS: [m][k], rows padded to 36 floats
+constexpr int LDB = BN + 4;     // B in LDS: [k][n], rows padded to 132 floats
+constexpr int kThreads = 256;
+constexpr int kGroupM = 8;
+
+static_assert(BM == 128 && BN == 128, "wave tiling below assumes 128x128");
+
+struct Slab {
+  float4 a[4];  // A: 4 x (one row, 4 consecutive k)
+  float4 b[4];  // B: 4 x (one k row, 4 consecutive n)
+};
+
+__device__ __forceinline__ float4 load4(const float *__restrict__ P, int64_t row, int64_t col, int64_t ld,
+                                        int64_t rows, int64_t cols, bool vec) {
+  if (vec && row < rows && col + 3 < cols) return *reinterpret_cast<const float4 *>(P + row * ld + col);
+  float t[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) t[q] = (row < rows && col + q < cols) ? P[row * ld + col + q] : 0.0f;
+  return make_float4(t[0], t[1], t[2], t[3]);
+}
+
+__device__ __forceinline__ void load_slab(Slab &s, const float *__restrict__ A, const float *__restrict__ B,
+                                          int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t m0,
+                                          int64_t n0, int64_t k0, bool a_vec, bool b_vec, int tid) {
+  // A: 128 rows x 32 k = 1024 float4, four per thread; 8 lanes cover a row.
+  // B: 32 k x 128 n = 1024 float4, four per thread; 32 lanes cover a row.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = tid + kThreads * i;
+    s.a[i] = load4(A, m0 + (idx >> 3), k0 + 4 * (idx & 7), lda, M, K, a_vec);
+    s.b[i] = load4(B, k0 + (idx >> 5), n0 + 4 * (idx & 31), ldb, K, N, b_vec);
+  }
+}
+
+__device__ __forceinline__ void store_slab(const Slab &s, float *__restrict__ As, float *__restrict__ Bs, int tid) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = tid + kThreads * i;
+    *reinterpret_cast<float4 *>(As + (idx >> 3) * LDA + 4 * (idx & 7)) = s.a[i];
+    *reinterpret_cast<float4 *>(Bs + (idx >> 5) * LDB + 4 * (idx & 31)) = s.b[i];
+  }
+}
+
+__device__ __forceinline__ void compute_slab(v16f (&acc)[2][2], const float *__restrict__ As,
+                                             const float *__restrict__ Bs, int wm, int wn, int lane) {
+  const int r = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int c = 0; c < BK / 8; ++c) {
+    float4 a[2];
+    float b[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      a[i] = *reinterpret_cast<const float4 *>(As + (wm * 64 + i * 32 + r) * LDA + 8 * c + 4 * h);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) b[j][s] = Bs[(8 * c + 4 * h + s) * LDB + wn * 64 + j * 32 + r];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const float av = s == 0 ? a[i].x : s == 1 ? a[i].y : s == 2 ? a[i].z : a[i].w;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, b[j][s], acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+}
+
+// Launch index -> (tile row, tile column): XCD-contiguous, then grouped.
+__device__ __forceinline__ void tile_coords(int64_t pid, int64_t tiles_m, int64_t tiles_n, bool xcd_remap,
+                                            int64_t &tm, int64_t &tn) {
+  const int64_t total = tiles_m * tiles_n;
+  if (xcd_remap) pid = (pid & 7) * (total >> 3) + (pid >> 3);
+  const int64_t width = kGroupM * tiles_n;
+  const int64_t group = pid / width;
+  const int64_t first_m = group * kGroupM;
+  const int64_t gsz = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;
+  tm = first_m + (pid % width) % gsz;
+  tn = (pid % width) / gsz;
+}
+
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(kThreads)
+gemm(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
+  const float *__restrict__ Ap = KH_PTR(A);
+  const float *__restrict__ Bp = KH_PTR(B);
+  float *__restrict__ Cp = KH_PTR(C);
+  const int64_t M = A_n0, K = A_n1, N = B_n1;
+  const int64_t lda = A_s0, ldb = B_s0, ldc = C_s0;
+
+  __shared__ __attribute__((aligned(16))) float As[2][BM * LDA];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDB];
+
+  const int tid = threadIdx.x;
+  const int lane = kh::lane_id();
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const bool a_vec = ((K & 3) == 0) && ((lda & 3) == 0) && kh::aligned16(Ap);
+  const bool b_vec = ((N & 3) == 0) && ((ldb & 3) == 0) && kh::aligned16(Bp);
+
+  const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int64_t total = tiles_m * tiles_n;
+  const int64_t nslabs = (K + BK - 1) / BK;
+  const int64_t nblocks = (int64_t)gridDim.x * gridDim.y * gridDim.z;
+  const int64_t bid = blockIdx.x + (int64_t)gridDim.x * (blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
+  const bool xcd_remap = (nblocks == total) && ((total & 7) == 0);
+
+  for (int64_t pid = bid; pid < total; pid += nblocks) {
+    int64_t tm, tn;
+    tile_coords(pid, tiles_m, tiles_n, xcd_remap, tm, tn);
+    const int64_t m0 = tm * BM, n0 = tn * BN;
+
+    v16f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
+
+    Slab s;
+    load_slab(s, Ap, Bp, M, N, K, lda, ldb, m0, n0, 0, a_vec, b_vec, tid);
+    store_slab(s, As[0], Bs[0], tid);
+    __syncthreads();
+    for (int64_t ks = 0; ks < nslabs; ++ks) {
+      const int cur = ks & 1;
+      const bool more = ks + 1 < nslabs;
+      if (more) load_slab(s, Ap, Bp, M, N, K, lda, ldb, m0, n0, (ks + 1) * BK, a_vec, b_vec, tid);
+      compute_slab(acc, As[cur], Bs[cur], wm, wn, lane);
+      if (more) store_slab(s, As[cur ^ 1], Bs[cur ^ 1], tid);
+      __syncthreads();
+    }
+
+    // Accumulator layout: lane l, register r -> row 8(r/4) + 4(l/32) + r%4,
+    // column l%32 of the 32x32 block.
+    const int col = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int64_t gc = n0 + wn * 64 + j * 32 + col;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t gr = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (gr < M && gc < N) Cp[gr * ldc + gc] = acc[i][j][r];
+        }
+      }
+    }
+  }
+}

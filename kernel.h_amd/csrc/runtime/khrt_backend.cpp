@@ -98,6 +98,38 @@ void **LaunchArgs::params() {
   return params_.data();
 }
 
+// Structural check of a 64-bit little-endian AMDGPU ELF image of `size`
+// bytes: header fields, and program headers, section headers and every
+// section with file contents inside the image. Returns "" when sound.
+std::string check_elf_image(const unsigned char *b, size_t size) {
+  auto rd16 = [&](size_t off) { uint16_t v; std::memcpy(&v, b + off, 2); return v; };
+  auto rd32 = [&](size_t off) { uint32_t v; std::memcpy(&v, b + off, 4); return v; };
+  auto rd64 = [&](size_t off) { uint64_t v; std::memcpy(&v, b + off, 8); return v; };
+  auto inside = [&](uint64_t off, uint64_t len) { return off <= size && len <= size - off; };
+  if (b[4] != 2 || b[5] != 1) return "image is not a 64-bit little-endian ELF";
+  if (rd16(18) != 0xE0) return "image is not an AMDGPU code object (e_machine " + std::to_string(rd16(18)) + ")";
+  const uint64_t phoff = rd64(32), shoff = rd64(40);
+  const uint16_t phentsize = rd16(54), phnum = rd16(56), shentsize = rd16(58), shnum = rd16(60);
+  if (phnum > 0 && (phentsize < 56 || !inside(phoff, uint64_t(phentsize) * phnum))) {
+    return "program header table lies outside the image (truncated?)";
+  }
+  if (shnum > 0 && (shentsize < 64 || !inside(shoff, uint64_t(shentsize) * shnum))) {
+    return "section header table lies outside the image (truncated?)";
+  }
+  for (uint16_t i = 0; i < phnum; ++i) {
+    const size_t p = phoff + size_t(i) * phentsize;
+    if (!inside(rd64(p + 8), rd64(p + 32))) return "segment " + std::to_string(i) + " lies outside the image";
+  }
+  for (uint16_t i = 0; i < shnum; ++i) {
+    const size_t s = shoff + size_t(i) * shentsize;
+    const uint32_t type = rd32(s + 4);
+    if (type != 8 /* SHT_NOBITS */ && type != 0 && !inside(rd64(s + 24), rd64(s + 32))) {
+      return "section " + std::to_string(i) + " lies outside the image";
+    }
+  }
+  return "";
+}
+
 void register_prelude(void *function, void *prelude) {
   std::lock_guard<std::mutex> lock(g_mu);
   g_prelude[function] = prelude;
@@ -230,6 +262,12 @@ int khrt_module_load_data(void **module, const void *image, size_t size) {
   const unsigned char *b = static_cast<const unsigned char *>(image);
   if (!(b[0] == 0x7f && b[1] == 'E' && b[2] == 'L' && b[3] == 'F')) {
     return fail(KHRT_E_INVALID, "khrt_module_load_data: image is not an ELF code object");
+  }
+  // hipModuleLoadData takes no size: a truncated image would be read past
+  // its end by the runtime. Check every table and section the loader will
+  // touch lies inside `size` first.
+  if (std::string err = check_elf_image(b, size); !err.empty()) {
+    return fail(KHRT_E_INVALID, "khrt_module_load_data: " + err);
   }
   if (int rc = ensure_device()) return rc;
   hipModule_t m = nullptr;

@@ -179,7 +179,7 @@ def check(rc: int) -> None:
 def _ptr(x) -> int | None:
     if x is None:
         return None
-    if isinstance(x, Buffer):
+    if isinstance(x, (Buffer, Stream, Event)):
         return x.ptr
     return int(x)
 

@@ -296,3 +296,21 @@ def test_corrupt_image_is_a_typed_error():
     with pytest.raises(kh.KhrtError) as e:
         kh.GpuModule(b"\x00" * 128)
     assert e.value.code == kh.KHRT_E_INVALID and "not an ELF" in e.value.message
+
+
+@pytest.mark.parametrize("name", ["vecadd", "scan"])
+def test_truncated_images_rejected_before_the_runtime(name):
+    # hipModuleLoadData has no size argument, so the ELF structure is checked
+    # on the host first: every truncation of a real code object is refused
+    # with KHRT_E_INVALID before any HIP call (this runs without a device).
+    blob = kh.code_object(name)
+    for cut in list(range(64, len(blob), 97)) + [len(blob) - 1]:
+        with pytest.raises(kh.KhrtError) as e:
+            kh.GpuModule(blob[:cut])
+        assert e.value.code == kh.KHRT_E_INVALID, (cut, e.value.message)
+        assert "outside the image" in e.value.message or "truncated" in e.value.message
+    bad = bytearray(blob)
+    bad[18] = 0x3E  # e_machine = x86-64
+    with pytest.raises(kh.KhrtError) as e:
+        kh.GpuModule(bytes(bad))
+    assert "not an AMDGPU code object" in e.value.message

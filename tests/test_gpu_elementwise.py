@@ -85,7 +85,10 @@ def test_fused_gelu_vs_fp64_reference(dev, n):
 
 
 def test_fused_gelu_extremes_finite(dev):
-    x = np.array([0.0, -1.0 / 3.0, 1e-30, -1e-30, 50.0, -50.0, 1e30, -1e30, 3.4e38, -3.4e38, 8.0, -8.0],
+    # |x| up to 2e38 keeps t = 1.5x + 0.5 inside fp32 (beyond ~2.27e38 the
+    # template's own fp32 fma overflows); t^3 overflowing must still give
+    # gelu(t) = t for large positive t and 0 for large negative t.
+    x = np.array([0.0, -1.0 / 3.0, 1e-30, -1e-30, 50.0, -50.0, 1e30, -1e30, 2e38, -2e38, 8.0, -8.0],
                  np.float32)
     n = x.size
     dx, do = up(x), empty(n)

@@ -1,0 +1,84 @@
+"""fp32 MFMA GEMM on the GPU against the pinned oracle.
+
+* Exact-integer fill (e2e_gemm_test.cpp:26-30, 70-75): products and K-deep
+  sums are exact in fp32 for K <= 4096, so the result must be bit-exact at
+  any accumulation order; sizes are the reference's {128, 512, 1024, 2048,
+  4096, 1000}.
+* BASELINE inputs U[-1,1]: relative Frobenius <= 1e-5 against the fp64
+  reference (e2e_gemm_test.cpp:281); 8192^3 is checked on a row sample.
+* Ragged shapes, the reference launch geometry, and the A*B^T negative
+  control (e2e_gemm_test.cpp:289-375).
+"""
+import numpy as np
+import pytest
+
+import kernelh as kh
+import oracle as O
+from khtest import down, empty, say, up
+
+pytestmark = pytest.mark.gpu
+
+
+def _gemm(A, B, m, n, k):
+    dA, dB, dC = up(A), up(B), empty(m * n)
+    say(f"gemm m={m} n={n} k={k}")
+    kh.gemm(dA, dB, dC, m, n, k)
+    return down(dC, m * n).reshape(m, n)
+
+
+@pytest.mark.parametrize("size", [128, 512, 1024, 2048, 4096, 1000])
+def test_gemm_integer_fill_bit_exact(dev, size):
+    A, B = O.gemm_int_inputs(size, size, size)
+    C = _gemm(A, B, size, size, size)
+    ref = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)  # exact integers
+    assert np.array_equal(C, ref)
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 512, 512), (2048, 2048, 2048), (8192, 8192, 256)])
+def test_gemm_baseline_inputs_rel_frobenius(dev, m, n, k):
+    A = O.uniform(m * k, 0xA11 + m, -1.0, 1.0).reshape(m, k)
+    B = O.uniform(k * n, 0xB22 + n, -1.0, 1.0).reshape(k, n)
+    C = _gemm(A, B, m, n, k)
+    rows = np.arange(m) if m <= 2048 else np.arange(0, m, 97)
+    ref = A[rows].astype(np.float64) @ B.astype(np.float64)
+    err = O.rel_frobenius(C[rows], ref)
+    print(f"gemm {m}x{n}x{k} rel-frobenius={err:.3e}")
+    assert err <= 1e-5
+
+
+def test_gemm_8192_cubed_row_sample(dev):
+    m = n = k = 8192
+    A = O.uniform(m * k, 0xA8192, -1.0, 1.0).reshape(m, k)
+    B = O.uniform(k * n, 0xB8192, -1.0, 1.0).reshape(k, n)
+    C = _gemm(A, B, m, n, k)
+    rows = np.concatenate([np.arange(0, m, 257), [m - 1]])
+    ref = A[rows].astype(np.float64) @ B.astype(np.float64)
+    err = O.rel_frobenius(C[rows], ref)
+    print(f"gemm 8192^3 rel-frobenius (rows sampled)={err:.3e}")
+    assert err <= 1e-5
+    assert np.all(np.isfinite(C))
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (100, 37, 53), (129, 130, 131), (7, 1000, 3), (300, 5, 4097),
+                                   (128, 256, 33), (255, 129, 64)])
+def test_gemm_ragged_shapes(dev, m, n, k):
+    A = O.uniform(m * k, 1, -1.0, 1.0).reshape(m, k)
+    B = O.uniform(k * n, 2, -1.0, 1.0).reshape(k, n)
+    C = _gemm(A, B, m, n, k)
+    ref = O.ref_gemm(A, B, m, n, k)
+    assert O.rel_frobenius(C, ref) <= 1e-5
+
+
+def test_gemm_reference_geometry_and_negative_control(dev):
+    m = n = k = 256
+    A, B = O.gemm_int_inputs(m, n, k)
+    dA, dB, dC = up(A), up(B), empty(m * n)
+    f = kh.template_function("gemm")
+    args = kh.LaunchArgs().add_memref(dA, [m, k]).add_memref(dB, [k, n]).add_memref(dC, [m, n])
+    assert args.param_count() == 21
+    say("gemm reference geometry ceil(m/32) x 256")
+    kh.kernel_launch(f, ((m + 31) // 32, 1, 1), (256, 1, 1), args)
+    C = down(dC, m * n).reshape(m, n)
+    assert np.array_equal(C, O.ref_gemm(A, B, m, n, k).astype(np.float32))
+    wrong = O.ref_gemm(A, B, m, n, k, transpose_b=True)
+    assert O.rel_frobenius(C, wrong) > 1e-5
