@@ -7,8 +7,10 @@
 // grid-stride step.
 #define KH_EW_UNROLL 4
 
-// Scan: 256 threads x 16 elements per tile.
-#define KH_SCAN_TILE 4096
+// Scan: workgroup size chosen by the launcher (the kernel accepts 256..1024);
+// each thread owns 16 elements, so a tile is 16 x KH_SCAN_THREADS elements.
+#define KH_SCAN_THREADS 1024
+#define KH_SCAN_TILE (16 * KH_SCAN_THREADS)
 
 // GEMM block tile (rows of C x columns of C per workgroup of 256 threads).
 #define KH_GEMM_BM 128

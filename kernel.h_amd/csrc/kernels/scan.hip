@@ -9,10 +9,15 @@
 // (scan.cpp:400-452). Here `scan` alone produces the final y in one pass over
 // HBM (read x once, write y once: 8 B/element):
 //
-//   * A workgroup of 256 threads owns a tile of 4096 elements (16 per
-//     thread, four dwordx4 loads). Tiles are handed out in launch order by
-//     an atomic ticket, so a tile only ever waits on tiles already owned by
-//     running workgroups (deadlock-free under any grid size).
+//   * A workgroup of W threads (256..1024, a multiple of 64) owns a tile of
+//     16 W elements (16 consecutive per thread, four dwordx4 loads). Tiles
+//     are handed out in order by an atomic ticket, so a tile only ever waits
+//     on tiles already owned by running workgroups (deadlock-free under any
+//     grid size).
+//   * Workgroups are persistent and pipelined: while a tile's prefix is
+//     being looked up, the workgroup already holds the ticket for its next
+//     tile and that tile's loads are in flight, so HBM latency overlaps the
+//     look-back.
 //   * Partial sums are carried in fp64. Every fp32 input is exact in fp64
 //     and, for inputs on a common 2^-e grid whose total needs <= 53 bits
 //     (every configuration the reference tests: U[0,1) on 2^-24 or
@@ -21,19 +26,26 @@
 //     template computes with double-float + 3-word expansions
 //     (scan.cpp:25-38).
 //   * Decoupled look-back (Merrill & Garland 2016): each tile publishes its
-//     aggregate (status 1) as soon as it is reduced, then its inclusive
-//     prefix (status 2). Wave 0 of a tile inspects 64 predecessors per step
-//     (one per lane) and stops at the nearest inclusive prefix.
+//     aggregate as soon as it is reduced, then its inclusive prefix. Wave 0
+//     of a tile inspects 256 predecessors per step (four per lane, loads
+//     issued together) and stops at the nearest inclusive prefix.
 //
 // Look-back state lives in the caller's totals buffers (the reference ABI
 // has no separate workspace):
-//   totals_lo as uint32: [0] = tile ticket, [1 + t] = status of tile t
-//   totals_hi as double: [2t] = aggregate of tile t, [2t+1] = inclusive prefix
-// Capacity: ceil(n/4096) tiles need (1 + tiles) words and 4 tiles-words of
-// T = ceil(n/256) words; the host launcher checks it. The state must be zero
-// when `scan` starts: `scan_reset` (same code object) clears it and the
-// runtime launches it first, in stream order, before every `scan`;
-// `scan_totals` clears it again afterwards.
+//   totals_lo as uint32: [0] = tile ticket
+//   totals_hi as 64-bit slots: [2t] = aggregate of tile t, [2t+1] = its
+//       inclusive prefix, each an fp64 bit pattern, all-ones = not published
+// All-ones cannot be a published value: an fp32 input widened to fp64 has
+// its low 29 mantissa bits clear and fp64 addition only yields canonical or
+// propagated NaN payloads, so a slot's single 64-bit load tells both whether
+// and what was published. Slots are written and polled with relaxed
+// agent-scope atomics (coherent across the 8 XCD L2s without the L2
+// write-back/invalidate an acquire/release pair would cost on every poll).
+// Capacity: tiles of >= 4096 elements need 16 B each in totals_hi
+// (T = ceil(n/256) floats); the kernel refuses (y := NaN) anything else.
+// `scan_reset` (same code object) clears the ticket and marks every slot
+// empty; the runtime launches it first, in stream order, before every
+// `scan`, and `scan_totals` does the same afterwards.
 //
 // Every wait is bounded: after kSpinLimit polls a tile gives up, poisons its
 // result with NaN and records the failure in the ticket word's top bit, so a
@@ -42,26 +54,21 @@
 
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kMaxThreads = 1024;
+constexpr int kMinThreads = 256;
 constexpr int kPerThread = 16;
-constexpr int kTile = kThreads * kPerThread;  // 4096
+constexpr int kMinTile = kMinThreads * kPerThread;  // 4096: sizes the state
+constexpr int kWindow = 4;  // predecessors polled per lane per look-back step
 constexpr uint32_t kSpinLimit = 1u << 22;
 constexpr uint32_t kFailBit = 0x80000000u;
+constexpr uint64_t kEmpty = ~0ull;
 
-__device__ __forceinline__ uint32_t load_acquire(const uint32_t *p) {
-  return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void store_release(uint32_t *p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ double load_relaxed(const double *p) {
+__device__ __forceinline__ uint64_t slot_load(const uint64_t *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void store_relaxed(double *p, double v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void slot_store(uint64_t *p, double v) {
+  __hip_atomic_store(p, (uint64_t)__double_as_longlong(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ double wave_sum_f64(double v) {
@@ -80,18 +87,8 @@ __device__ __forceinline__ double wave_incl_scan_f64(double v, int lane) {
   return v;
 }
 
-// Scans one 4096-element tile: load, fp64 local + wave + block scans,
-// look-back for the tile's exclusive prefix, store.
-__device__ __forceinline__ void scan_tile(const float *__restrict__ X, float *__restrict__ Y, uint32_t *state,
-                                          double *vals, int64_t n, int64_t ntiles, int64_t tile, bool vec,
-                                          double *s_wave_total, double *s_prefix) {
-  const int tid = threadIdx.x;
-  const int lane = kh::lane_id();
-  const int wave = tid / kh::kWave;
-
-  // ---- load 16 consecutive elements per thread ----------------------------
-  const int64_t base = tile * kTile + (int64_t)tid * kPerThread;
-  float v[kPerThread];
+__device__ __forceinline__ void load_tile(float (&v)[kPerThread], const float *__restrict__ X, int64_t base,
+                                          int64_t n, bool vec) {
   if (vec && base + kPerThread <= n) {
 #pragma unroll
     for (int q = 0; q < kPerThread / 4; ++q) {
@@ -105,90 +102,10 @@ __device__ __forceinline__ void scan_tile(const float *__restrict__ X, float *__
 #pragma unroll
     for (int q = 0; q < kPerThread; ++q) v[q] = (base + q < n) ? X[base + q] : 0.0f;
   }
+}
 
-  // ---- thread-local inclusive scan in fp64 --------------------------------
-  double p[kPerThread];
-  double acc = 0.0;
-#pragma unroll
-  for (int q = 0; q < kPerThread; ++q) {
-    acc += (double)v[q];
-    p[q] = acc;
-  }
-  // ---- wave scan of thread totals, then block totals ----------------------
-  const double incl = wave_incl_scan_f64(acc, lane);
-  const double thread_excl = incl - acc;  // exact: both are exact partial sums
-  if (lane == kh::kWave - 1) s_wave_total[wave] = incl;
-  __syncthreads();
-  double wave_excl = 0.0, agg = 0.0;
-#pragma unroll
-  for (int w = 0; w < kThreads / kh::kWave; ++w) {
-    const double t = s_wave_total[w];
-    if (w < wave) wave_excl += t;
-    agg += t;
-  }
-
-  // ---- decoupled look-back (wave 0) ----------------------------------------
-  if (wave == 0) {
-    double excl = 0.0;
-    if (tile == 0) {
-      if (ntiles > 1 && lane == 0) {
-        store_relaxed(&vals[1], agg);
-        store_release(&state[1], 2u);
-      }
-    } else {
-      if (lane == 0) {
-        store_relaxed(&vals[2 * tile], agg);
-        store_release(&state[1 + tile], 1u);
-      }
-      int64_t end = tile - 1;  // newest predecessor still to account for
-      uint32_t spins = 0;
-      bool failed = false;
-      for (;;) {
-        const int64_t idx = end - lane;
-        // Lanes before tile 0 act as an inclusive prefix of value 0.
-        const uint32_t st = (idx >= 0) ? load_acquire(&state[1 + idx]) : 2u;
-        const uint64_t m_incl = __ballot(st == 2u);
-        const uint64_t m_zero = __ballot(st == 0u);
-        const int first_incl = m_incl ? __builtin_ctzll(m_incl) : kh::kWave;
-        const uint64_t below = (first_incl >= kh::kWave) ? ~0ull : ((1ull << first_incl) - 1ull);
-        if ((m_zero & below) != 0) {
-          // A predecessor nearer than the first inclusive prefix has not
-          // published yet: poll the window again (bounded).
-          if (++spins > kSpinLimit) {
-            failed = true;
-            break;
-          }
-          __builtin_amdgcn_s_sleep(1);
-          continue;
-        }
-        double contrib = 0.0;
-        if (lane < first_incl) {
-          contrib = load_relaxed(&vals[2 * idx]);
-        } else if (lane == first_incl && idx >= 0) {
-          contrib = load_relaxed(&vals[2 * idx + 1]);
-        }
-        excl += wave_sum_f64(contrib);
-        if (first_incl < kh::kWave) break;
-        end -= kh::kWave;
-      }
-      if (failed) {
-        excl = __builtin_nan("");
-        if (lane == 0) atomicOr(state, kFailBit);
-      }
-      if (lane == 0) {
-        store_relaxed(&vals[2 * tile + 1], excl + agg);
-        store_release(&state[1 + tile], 2u);
-      }
-    }
-    if (lane == 0) *s_prefix = excl;
-  }
-  __syncthreads();
-
-  // ---- finish: y = fl32(prefix + wave_excl + thread_excl + local) ---------
-  const double off = *s_prefix + wave_excl + thread_excl;
-  float o[kPerThread];
-#pragma unroll
-  for (int q = 0; q < kPerThread; ++q) o[q] = (float)(off + p[q]);
+__device__ __forceinline__ void store_tile(const float (&o)[kPerThread], float *__restrict__ Y, int64_t base,
+                                           int64_t n, bool vec) {
   if (vec && base + kPerThread <= n) {
 #pragma unroll
     for (int q = 0; q < kPerThread / 4; ++q)
@@ -200,9 +117,64 @@ __device__ __forceinline__ void scan_tile(const float *__restrict__ X, float *__
   }
 }
 
+// Exclusive prefix of `tile` from its predecessors' published slots (run by
+// one whole wave; the result is wave-uniform). NaN if the bounded wait ran
+// out.
+__device__ __forceinline__ double look_back(uint64_t *slots, uint32_t *state, int64_t tile, int lane) {
+  double excl = 0.0;
+  int64_t end = tile - 1;  // newest predecessor still to account for
+  uint32_t spins = 0;
+  for (;;) {
+    // Lane l, slot j covers distance d = l + 64 j behind `end`.
+    uint64_t inc[kWindow], ag[kWindow];
+#pragma unroll
+    for (int j = 0; j < kWindow; ++j) {
+      const int64_t idx = end - lane - kh::kWave * j;
+      // Slots before tile 0 act as an inclusive prefix of value 0.
+      inc[j] = (idx >= 0) ? slot_load(&slots[2 * idx + 1]) : 0ull;
+      ag[j] = (idx >= 0) ? slot_load(&slots[2 * idx]) : kEmpty;
+    }
+    // Nearest inclusive prefix, and whether every nearer predecessor has at
+    // least published its aggregate.
+    int first = kWindow * kh::kWave;
+#pragma unroll
+    for (int j = kWindow - 1; j >= 0; --j) {
+      const uint64_t m = __ballot(inc[j] != kEmpty);
+      if (m) first = kh::kWave * j + __builtin_ctzll(m);
+    }
+    bool pending = false;
+#pragma unroll
+    for (int j = 0; j < kWindow; ++j) {
+      const int d = lane + kh::kWave * j;
+      if (d < first && ag[j] == kEmpty) pending = true;
+    }
+    if (__ballot(pending) != 0) {
+      if (++spins > kSpinLimit) {
+        if (lane == 0) atomicOr(state, kFailBit);
+        return __builtin_nan("");
+      }
+      __builtin_amdgcn_s_sleep(1);
+      continue;
+    }
+    double contrib = 0.0;
+#pragma unroll
+    for (int j = 0; j < kWindow; ++j) {
+      const int d = lane + kh::kWave * j;
+      if (d < first) {
+        contrib += __longlong_as_double((long long)ag[j]);
+      } else if (d == first) {
+        contrib += __longlong_as_double((long long)inc[j]);
+      }
+    }
+    excl += wave_sum_f64(contrib);
+    if (first < kWindow * kh::kWave) return excl;
+    end -= kWindow * kh::kWave;
+  }
+}
+
 }  // namespace
 
-extern "C" __global__ void __launch_bounds__(kThreads)
+extern "C" __global__ void __launch_bounds__(kMaxThreads)
 scan(KH_MEMREF1(const float, x), KH_MEMREF1(float, y), KH_MEMREF1(float, y_lo),
      KH_MEMREF1(float, totals_hi), KH_MEMREF1(float, totals_lo)) {
   (void)y_lo_alloc;
@@ -210,44 +182,118 @@ scan(KH_MEMREF1(const float, x), KH_MEMREF1(float, y), KH_MEMREF1(float, y_lo),
   const float *__restrict__ X = KH_PTR(x);
   float *__restrict__ Y = KH_PTR(y);
   uint32_t *state = reinterpret_cast<uint32_t *>(KH_PTR(totals_lo));
-  double *vals = reinterpret_cast<double *>(KH_PTR(totals_hi));
+  uint64_t *slots = reinterpret_cast<uint64_t *>(KH_PTR(totals_hi));
   const int64_t n = x_n0;
-  const int64_t ntiles = (n + kTile - 1) / kTile;
+  const int64_t tile_elems = (int64_t)blockDim.x * kPerThread;
+  const int64_t ntiles = (n + tile_elems - 1) / tile_elems;
   const int tid = threadIdx.x;
+  const int lane = kh::lane_id();
+  const int wave = tid / kh::kWave;
+  const int nwaves = blockDim.x / kh::kWave;
 
-  __shared__ int64_t s_tile;
-  __shared__ double s_wave_total[kThreads / kh::kWave];
+  __shared__ int64_t s_ticket[2];
+  __shared__ double s_wave_total[kMaxThreads / kh::kWave];
   __shared__ double s_prefix;
 
-  const bool vec = kh::aligned16(X) && kh::aligned16(Y);
-
-  if (ntiles == 1) {
-    // One tile: block 0 owns it and no look-back state is touched.
-    if (blockIdx.x == 0) scan_tile(X, Y, state, vals, n, ntiles, 0, vec, s_wave_total, &s_prefix);
+  // The look-back state needs 16 B per tile in totals_hi; workgroups of at
+  // least 256 threads always fit the reference's T = ceil(n/256) floats.
+  // Anything smaller is refused here by poisoning y, never by a hang.
+  if (ntiles > 1 && (blockDim.x < kMinThreads || 4 * ntiles > totals_hi_n0)) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + tid; i < n; i += (int64_t)blockDim.x * gridDim.x)
+      Y[i] = __builtin_nanf("");
     return;
   }
+  const bool vec = kh::aligned16(X) && kh::aligned16(Y);
+  const bool single = ntiles == 1;  // one tile: block 0, no look-back state
+
+  if (single) {
+    if (blockIdx.x != 0) return;
+    s_ticket[0] = 0;
+  } else if (tid == 0) {
+    s_ticket[0] = (int64_t)(atomicAdd(state, 1u) & ~kFailBit);
+  }
+  __syncthreads();
+  int64_t tile = s_ticket[0];
+  if (tile >= ntiles) return;
+
+  float v[kPerThread];
+  load_tile(v, X, tile * tile_elems + (int64_t)tid * kPerThread, n, vec);
+  int parity = 0;
+
   for (;;) {
-    if (tid == 0) s_tile = (int64_t)(atomicAdd(state, 1u) & ~kFailBit);
+    // The next ticket is fetched by the last wave while the others reduce.
+    if (wave == nwaves - 1 && lane == 0) {
+      s_ticket[parity ^ 1] = single ? ntiles : (int64_t)(atomicAdd(state, 1u) & ~kFailBit);
+    }
+
+    // ---- thread total (fp64), wave scan, block totals -----------------------
+    double acc = 0.0;
+#pragma unroll
+    for (int q = 0; q < kPerThread; ++q) acc += (double)v[q];
+    const double incl = wave_incl_scan_f64(acc, lane);
+    const double thread_excl = incl - acc;  // exact: both are exact partial sums
+    if (lane == kh::kWave - 1) s_wave_total[wave] = incl;
     __syncthreads();
-    const int64_t tile = s_tile;
-    if (tile >= ntiles) return;
-    scan_tile(X, Y, state, vals, n, ntiles, tile, vec, s_wave_total, &s_prefix);
-    __syncthreads();  // s_tile / s_wave_total / s_prefix are reused
+    double wave_excl = 0.0, agg = 0.0;
+    for (int w = 0; w < nwaves; ++w) {
+      const double t = s_wave_total[w];
+      if (w < wave) wave_excl += t;
+      agg += t;
+    }
+    const int64_t next = s_ticket[parity ^ 1];
+
+    // ---- publish the aggregate, then start the next tile's loads -------------
+    // (tile 0 has no predecessors: its aggregate is its inclusive prefix.)
+    if (!single && wave == 0 && lane == 0) slot_store(&slots[2 * tile + (tile == 0 ? 1 : 0)], agg);
+    float vn[kPerThread];
+    if (next < ntiles) load_tile(vn, X, next * tile_elems + (int64_t)tid * kPerThread, n, vec);
+
+    // ---- decoupled look-back (wave 0) -----------------------------------------
+    if (wave == 0) {
+      double excl = 0.0;
+      if (tile > 0) {
+        excl = look_back(slots, state, tile, lane);
+        if (lane == 0) slot_store(&slots[2 * tile + 1], excl + agg);
+      }
+      if (lane == 0) s_prefix = excl;
+    }
+    __syncthreads();
+
+    // ---- y = fl32(prefix + wave_excl + thread_excl + running local sum) ------
+    double run = s_prefix + wave_excl + thread_excl;
+    float o[kPerThread];
+#pragma unroll
+    for (int q = 0; q < kPerThread; ++q) {
+      run += (double)v[q];
+      o[q] = (float)run;
+    }
+    store_tile(o, Y, tile * tile_elems + (int64_t)tid * kPerThread, n, vec);
+
+    if (next >= ntiles) return;
+    tile = next;
+#pragma unroll
+    for (int q = 0; q < kPerThread; ++q) v[q] = vn[q];
+    parity ^= 1;
   }
 }
 
-// Clears the look-back state (ticket + 1 status word per tile) in
-// totals_lo. Launched by the runtime before every `scan` on the same stream.
+// Clears the ticket (totals_lo[0]) and marks every tile slot in totals_hi
+// empty. Sized for the smallest tile any scan launch uses (256 threads).
+__device__ __forceinline__ void reset_state(uint32_t *state, uint64_t *slots, int64_t ntiles) {
+  const int64_t stride = (int64_t)blockDim.x * gridDim.x;
+  const int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i0 == 0) state[0] = 0u;
+  for (int64_t i = i0; i < 2 * ntiles; i += stride) slots[i] = kEmpty;
+}
+
+// Launched by the runtime before every `scan` on the same stream.
 extern "C" __global__ void __launch_bounds__(256)
 scan_reset(KH_MEMREF1(const float, x), KH_MEMREF1(float, y), KH_MEMREF1(float, y_lo),
            KH_MEMREF1(float, totals_hi), KH_MEMREF1(float, totals_lo)) {
-  const int64_t n = x_n0;
-  const int64_t ntiles = (n + kTile - 1) / kTile;
+  const int64_t ntiles = (x_n0 + kMinTile - 1) / kMinTile;
   if (ntiles <= 1) return;
-  uint32_t *state = reinterpret_cast<uint32_t *>(KH_PTR(totals_lo));
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < ntiles + 1;
-       i += (int64_t)blockDim.x * gridDim.x)
-    state[i] = 0u;
+  reset_state(reinterpret_cast<uint32_t *>(KH_PTR(totals_lo)), reinterpret_cast<uint64_t *>(KH_PTR(totals_hi)),
+              ntiles);
 }
 
 // The reference's second pass (scan.cpp:350-453). With the single-pass
@@ -261,12 +307,11 @@ scan_totals(KH_MEMREF1(float, totals_hi), KH_MEMREF1(float, totals_lo), KH_MEMRE
             KH_MEMREF1(float, y_lo)) {
   const int64_t n = y_n0;
   const int64_t T = off_hi_n0;
-  const int64_t ntiles = (n + kTile - 1) / kTile;
+  const int64_t ntiles = (n + kMinTile - 1) / kMinTile;
   const float *__restrict__ Y = KH_PTR(y);
   float *__restrict__ oh = KH_PTR(off_hi);
   float *__restrict__ ol = KH_PTR(off_lo);
   float *__restrict__ ol2 = KH_PTR(off_lo2);
-  uint32_t *state = reinterpret_cast<uint32_t *>(KH_PTR(totals_lo));
   const int64_t stride = (int64_t)blockDim.x * gridDim.x;
   for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < T; b += stride) {
     oh[b] = (b == 0) ? 0.0f : Y[b * 256 - 1];
@@ -274,6 +319,7 @@ scan_totals(KH_MEMREF1(float, totals_hi), KH_MEMREF1(float, totals_lo), KH_MEMRE
     ol2[b] = 0.0f;
   }
   if (ntiles > 1) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < ntiles + 1; i += stride) state[i] = 0u;
+    reset_state(reinterpret_cast<uint32_t *>(KH_PTR(totals_lo)), reinterpret_cast<uint64_t *>(KH_PTR(totals_hi)),
+                ntiles);
   }
 }

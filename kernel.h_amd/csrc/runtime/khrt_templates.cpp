@@ -179,6 +179,7 @@ int geometry(const char *name, const Shape &s, khrt_dim3 &grid, khrt_dim3 &block
   } else if (t == "scan" || t == "scan_totals") {
     if (!need(s, "n", n)) return khrt::fail(KHRT_E_INVALID, t + ": shape attribute 'n' is required and must be positive");
     if (t == "scan") {
+      block.x = KH_SCAN_THREADS;
       grid.x = clamp_grid(ceil_div(n, KH_SCAN_TILE));
     } else {
       grid.x = clamp_grid(std::min<int64_t>(ceil_div(ceil_div(n, 256) + 1, 256), 1024));
@@ -214,6 +215,19 @@ int launch_template(const char *name, khrt::LaunchArgs &args, const Shape &shape
   if (int rc = geometry(name, shape, grid, block)) return rc;
   void *fn = nullptr;
   if (int rc = get_function(t->co, t->name, &fn)) return rc;
+  if (std::strcmp(name, "scan") == 0) {
+    // The look-back scan is persistent: one resident wave of workgroups
+    // loops over tiles, so launch no more workgroups than fit at once.
+    int per_cu = 0;
+    khrt_device_limits live;
+    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, static_cast<hipFunction_t>(fn),
+                                                           static_cast<int>(block.x), 0) == hipSuccess &&
+        per_cu > 0 && khrt_live_limits(&live) == 0 && live.cu_count > 0) {
+      grid.x = static_cast<unsigned>(std::min<int64_t>(grid.x, int64_t(per_cu) * live.cu_count));
+    } else {
+      (void)hipGetLastError();
+    }
+  }
   return khrt::verified_launch(fn, grid, block, 0, stream, args.params(), args.count());
 }
 
@@ -325,11 +339,13 @@ int kh_scan(const float *x, float *y, float *y_lo, float *totals_hi, float *tota
   if (n <= 0) return bad("scan: n must be positive");
   if (!x || !y || !totals_hi || !totals_lo) return bad("scan: null buffer");
   const int64_t T = ceil_div(n, 256);
-  const int64_t tiles = ceil_div(n, KH_SCAN_TILE);
+  const int64_t tiles = ceil_div(n, 4096);  // smallest tile the kernel accepts
   if (tiles > 1 && (reinterpret_cast<uintptr_t>(totals_hi) & 7u) != 0) {
     return bad("scan: totals_hi must be 8-byte aligned (it holds the fp64 look-back values)");
   }
-  if (tiles > 1 && (T < tiles + 1 || T < 4 * tiles)) return bad("scan: totals buffers too small for the look-back state");
+  // Look-back state: 16 B per 4096-element tile in totals_hi, the ticket in
+  // totals_lo[0]. T = ceil(n/256) floats always suffices for n > 4096.
+  if (tiles > 1 && T < 4 * tiles) return bad("scan: totals buffers too small for the look-back state");
   khrt::LaunchArgs args;
   args.add_memref(x, {n});
   args.add_memref(y, {n});
