@@ -1,0 +1,98 @@
+"""Fused fp32 MFMA attention on the GPU against the fp64 reference rows.
+
+Tolerance: every element |g - r| <= 2e-3 + 2e-3 |r| (e2e_attention_test.cpp:
+298-311). Covers the reference's e2e shape (b=2, h=8, s in {512, 1024},
+LCG seeds 0x313A171B / 0x51AC0D3E / 0x29C0FFEE, attention_test.cpp:64-79,
+all rows), the BASELINE shapes b=4, h=16, s in {1024, 4096} with N(0,1)
+inputs (row sample), ragged sequence lengths, the reference launch geometry
+and the no-1/sqrt(d) negative control (e2e_attention_test.cpp:319-348).
+"""
+import numpy as np
+import pytest
+
+import kernelh as kh
+import oracle as O
+from khtest import down, empty, say, up
+
+pytestmark = pytest.mark.gpu
+D = 64
+
+
+def _attention(Q, K, V, b, h, s):
+    n = b * h * s * D
+    dq, dk, dv, do = up(Q), up(K), up(V), empty(n)
+    say(f"attention b={b} h={h} s={s}")
+    kh.attention(dq, dk, dv, do, b, h, s, D)
+    return down(do, n).reshape(b * h, s, D)
+
+
+def _rows(b, h, s, count, seed):
+    if count is None:
+        return np.repeat(np.arange(b * h), s), np.tile(np.arange(s), b * h)
+    rng = np.random.default_rng(seed)
+    bh = rng.integers(0, b * h, count)
+    qi = rng.integers(0, s, count)
+    bh[:2], qi[:2] = [0, b * h - 1], [0, s - 1]
+    return bh, qi
+
+
+def _check(Q, K, V, got, b, h, s, count=None, seed=0):
+    bh, qi = _rows(b, h, s, count, seed)
+    ref = O.ref_attention_rows(Q, K, V, s, D, bh, qi)
+    g = got[bh, qi]
+    viol = O.attention_violation(g, ref)
+    print(f"attention b={b} h={h} s={s} rows={bh.size} max-abs={np.max(np.abs(g - ref)):.3e} viol={viol:.3e}")
+    assert np.all(np.isfinite(g))
+    assert viol <= 2e-3
+    return g, ref, bh, qi
+
+
+@pytest.mark.parametrize("s", [512, 1024])
+def test_attention_reference_e2e_shape_all_rows(dev, s):
+    b, h = 2, 8
+    n = b * h * s * D
+    Q, _ = O.lcg_fill(n, 0x313A171B)
+    K, _ = O.lcg_fill(n, 0x51AC0D3E)
+    V, _ = O.lcg_fill(n, 0x29C0FFEE)
+    O.set_threads(8)
+    _check(Q, K, V, _attention(Q, K, V, b, h, s), b, h, s)
+
+
+@pytest.mark.parametrize("s", [1024, 4096])
+def test_attention_baseline_shapes(dev, s):
+    b, h = 4, 16
+    n = b * h * s * D
+    Q = O.normal(n, 0xA1, 0.0, 1.0)
+    K = O.normal(n, 0xA2, 0.0, 1.0)
+    V = O.normal(n, 0xA3, 0.0, 1.0)
+    O.set_threads(8)
+    _check(Q, K, V, _attention(Q, K, V, b, h, s), b, h, s, count=256, seed=s)
+
+
+@pytest.mark.parametrize("b,h,s", [(1, 1, 1), (1, 2, 100), (2, 3, 67), (1, 1, 129), (3, 1, 200)])
+def test_attention_ragged_sequences(dev, b, h, s):
+    n = b * h * s * D
+    Q = O.normal(n, 1, 0.0, 1.0)
+    K = O.normal(n, 2, 0.0, 1.0)
+    V = O.normal(n, 3, 0.0, 1.0)
+    _check(Q, K, V, _attention(Q, K, V, b, h, s), b, h, s)
+
+
+def test_attention_reference_geometry_and_negative_control(dev):
+    b, h, s = 1, 2, 256
+    n = b * h * s * D
+    Q, _ = O.lcg_fill(n, 0x313A171B)
+    K, _ = O.lcg_fill(n, 0x51AC0D3E)
+    V, _ = O.lcg_fill(n, 0x29C0FFEE)
+    dq, dk, dv, do = up(Q), up(K), up(V), empty(n)
+    f = kh.template_function("attention")
+    args = kh.LaunchArgs()
+    for buf in (dq, dk, dv, do):
+        args.add_memref(buf, [b, h, s, D])
+    assert args.param_count() == 44
+    say("attention reference geometry (seq, heads, batch) x 64")
+    kh.kernel_launch(f, (s, h, b), (64, 1, 1), args)
+    got = down(do, n).reshape(b * h, s, D)
+    g, ref, bh, qi = _check(Q, K, V, got, b, h, s)
+    wrong = O.ref_attention_rows(Q, K, V, s, D, bh, qi, scaled=False)
+    assert O.attention_violation(g, wrong) > 2e-3
