@@ -113,6 +113,43 @@ def make_cases(kh, rng, only):
     return cases
 
 
+def measure_ceilings(kh, stream, reps=5):
+    """Measured roofline denominators: triad and copy over 2^28 floats per
+    buffer (3 GiB / 2 GiB moved per launch, beyond the 256 MB MALL, as the
+    reference's roofline_triad, bench/harness/roofline.cpp:60-84) and the
+    fp32 MFMA microbenchmark (8 independent chains per wave)."""
+    n = 1 << 28
+    a, b, c = kh.Buffer(4 * n), kh.Buffer(4 * n), kh.Buffer(4 * n)
+    a.fill(1.0, stream)
+    b.fill(2.0, stream)
+    e0, e1 = kh.Event(), kh.Event()
+
+    def timed(fn):
+        fn()
+        stream.synchronize()
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_ms(e1) / reps
+
+    t_triad = timed(lambda: kh.roofline_triad(a, b, c, n, stream))
+    t_copy = timed(lambda: kh.roofline_copy(a, c, n, stream))
+    cu = kh.device_info()["cu_count"]
+    blocks, iters = cu * 8, 64
+    out = kh.Buffer(4 * blocks * 256)
+    flops = float(blocks) * 4 * iters * 8 * 4096
+    t_mfma = timed(lambda: kh.roofline_mfma(out, blocks, iters, stream))
+    for buf in (a, b, c, out):
+        buf.free()
+    return {"hbm_triad_gbps": 12.0 * n / (t_triad * 1e-3) / 1e9,
+            "hbm_copy_gbps": 8.0 * n / (t_copy * 1e-3) / 1e9,
+            "fp32_mfma_tflops": flops / (t_mfma * 1e-3) / 1e12,
+            "triad_bytes_per_launch": 12 * n, "copy_bytes_per_launch": 8 * n,
+            "mfma_config": f"{blocks} workgroups x 4 waves x {iters} x 8 v_mfma_f32_32x32x2f32"}
+
+
 def available(kh, name):
     try:
         kh.code_object(name)
@@ -164,6 +201,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-rotate", action="store_true", help="reuse one buffer set (cache-warm)")
+    ap.add_argument("--no-ceilings", action="store_true", help="skip the measured roofline microbenchmarks")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "
@@ -212,21 +250,51 @@ def main() -> int:
     wall = time.perf_counter() - t0
     for c in cases:
         e0, e1 = ev[c.name]
-        c.ms = [e0.elapsed_ms(e1) / a.steps]
+        c.ms_host = e0.elapsed_ms(e1) / a.steps
     log(f"[bench] timed {a.steps} steps in {wall:.3f} s")
+
+    # GPU-side launch duration: the same K back-to-back launches, queued
+    # behind a ~0.35 ms copy so that the host has enqueued them all before
+    # the first one starts. Microsecond-scale kernels are otherwise timed at
+    # the host's submission rate (Python + launch API), not the GPU's.
+    prime_n = 1 << 27
+    pa, pb = kh.Buffer(4 * prime_n), kh.Buffer(4 * prime_n)
+    for c in cases:
+        e0, e1 = ev[c.name]
+        kh.roofline_copy(pa, pb, prime_n, stream)
+        e0.record(stream)
+        for i in range(a.steps):
+            c.launch(c.sets[(a.warmup + i) % len(c.sets)], stream)
+        e1.record(stream)
+        e1.synchronize()
+        c.ms = [e0.elapsed_ms(e1) / a.steps]
+    pa.free()
+    pb.free()
+
+    ceilings = None
+    if not a.no_ceilings:
+        ceilings = measure_ceilings(kh, stream)
+        log(f"[bench] measured ceilings: triad {ceilings['hbm_triad_gbps']:.0f} GB/s, copy "
+            f"{ceilings['hbm_copy_gbps']:.0f} GB/s, fp32 MFMA {ceilings['fp32_mfma_tflops']:.1f} TFLOP/s")
 
     kernels = {}
     for c in cases:
         ms = float(np.mean(c.ms))
         rate = c.work / (ms * 1e-3) / (1e12 if c.unit == "TFLOP/s" else 1e9)
         peak = FP32_MFMA_PEAK_TFLOPS if c.bound == "mfma" else HBM_PEAK_GBPS
-        kernels[c.name] = {"config": c.config, "ms_mean": ms,
-                           "rate": rate, "unit": c.unit,
+        rate_host = c.work / (c.ms_host * 1e-3) / (1e12 if c.unit == "TFLOP/s" else 1e9)
+        kernels[c.name] = {"config": c.config, "ms_mean": ms, "ms_host_paced": c.ms_host,
+                           "rate": rate, "rate_host_paced": rate_host, "unit": c.unit,
                            "bound": c.bound, "peak": peak, "frac": rate / peak,
                            "algorithmic_work_per_launch": c.work, "buffer_sets": len(c.sets)}
+        if ceilings:
+            meas = ceilings["fp32_mfma_tflops"] if c.bound == "mfma" else ceilings["hbm_triad_gbps"]
+            kernels[c.name]["measured_ceiling"] = meas
+            kernels[c.name]["frac_of_measured"] = rate / meas
         if c.traffic_note:
             kernels[c.name]["note"] = c.traffic_note
-        log(f"[bench] {c.name:10s} {ms:9.4f} ms  {rate:9.1f} {c.unit}  ({100 * rate / peak:5.1f}% of peak)")
+        log(f"[bench] {c.name:10s} {ms:9.4f} ms  {rate:9.1f} {c.unit}  ({100 * rate / peak:5.1f}% of peak"
+            + (f", {100 * kernels[c.name]['frac_of_measured']:5.1f}% of measured)" if ceilings else ")"))
 
     head = "gemm" if "gemm" in kernels else (cases[0].name if cases else None)
     hk = kernels.get(head, {})
@@ -248,6 +316,7 @@ def main() -> int:
             "bound": hk["bound"], "achieved": hk["rate"], "peak": hk["peak"],
             "unit": hk["unit"], "frac": hk["frac"], "traffic": None, "kernel": head},
         "kernels": kernels,
+        "measured_ceilings": ceilings,
         "device": {"name": info["name"], "arch": info["arch"], "cu_count": info["cu_count"]},
     }
     if not a.no_cpu:

@@ -265,6 +265,19 @@ KHRT_API int kh_gemm(const float *A, const float *B, float *C, int64_t m, int64_
 KHRT_API int kh_attention(const float *Q, const float *K, const float *V, float *O, int64_t batch,
                           int64_t heads, int64_t seq, int64_t head_dim, void *stream);
 
+/* ---- 6. Roofline microbenchmarks (bench/refs/roofline.hip:22-53,
+ *         bench/harness/roofline.cpp:60-130) ------------------------------ */
+/* c = a + b over n floats (n a multiple of 4, 16-byte aligned buffers):
+ * the measured HBM ceiling when 12 n bytes exceed the 256 MB MALL. */
+KHRT_API int kh_roofline_triad(const float *a, const float *b, float *c, int64_t n, void *stream);
+/* dst = src over n floats (n a multiple of 4, 16-byte aligned): a kernel of
+ * exactly known traffic (4n B read, 4n B written) for counter calibration. */
+KHRT_API int kh_roofline_copy(const float *src, float *dst, int64_t n, void *stream);
+/* fp32 MFMA rate: `blocks` workgroups of 256 threads each run `iters`
+ * rounds of 8 independent v_mfma_f32_32x32x2f32 per wave. FLOPs executed =
+ * blocks * 4 * iters * 8 * 4096. out needs blocks * 256 floats. */
+KHRT_API int kh_roofline_mfma(float *out, int64_t blocks, int64_t iters, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

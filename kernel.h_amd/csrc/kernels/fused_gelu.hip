@@ -18,10 +18,9 @@
 // absolute error of out is a few fp32 ulps of |t|, far inside the 1e-4
 // fp64-reference tolerance (e2e_fused_gelu_test.cpp:63).
 #include "kh_device.h"
+#include "kh_tiles.h"
 
-#ifndef KH_UNROLL
-#define KH_UNROLL 4
-#endif
+#define KH_UNROLL KH_EW_UNROLL
 
 namespace {
 
@@ -56,21 +55,21 @@ fused_gelu(KH_MEMREF1(const float, x), KH_MEMREF1(float, tmp), KH_MEMREF1(float,
   const int64_t nthreads = (int64_t)blockDim.x * gridDim.x;
 
   if (kh::aligned16(X) && kh::aligned16(O)) {
+    // Streamed once: nontemporal dwordx4 loads/stores, KH_UNROLL in flight.
     const int64_t n4 = n >> 2;
-    const float4 *__restrict__ X4 = reinterpret_cast<const float4 *>(X);
-    float4 *__restrict__ O4 = reinterpret_cast<float4 *>(O);
+    const int64_t bd = blockDim.x;
     const int64_t step = nthreads * KH_UNROLL;
-    int64_t i = (int64_t)blockIdx.x * blockDim.x * KH_UNROLL + tid;
-    for (; i + (KH_UNROLL - 1) * (int64_t)blockDim.x < n4; i += step) {
+    int64_t i = (int64_t)blockIdx.x * bd * KH_UNROLL + tid;
+    for (; i + (KH_UNROLL - 1) * bd < n4; i += step) {
       float4 v[KH_UNROLL];
 #pragma unroll
-      for (int u = 0; u < KH_UNROLL; ++u) v[u] = X4[i + u * (int64_t)blockDim.x];
+      for (int u = 0; u < KH_UNROLL; ++u) v[u] = kh::load_nt(X + 4 * (i + u * bd));
 #pragma unroll
-      for (int u = 0; u < KH_UNROLL; ++u) O4[i + u * (int64_t)blockDim.x] = gelu4(v[u]);
+      for (int u = 0; u < KH_UNROLL; ++u) kh::store_nt(O + 4 * (i + u * bd), gelu4(v[u]));
     }
     for (int u = 0; u < KH_UNROLL; ++u) {
-      const int64_t j = i + u * (int64_t)blockDim.x;
-      if (j < n4) O4[j] = gelu4(X4[j]);
+      const int64_t j = i + u * bd;
+      if (j < n4) kh::store_nt(O + 4 * j, gelu4(kh::load_nt(X + 4 * j)));
     }
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + tid;
     const int64_t t = (n4 << 2) + gid;

@@ -50,7 +50,7 @@ __device__ __forceinline__ void layernorm_rows_regs(const float *__restrict__ X,
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const int64_t c = (int64_t)(lane + j * kh::kWave) * 4;
-      v[j] = (c < cols) ? *reinterpret_cast<const float4 *>(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+      v[j] = (c < cols) ? kh::load_nt(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     float s = 0.0f;
 #pragma unroll
@@ -76,7 +76,7 @@ __device__ __forceinline__ void layernorm_rows_regs(const float *__restrict__ X,
         o.y = fmaf((v[j].y - mean) * inv, g[j].y, b[j].y);
         o.z = fmaf((v[j].z - mean) * inv, g[j].z, b[j].z);
         o.w = fmaf((v[j].w - mean) * inv, g[j].w, b[j].w);
-        *reinterpret_cast<float4 *>(yr + c) = o;
+        kh::store_nt(yr + c, o);
       }
     }
   }

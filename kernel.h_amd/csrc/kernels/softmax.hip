@@ -34,7 +34,7 @@ __device__ __forceinline__ void softmax_row_regs(const float *__restrict__ xr, f
   for (int j = 0; j < V; ++j) {
     const int64_t c = (int64_t)(lane + j * kh::kWave) * 4;
     if (c < cols) {
-      v[j] = *reinterpret_cast<const float4 *>(xr + c);
+      v[j] = kh::load_nt(xr + c);
     } else {
       v[j] = make_float4(ninf, ninf, ninf, ninf);
     }
@@ -64,7 +64,7 @@ __device__ __forceinline__ void softmax_row_regs(const float *__restrict__ xr, f
       o.y = v[j].y * inv;
       o.z = v[j].z * inv;
       o.w = v[j].w * inv;
-      *reinterpret_cast<float4 *>(yr + c) = o;
+      kh::store_nt(yr + c, o);
     }
   }
 }

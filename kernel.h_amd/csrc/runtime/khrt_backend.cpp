@@ -9,7 +9,9 @@
 #include "kernelh/khrt_internal.hpp"
 
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <unordered_map>
 
@@ -19,7 +21,13 @@ namespace {
 thread_local std::string g_error;
 int g_device = -1;
 std::mutex g_mu;
-std::unordered_map<void *, void *> g_prelude;
+struct Prelude {
+  void *function;  // kernel launched first with the same parameters
+  void *module;    // module both kernels live in
+};
+std::unordered_map<void *, Prelude> g_prelude;
+// Private copy of each loaded module's code object, keyed by module.
+std::unordered_map<void *, std::unique_ptr<unsigned char[], void (*)(void *)>> g_images;
 }  // namespace
 
 void set_error(const std::string &msg) { g_error = msg.empty() ? std::string("(unspecified error)") : msg; }
@@ -130,15 +138,15 @@ std::string check_elf_image(const unsigned char *b, size_t size) {
   return "";
 }
 
-void register_prelude(void *function, void *prelude) {
+void register_prelude(void *function, void *prelude, void *module) {
   std::lock_guard<std::mutex> lock(g_mu);
-  g_prelude[function] = prelude;
+  g_prelude[function] = Prelude{prelude, module};
 }
 
 void *prelude_for(void *function) {
   std::lock_guard<std::mutex> lock(g_mu);
   auto it = g_prelude.find(function);
-  return it == g_prelude.end() ? nullptr : it->second;
+  return it == g_prelude.end() ? nullptr : it->second.function;
 }
 
 }  // namespace khrt
@@ -270,9 +278,21 @@ int khrt_module_load_data(void **module, const void *image, size_t size) {
     return fail(KHRT_E_INVALID, "khrt_module_load_data: " + err);
   }
   if (int rc = ensure_device()) return rc;
+  // The HIP runtime may read the image after hipModuleLoadData returns
+  // (code objects are loaded lazily), so the caller's buffer must outlive
+  // the module. Keep a private copy until khrt_module_unload instead, so a
+  // caller may free its image right after this call.
+  std::unique_ptr<unsigned char[], void (*)(void *)> copy(
+      static_cast<unsigned char *>(std::aligned_alloc(4096, (size + 4095) / 4096 * 4096)), std::free);
+  if (!copy) return fail(KHRT_E_INVALID, "khrt_module_load_data: out of host memory");
+  std::memcpy(copy.get(), image, size);
   hipModule_t m = nullptr;
-  const hipError_t e = hipModuleLoadData(&m, image);
+  const hipError_t e = hipModuleLoadData(&m, copy.get());
   if (e != hipSuccess) return fail_hip(e, "hipModuleLoadData");
+  {
+    std::lock_guard<std::mutex> lock(g_mu);
+    g_images.emplace(static_cast<void *>(m), std::move(copy));
+  }
   *module = m;
   return 0;
 }
@@ -291,7 +311,7 @@ int khrt_module_get_function(void **function, void *module, const char *name) {
   if (std::strcmp(name, "scan") == 0) {
     hipFunction_t reset = nullptr;
     if (hipModuleGetFunction(&reset, static_cast<hipModule_t>(module), "scan_reset") == hipSuccess) {
-      register_prelude(f, reset);
+      register_prelude(f, reset, module);
     } else {
       (void)hipGetLastError();
     }
@@ -302,7 +322,14 @@ int khrt_module_get_function(void **function, void *module, const char *name) {
 int khrt_module_unload(void *module) {
   if (module == nullptr) return fail(KHRT_E_INVALID, "khrt_module_unload: null module");
   const hipError_t e = hipModuleUnload(static_cast<hipModule_t>(module));
-  return e == hipSuccess ? 0 : fail_hip(e, "hipModuleUnload");
+  if (e != hipSuccess) return fail_hip(e, "hipModuleUnload");
+  std::lock_guard<std::mutex> lock(g_mu);
+  g_images.erase(module);  // the private image copy goes with the module
+  for (auto it = g_prelude.begin(); it != g_prelude.end();) {
+    it = (it->second.module == module) ? g_prelude.erase(it) : std::next(it);
+  }
+  clear_occupancy_cache();
+  return 0;
 }
 
 int khrt_launch_raw(void *function, khrt_dim3 grid, khrt_dim3 block, size_t shared_bytes, void *stream,

@@ -15,8 +15,10 @@
 #include <climits>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <limits>
 #include <mutex>
+#include <unordered_map>
 
 namespace {
 
@@ -74,15 +76,41 @@ std::mutex g_live_mu;
 // Vendor occupancy API for a loaded function: blocks per CU, -1 if
 // unavailable (the reference's query_occupancy_max_blocks_runtime hook,
 // lib/runtime/query_occupancy.cpp).
+// Answers are cached per (function, block, shared): the query is a
+// few microseconds of host time, paid on every verified launch otherwise.
+// The cache is dropped whenever a module is unloaded (function handles of
+// an unloaded module may be reused).
+struct OccKey {
+  void *function;
+  int block;
+  size_t shared;
+  bool operator==(const OccKey &o) const { return function == o.function && block == o.block && shared == o.shared; }
+};
+struct OccKeyHash {
+  size_t operator()(const OccKey &k) const {
+    return std::hash<void *>()(k.function) ^ (size_t(k.block) << 20) ^ (k.shared << 1);
+  }
+};
+std::mutex g_occ_mu;
+std::unordered_map<OccKey, int, OccKeyHash> g_occ;
+
 int occupancy_blocks(void *function, int block, size_t shared) {
   if (function == nullptr || block <= 0) return -1;
+  const OccKey key{function, block, shared};
+  {
+    std::lock_guard<std::mutex> lock(g_occ_mu);
+    auto it = g_occ.find(key);
+    if (it != g_occ.end()) return it->second;
+  }
   int blocks = 0;
   const hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(
       &blocks, static_cast<hipFunction_t>(function), block, shared);
   if (e != hipSuccess) {
     (void)hipGetLastError();
-    return -1;
+    blocks = -1;
   }
+  std::lock_guard<std::mutex> lock(g_occ_mu);
+  g_occ[key] = blocks;
   return blocks;
 }
 
@@ -173,6 +201,11 @@ int resolve_live(khrt_device_limits *out) {
 }  // namespace
 
 namespace khrt {
+
+void clear_occupancy_cache() {
+  std::lock_guard<std::mutex> lock(g_occ_mu);
+  g_occ.clear();
+}
 
 int verified_launch(void *function, khrt_dim3 grid, khrt_dim3 block, size_t shared, void *stream, void **params,
                     size_t nparams) {

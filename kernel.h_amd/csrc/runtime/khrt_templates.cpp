@@ -30,6 +30,7 @@ KH_DECLARE_CO(scan)
 KH_DECLARE_CO(gemm)
 KH_DECLARE_CO(attention)
 KH_DECLARE_CO(util)
+KH_DECLARE_CO(roofline)
 
 namespace {
 
@@ -44,6 +45,7 @@ const CodeObject kCodeObjects[] = {
     {"softmax", kh_co_softmax, kh_co_softmax_end},    {"layernorm", kh_co_layernorm, kh_co_layernorm_end},
     {"scan", kh_co_scan, kh_co_scan_end},             {"gemm", kh_co_gemm, kh_co_gemm_end},
     {"attention", kh_co_attention, kh_co_attention_end}, {"util", kh_co_util, kh_co_util_end},
+    {"roofline", kh_co_roofline, kh_co_roofline_end},
 };
 
 struct KernelResources {
@@ -393,6 +395,51 @@ int kh_attention(const float *Q, const float *K, const float *V, float *O, int64
   args.add_memref(O, {batch, heads, seq, head_dim});
   return launch_template("attention", args,
                          {{"batch", batch}, {"heads", heads}, {"seq", seq}, {"head_dim", head_dim}}, stream);
+}
+
+// Streaming roofline kernels: 32 workgroups of 256 per CU, grid-strided.
+static int launch_stream_roofline(const char *symbol, khrt::LaunchArgs &args, void *stream) {
+  void *fn = nullptr;
+  if (int rc = get_function("roofline", symbol, &fn)) return rc;
+  khrt_device_limits live;
+  if (int rc = khrt_live_limits(&live)) return rc;
+  const unsigned grid = static_cast<unsigned>(std::max<int64_t>(1, live.cu_count) * 32);
+  return khrt::verified_launch(fn, khrt_dim3{grid, 1, 1}, khrt_dim3{256, 1, 1}, 0, stream, args.params(), args.count());
+}
+
+static bool vec_ok(const void *p, int64_t n) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0 && n > 0 && (n & 3) == 0;
+}
+
+int kh_roofline_triad(const float *a, const float *b, float *c, int64_t n, void *stream) {
+  if (!a || !b || !c) return bad("roofline_triad: null buffer");
+  if (!vec_ok(a, n) || !vec_ok(b, n) || !vec_ok(c, n)) return bad("roofline_triad: n % 4 == 0 and 16-byte alignment required");
+  khrt::LaunchArgs args;
+  args.add_memref(a, {n});
+  args.add_memref(b, {n});
+  args.add_memref(c, {n});
+  return launch_stream_roofline("roofline_triad", args, stream);
+}
+
+int kh_roofline_copy(const float *src, float *dst, int64_t n, void *stream) {
+  if (!src || !dst) return bad("roofline_copy: null buffer");
+  if (!vec_ok(src, n) || !vec_ok(dst, n)) return bad("roofline_copy: n % 4 == 0 and 16-byte alignment required");
+  khrt::LaunchArgs args;
+  args.add_memref(src, {n});
+  args.add_memref(dst, {n});
+  return launch_stream_roofline("roofline_copy", args, stream);
+}
+
+int kh_roofline_mfma(float *out, int64_t blocks, int64_t iters, void *stream) {
+  if (!out) return bad("roofline_mfma: null buffer");
+  if (blocks <= 0 || blocks > (1 << 20) || iters <= 0) return bad("roofline_mfma: blocks in [1, 2^20], iters > 0");
+  void *fn = nullptr;
+  if (int rc = get_function("roofline", "roofline_mfma", &fn)) return rc;
+  khrt::LaunchArgs args;
+  args.add_memref(out, {blocks * 256});
+  args.add_scalar_bytes(&iters, sizeof(iters));
+  return khrt::verified_launch(fn, khrt_dim3{static_cast<unsigned>(blocks), 1, 1}, khrt_dim3{256, 1, 1}, 0, stream,
+                               args.params(), args.count());
 }
 
 }  // extern "C"

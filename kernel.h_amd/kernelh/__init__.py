@@ -149,6 +149,9 @@ SIGNATURES = {
     "kh_scan_totals": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
     "kh_gemm": (_i, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "kh_attention": (_i, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "kh_roofline_triad": (_i, [_vp, _vp, _vp, _i64, _vp]),
+    "kh_roofline_copy": (_i, [_vp, _vp, _i64, _vp]),
+    "kh_roofline_mfma": (_i, [_vp, _i64, _i64, _vp]),
 }
 
 
@@ -256,13 +259,23 @@ class Buffer:
 
 
 class GpuModule:
-    """Loaded code object (gpu_module.hpp): hipModuleLoadData / GetFunction."""
+    """Loaded code object (gpu_module.hpp): hipModuleLoadData / GetFunction.
+    The runtime keeps its own copy of the image; the module is unloaded when
+    this object is (RAII, as GpuModule's destructor in the reference)."""
 
     def __init__(self, image: bytes):
-        self._image = ctypes.create_string_buffer(image, len(image))
+        self.handle = None
+        buf = ctypes.create_string_buffer(image, len(image))
         m = ctypes.c_void_p()
-        check(lib.khrt_module_load_data(ctypes.byref(m), ctypes.addressof(self._image), len(image)))
+        check(lib.khrt_module_load_data(ctypes.byref(m), ctypes.addressof(buf), len(image)))
         self.handle = m.value
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib.khrt_module_unload(self.handle)
+        except Exception:
+            pass
 
     def get_function(self, name: str) -> int:
         f = ctypes.c_void_p()
@@ -456,6 +469,20 @@ def gemm(A, B, C, m: int, n: int, k: int, stream=None) -> None:
 
 def attention(Q, K, V, O, batch: int, heads: int, seq: int, head_dim: int, stream=None) -> None:
     check(lib.kh_attention(_ptr(Q), _ptr(K), _ptr(V), _ptr(O), batch, heads, seq, head_dim, _ptr(stream)))
+
+
+def roofline_triad(a, b, c, n: int, stream=None) -> None:
+    check(lib.kh_roofline_triad(_ptr(a), _ptr(b), _ptr(c), n, _ptr(stream)))
+
+
+def roofline_copy(src, dst, n: int, stream=None) -> None:
+    check(lib.kh_roofline_copy(_ptr(src), _ptr(dst), n, _ptr(stream)))
+
+
+def roofline_mfma(out, blocks: int, iters: int, stream=None) -> float:
+    """Launches the MFMA microbenchmark; returns the FLOPs it executes."""
+    check(lib.kh_roofline_mfma(_ptr(out), blocks, iters, _ptr(stream)))
+    return float(blocks) * 4 * iters * 8 * 4096
 
 
 def scan_workspace_floats(n: int) -> int:

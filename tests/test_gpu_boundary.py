@@ -68,12 +68,36 @@ def test_reference_raw_protocol_vecadd(dev):
     n = 65536 + 3
     a, b = O.vecadd_inputs(n)
     da, db, dc = up(a), up(b), empty(n)
-    f = kh.GpuModule(kh.code_object("vecadd")).get_function("vecadd")
+    m = kh.GpuModule(kh.code_object("vecadd"))  # kept alive while f is used
+    f = m.get_function("vecadd")
     args = kh.LaunchArgs().add_memref(da, [n]).add_memref(db, [n]).add_memref(dc, [n])
     assert args.param_count() == 15
     say("raw vecadd reference geometry")
     kh.kernel_launch(f, ((n + 255) // 256, 1, 1), (256, 1, 1), args)
     assert np.array_equal(down(dc, n), O.ref_vecadd(a, b))
+
+
+def test_module_outlives_caller_image_buffer(dev):
+    # The runtime copies the image: the caller's buffer may be freed and
+    # overwritten right after the load (regression test for a freed image
+    # being read by the HIP runtime after hipModuleLoadData).
+    import ctypes
+    blob = kh.code_object("vecadd")
+    buf = ctypes.create_string_buffer(blob, len(blob))
+    h = ctypes.c_void_p()
+    kh.check(kh.lib.khrt_module_load_data(ctypes.byref(h), ctypes.addressof(buf), len(blob)))
+    ctypes.memset(buf, 0xAB, len(blob))
+    del buf
+    f = ctypes.c_void_p()
+    kh.check(kh.lib.khrt_module_get_function(ctypes.byref(f), h, b"vecadd"))
+    n = 4096
+    a, b = O.vecadd_inputs(n)
+    da, db, dc = up(a), up(b), empty(n)
+    args = kh.LaunchArgs().add_memref(da, [n]).add_memref(db, [n]).add_memref(dc, [n])
+    say("vecadd from a module whose caller image was overwritten")
+    kh.kernel_launch(f.value, (16, 1, 1), (256, 1, 1), args)
+    assert np.array_equal(down(dc, n), O.ref_vecadd(a, b))
+    kh.check(kh.lib.khrt_module_unload(h))
 
 
 def test_events_time_a_launch(dev):
