@@ -39,6 +39,14 @@ ROTATE_BYTES = 1 << 30  # rotate buffer sets until the working set exceeds 1 GiB
 
 METRIC = "GEMM-8192 fp32 TFLOPS + softmax/scan HBM GB/s, % of MI355X roofline"
 
+# HBM bytes per launch from two rocprofv3 --pmc passes (FETCH_SIZE scaled by
+# 2.000 and WRITE_SIZE by 1.000, the factors a copy kernel of known size
+# reads), recorded in profiles/templates_baseline_sizes_hbm_traffic.md.
+PMC_TRAFFIC_BYTES = {
+    "vecadd": 201361158, "softmax": 33630353, "layernorm": 33709000, "scan": 539694765,
+    "fused_gelu": 537445000, "gemm": 7050662585, "attention": 1208055525,
+}
+
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
@@ -291,6 +299,8 @@ def main() -> int:
             meas = ceilings["fp32_mfma_tflops"] if c.bound == "mfma" else ceilings["hbm_triad_gbps"]
             kernels[c.name]["measured_ceiling"] = meas
             kernels[c.name]["frac_of_measured"] = rate / meas
+        if c.name in PMC_TRAFFIC_BYTES:
+            kernels[c.name]["traffic_bytes_pmc"] = PMC_TRAFFIC_BYTES[c.name]
         if c.traffic_note:
             kernels[c.name]["note"] = c.traffic_note
         log(f"[bench] {c.name:10s} {ms:9.4f} ms  {rate:9.1f} {c.unit}  ({100 * rate / peak:5.1f}% of peak"
@@ -314,7 +324,7 @@ def main() -> int:
                    "buffer_rotation": not a.no_rotate},
         "roofline": None if not hk else {
             "bound": hk["bound"], "achieved": hk["rate"], "peak": hk["peak"],
-            "unit": hk["unit"], "frac": hk["frac"], "traffic": None, "kernel": head},
+            "unit": hk["unit"], "frac": hk["frac"], "traffic": PMC_TRAFFIC_BYTES.get(head), "kernel": head},
         "kernels": kernels,
         "measured_ceilings": ceilings,
         "device": {"name": info["name"], "arch": info["arch"], "cu_count": info["cu_count"]},
