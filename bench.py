@@ -170,34 +170,53 @@ def set_bytes(sets):
     return sum(b.nbytes for b in sets)
 
 
+def _gemm_rows_rate(O, A, B, M, threads, budget_s):
+    """Grows a row sample of the 8192^3 fp64 GEMM reference until it has run
+    for about budget_s seconds; returns (TFLOP/s, rows, seconds)."""
+    O.set_threads(threads)
+    done, dt, rows = 0, 0.0, max(threads, 2)
+    while dt < budget_s and done < M:
+        rows = min(rows, M - done)
+        t = time.perf_counter()
+        O.ref_gemm(A, B, M, M, M, row0=done, nrows=rows)
+        dt += time.perf_counter() - t
+        done += rows
+        rows = max(rows, int(rows * min(4.0, 0.9 * (budget_s - dt) / max(time.perf_counter() - t, 1e-3))))
+    return 2.0 * done * M * M / dt / 1e12, done, dt
+
+
 def cpu_baseline(budget_s: float):
-    """Times the oracle's fp64 GEMM reference (the CPU restatement of
-    e2e_gemm_test.cpp:92-110) on a row sample of the 8192^3 problem, on all
-    host cores via OpenMP. Reported in TFLOP/s like `value`."""
+    """The oracle's fp64 references (CPU restatements of the reference's
+    e2e checks) timed on this host: the GEMM reference (e2e_gemm_test.cpp:
+    92-110) on a row sample of the 8192^3 problem on all cores via OpenMP
+    (the headline, in `value`'s unit) and on one core, plus all-core rates
+    of the softmax and scan references at the BASELINE sizes."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle as O
     cores = len(os.sched_getaffinity(0))
-    O.set_threads(cores)
     M = 8192
     rng = np.random.default_rng(7)
-    A = u24(rng, 64 * M, -1, 1)  # only the sampled rows of A are touched
+    A = u24(rng, M * M, -1, 1)
     B = u24(rng, M * M, -1, 1)
-    rows = max(cores, 8)
-    t0 = time.perf_counter()
-    O.ref_gemm(A, B, 64, M, M, row0=0, nrows=min(rows, 64))
-    dt = time.perf_counter() - t0
-    done = min(rows, 64)
-    # Grow the sample to fill the budget (at most 64 rows of A available).
-    while dt < budget_s and done < 64:
-        extra = min(64 - done, max(1, int(done * (budget_s / max(dt, 1e-3) - 1))))
-        t1 = time.perf_counter()
-        O.ref_gemm(A, B, 64, M, M, row0=done, nrows=extra)
-        dt += time.perf_counter() - t1
-        done += extra
-    tflops = 2.0 * done * M * M / dt / 1e12
-    return {"value": tflops, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"fp64 rank-1 GEMM reference (oracle kho_ref_gemm), {done} of 8192 rows of the "
-                      f"8192^3 problem, {dt:.1f} s on {cores} threads"}
+    tf_all, rows_all, s_all = _gemm_rows_rate(O, A, B, M, cores, 0.6 * budget_s)
+    tf_one, rows_one, s_one = _gemm_rows_rate(O, A, B, M, 1, 0.25 * budget_s)
+    del A, B
+    O.set_threads(cores)
+    x = (rng.standard_normal(4096 * 1024) * 4.0).astype(np.float32)
+    t = time.perf_counter()
+    O.ref_softmax(x, 4096, 1024)
+    sm = 8.0 * x.size / (time.perf_counter() - t) / 1e9
+    xs = u24(rng, 1 << 26, 0, 1)
+    t = time.perf_counter()
+    O.ref_scan(xs)
+    sc = 8.0 * xs.size / (time.perf_counter() - t) / 1e9
+    return {"value": tf_all, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"fp64 rank-1 GEMM reference (oracle kho_ref_gemm): {rows_all} of 8192 rows of the "
+                      f"8192^3 problem in {s_all:.1f} s on {cores} threads",
+            "single_thread": {"value": tf_one, "unit": "TFLOP/s", "cores": 1,
+                              "sample": f"{rows_one} rows in {s_one:.1f} s"},
+            "other_kernels": {"softmax_4096x1024_gbps": sm, "scan_2^26_gbps_single_thread": sc,
+                              "note": "fp64 references, same inputs as the GPU rows; scan is serial"}}
 
 
 def main() -> int:
