@@ -7,8 +7,8 @@
 // template pins them (mean first, then the mean of squared deviations; no
 // Welford), but the row is read from HBM once: one wavefront holds the row
 // in registers (dwordx4 loads), so the second pass runs on registers. gamma
-// and beta are loaded once per wavefront and reused for every row it
-// normalises. Traffic: 8 B per element + 8 B per column.
+// and beta are read per row from L2 (every row shares them, so HBM sees them
+// once). Traffic: 8 B per element + 8 B per column.
 //
 // Wider rows than the register path, unaligned or odd-width rows take a
 // streaming form with the same two-pass statistics (the row is re-read from
@@ -18,30 +18,21 @@
 #include "kh_device.h"
 
 #ifndef KH_LN_MAXV
-#define KH_LN_MAXV 8
+#define KH_LN_MAXV 16  // float4 per lane on the register path: cols <= 4096
 #endif
 
 namespace {
 
 constexpr float kEps = 1e-5f;
 
+// gamma and beta are re-read per row from L2 (cols x 8 B, shared by every
+// row) rather than held in registers: holding them doubled the register
+// footprint and halved the number of rows in flight.
 template <int V>
 __device__ __forceinline__ void layernorm_rows_regs(const float *__restrict__ X, const float *__restrict__ G,
                                                     const float *__restrict__ B, float *__restrict__ Y,
                                                     int64_t rows, int64_t cols, int64_t xs, int64_t ys,
                                                     int64_t r0, int64_t rstep, int lane) {
-  float4 g[V], b[V];
-#pragma unroll
-  for (int j = 0; j < V; ++j) {
-    const int64_t c = (int64_t)(lane + j * kh::kWave) * 4;
-    if (c < cols) {
-      g[j] = *reinterpret_cast<const float4 *>(G + c);
-      b[j] = *reinterpret_cast<const float4 *>(B + c);
-    } else {
-      g[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-      b[j] = g[j];
-    }
-  }
   const float inv_cols = 1.0f / (float)cols;
   for (int64_t r = r0; r < rows; r += rstep) {
     const float *xr = X + r * xs;
@@ -71,11 +62,13 @@ __device__ __forceinline__ void layernorm_rows_regs(const float *__restrict__ X,
     for (int j = 0; j < V; ++j) {
       const int64_t c = (int64_t)(lane + j * kh::kWave) * 4;
       if (c < cols) {
+        const float4 g = *reinterpret_cast<const float4 *>(G + c);
+        const float4 b = *reinterpret_cast<const float4 *>(B + c);
         float4 o;
-        o.x = fmaf((v[j].x - mean) * inv, g[j].x, b[j].x);
-        o.y = fmaf((v[j].y - mean) * inv, g[j].y, b[j].y);
-        o.z = fmaf((v[j].z - mean) * inv, g[j].z, b[j].z);
-        o.w = fmaf((v[j].w - mean) * inv, g[j].w, b[j].w);
+        o.x = fmaf((v[j].x - mean) * inv, g.x, b.x);
+        o.y = fmaf((v[j].y - mean) * inv, g.y, b.y);
+        o.z = fmaf((v[j].z - mean) * inv, g.z, b.z);
+        o.w = fmaf((v[j].w - mean) * inv, g.w, b.w);
         kh::store_nt(yr + c, o);
       }
     }
@@ -98,34 +91,48 @@ __device__ __forceinline__ void layernorm_row_stream(const float *__restrict__ x
   for (int64_t c = lane; c < cols; c += kh::kWave) yr[c] = fmaf((xr[c] - mean) * inv, G[c], B[c]);
 }
 
-}  // namespace
-
-extern "C" __global__ void __launch_bounds__(256)
-layernorm(KH_MEMREF2(const float, x), KH_MEMREF1(const float, gamma), KH_MEMREF1(const float, beta),
-          KH_MEMREF2(float, y)) {
-  const float *__restrict__ X = KH_PTR(x);
-  const float *__restrict__ G = KH_PTR(gamma);
-  const float *__restrict__ B = KH_PTR(beta);
-  float *__restrict__ Y = KH_PTR(y);
-  const int64_t rows = x_n0, cols = x_n1;
-  const int64_t xs = x_s0, ys = y_s0;
+// Shared by both symbols; WIDE selects the register-path widths compiled in
+// (the kernel's register allocation is that of its widest path).
+template <bool WIDE>
+__device__ __forceinline__ void layernorm_all(const float *__restrict__ X, const float *__restrict__ G,
+                                              const float *__restrict__ B, float *__restrict__ Y, int64_t rows,
+                                              int64_t cols, int64_t xs, int64_t ys) {
   const int lane = kh::lane_id();
   const int64_t waves_per_block = blockDim.x / kh::kWave;
   const int64_t r0 = blockIdx.x * waves_per_block + threadIdx.x / kh::kWave;
   const int64_t rstep = waves_per_block * gridDim.x;
-
   const bool vec = ((cols & 3) == 0) && ((xs & 3) == 0) && ((ys & 3) == 0) && kh::aligned16(X) &&
                    kh::aligned16(Y) && kh::aligned16(G) && kh::aligned16(B);
   const int64_t v4 = (cols + 255) / 256;
-  if (vec && v4 <= 1) {
+  if (!WIDE && vec && v4 <= 1) {
     layernorm_rows_regs<1>(X, G, B, Y, rows, cols, xs, ys, r0, rstep, lane);
-  } else if (vec && v4 <= 2) {
+  } else if (!WIDE && vec && v4 <= 2) {
     layernorm_rows_regs<2>(X, G, B, Y, rows, cols, xs, ys, r0, rstep, lane);
-  } else if (vec && v4 <= 4) {
+  } else if (!WIDE && vec && v4 <= 4) {
     layernorm_rows_regs<4>(X, G, B, Y, rows, cols, xs, ys, r0, rstep, lane);
-  } else if (vec && v4 <= KH_LN_MAXV) {
+  } else if (WIDE && vec && v4 <= 8) {
+    layernorm_rows_regs<8>(X, G, B, Y, rows, cols, xs, ys, r0, rstep, lane);
+  } else if (WIDE && vec && v4 <= KH_LN_MAXV) {
     layernorm_rows_regs<KH_LN_MAXV>(X, G, B, Y, rows, cols, xs, ys, r0, rstep, lane);
   } else {
     for (int64_t r = r0; r < rows; r += rstep) layernorm_row_stream(X + r * xs, G, B, Y + r * ys, cols, lane);
   }
+}
+
+}  // namespace
+
+// The reference symbol: register path for rows up to 1024 floats, any other
+// shape through the streaming path.
+extern "C" __global__ void __launch_bounds__(256)
+layernorm(KH_MEMREF2(const float, x), KH_MEMREF1(const float, gamma), KH_MEMREF1(const float, beta),
+          KH_MEMREF2(float, y)) {
+  layernorm_all<false>(KH_PTR(x), KH_PTR(gamma), KH_PTR(beta), KH_PTR(y), x_n0, x_n1, x_s0, y_s0);
+}
+
+// Same arguments and results; register path for rows of 1025..4096 floats
+// (the launcher picks it for those widths).
+extern "C" __global__ void __launch_bounds__(256)
+layernorm_wide(KH_MEMREF2(const float, x), KH_MEMREF1(const float, gamma), KH_MEMREF1(const float, beta),
+               KH_MEMREF2(float, y)) {
+  layernorm_all<true>(KH_PTR(x), KH_PTR(gamma), KH_PTR(beta), KH_PTR(y), x_n0, x_n1, x_s0, y_s0);
 }

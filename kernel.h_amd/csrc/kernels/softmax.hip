@@ -20,7 +20,7 @@
 #include "kh_device.h"
 
 #ifndef KH_SM_MAXV
-#define KH_SM_MAXV 8  // float4 per lane on the register path: cols <= 2048
+#define KH_SM_MAXV 16  // float4 per lane on the register path: cols <= 4096
 #endif
 
 namespace {
@@ -89,35 +89,50 @@ __device__ __forceinline__ void softmax_row_stream(const float *__restrict__ xr,
   for (int64_t c = lane; c < cols; c += kh::kWave) yr[c] = kh::exp2_hw(fmaf(xr[c], kh::kLog2e, mb)) * inv;
 }
 
-}  // namespace
-
-extern "C" __global__ void __launch_bounds__(256)
-softmax(KH_MEMREF2(const float, x), KH_MEMREF2(float, y)) {
-  const float *__restrict__ X = KH_PTR(x);
-  float *__restrict__ Y = KH_PTR(y);
-  const int64_t rows = x_n0, cols = x_n1;
-  const int64_t xs = x_s0, ys = y_s0;
+// Row loop shared by both symbols. WIDE selects which register-path widths
+// are compiled in: the kernel's register allocation is that of its widest
+// path, so the narrow symbol stays lean (more rows in flight per CU).
+template <bool WIDE>
+__device__ __forceinline__ void softmax_rows(const float *__restrict__ X, float *__restrict__ Y, int64_t rows,
+                                             int64_t cols, int64_t xs, int64_t ys) {
   const int lane = kh::lane_id();
   const int64_t waves_per_block = blockDim.x / kh::kWave;
   const int64_t wave = threadIdx.x / kh::kWave;
   const int64_t nwaves = waves_per_block * gridDim.x;
-
   const bool vec = ((cols & 3) == 0) && ((xs & 3) == 0) && ((ys & 3) == 0) && kh::aligned16(X) &&
                    kh::aligned16(Y);
   const int64_t v4 = (cols + 255) / 256;  // float4 per lane needed
   for (int64_t r = blockIdx.x * waves_per_block + wave; r < rows; r += nwaves) {
     const float *xr = X + r * xs;
     float *yr = Y + r * ys;
-    if (vec && v4 <= 1) {
+    if (!WIDE && vec && v4 <= 1) {
       softmax_row_regs<1>(xr, yr, cols, lane);
-    } else if (vec && v4 <= 2) {
+    } else if (!WIDE && vec && v4 <= 2) {
       softmax_row_regs<2>(xr, yr, cols, lane);
-    } else if (vec && v4 <= 4) {
+    } else if (!WIDE && vec && v4 <= 4) {
       softmax_row_regs<4>(xr, yr, cols, lane);
-    } else if (vec && v4 <= KH_SM_MAXV) {
+    } else if (WIDE && vec && v4 <= 8) {
+      softmax_row_regs<8>(xr, yr, cols, lane);
+    } else if (WIDE && vec && v4 <= KH_SM_MAXV) {
       softmax_row_regs<KH_SM_MAXV>(xr, yr, cols, lane);
     } else {
       softmax_row_stream(xr, yr, cols, lane);
     }
   }
+}
+
+}  // namespace
+
+// The reference symbol: register path for rows up to 1024 floats, any other
+// shape through the streaming path.
+extern "C" __global__ void __launch_bounds__(256)
+softmax(KH_MEMREF2(const float, x), KH_MEMREF2(float, y)) {
+  softmax_rows<false>(KH_PTR(x), KH_PTR(y), x_n0, x_n1, x_s0, y_s0);
+}
+
+// Same arguments and results; register path for rows of 1025..4096 floats
+// (the launcher picks it for those widths).
+extern "C" __global__ void __launch_bounds__(256)
+softmax_wide(KH_MEMREF2(const float, x), KH_MEMREF2(float, y)) {
+  softmax_rows<true>(KH_PTR(x), KH_PTR(y), x_n0, x_n1, x_s0, y_s0);
 }

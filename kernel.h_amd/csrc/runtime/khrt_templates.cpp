@@ -209,6 +209,21 @@ int geometry(const char *name, const Shape &s, khrt_dim3 &grid, khrt_dim3 &block
   return 0;
 }
 
+// Symbol the launcher runs for a template at a shape. Every symbol of a
+// template takes the same arguments and computes the same result; the
+// variants differ in which register paths they compile in (softmax and
+// layernorm rows of 1025..4096 floats use the *_wide variant).
+const char *launch_symbol(const Template *t, const Shape &s) {
+  const std::string n = t->name;
+  if (n == "softmax" || n == "layernorm") {
+    auto it = s.find("cols");
+    if (it != s.end() && it->second > 1024 && it->second <= 4096 && (it->second & 3) == 0) {
+      return n == "softmax" ? "softmax_wide" : "layernorm_wide";
+    }
+  }
+  return t->name;
+}
+
 // Packs, verifies and launches template `name`.
 int launch_template(const char *name, khrt::LaunchArgs &args, const Shape &shape, void *stream) {
   const Template *t = find_template(name);
@@ -216,7 +231,7 @@ int launch_template(const char *name, khrt::LaunchArgs &args, const Shape &shape
   khrt_dim3 grid, block;
   if (int rc = geometry(name, shape, grid, block)) return rc;
   void *fn = nullptr;
-  if (int rc = get_function(t->co, t->name, &fn)) return rc;
+  if (int rc = get_function(t->co, launch_symbol(t, shape), &fn)) return rc;
   if (std::strcmp(name, "scan") == 0) {
     // The look-back scan is persistent: one resident wave of workgroups
     // loops over tiles, so launch no more workgroups than fit at once.

@@ -72,6 +72,32 @@ def test_softmax_reference_geometry(dev):
     assert np.max(np.abs(down(dy, rows * cols).reshape(rows, cols) - O.ref_softmax(x, rows, cols))) <= 1e-4
 
 
+@pytest.mark.parametrize("symbol", ["softmax", "softmax_wide", "layernorm", "layernorm_wide"])
+@pytest.mark.parametrize("cols", [256, 1000, 1024, 2048, 4096, 5000])
+def test_every_row_symbol_at_every_width(dev, symbol, cols):
+    # Each symbol of a template computes the same result at every width (the
+    # launcher picks one by width; raw callers may launch either).
+    rows = 37
+    x, seed = O.lcg_fill(rows * cols, 0x27AB13)
+    g, seed = O.lcg_fill(cols, seed)
+    b, seed = O.lcg_fill(cols, seed)
+    m = kh.GpuModule(kh.code_object(symbol.split("_")[0]))
+    f = m.get_function(symbol)
+    dx, dy = up(x), empty(rows * cols)
+    args = kh.LaunchArgs().add_memref(dx, [rows, cols])
+    if symbol.startswith("layernorm"):
+        dg, db = up(g), up(b)
+        args.add_memref(dg, [cols]).add_memref(db, [cols])
+        ref = O.ref_layernorm(x, g, b, rows, cols)
+    else:
+        ref = O.ref_softmax(x, rows, cols)
+    args.add_memref(dy, [rows, cols])
+    say(f"{symbol} rows={rows} cols={cols}")
+    kh.kernel_launch(f, (5, 1, 1), (256, 1, 1), args)
+    got = down(dy, rows * cols).reshape(rows, cols)
+    assert np.max(np.abs(got - ref)) <= 1e-4
+
+
 def _layernorm(x, g, b, rows, cols):
     dx, dg, db, dy = up(x), up(g), up(b), empty(rows * cols)
     say(f"layernorm {rows}x{cols}")
