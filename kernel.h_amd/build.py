@@ -52,6 +52,14 @@ DEVICE_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", KDIR,
 ]
+# Per-code-object additions. scan: the atomic optimizer rewrites the ticket
+# atomicAdd into a wave-reduced form whose result is read back at once,
+# which makes the wave wait for the atomic (and every older memory operation)
+# right where it is issued; the plain atomic's result is first waited on at
+# the barrier that publishes it.
+EXTRA_DEVICE_FLAGS = {
+    "scan": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+}
 HOST_FLAGS = [
     "-O2", "-g", "-fPIC", "-std=c++20", "-Wall", "-Wextra", "-fvisibility=hidden",
     "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f"-I{REPO}/include",
@@ -74,7 +82,7 @@ def run(cmd, verbose=False, **kw):
 def compile_co(name: str, verbose: bool) -> str:
     src = os.path.join(KDIR, name + ".hip")
     out = os.path.join(CO, name + ".hsaco")
-    run([HIPCC, *DEVICE_FLAGS, "-c", src, "-o", out], verbose)
+    run([HIPCC, *DEVICE_FLAGS, *EXTRA_DEVICE_FLAGS.get(name, []), "-c", src, "-o", out], verbose)
     isa = run([OBJDUMP, "-d", f"--mcpu={ARCH}", out])
     with open(os.path.join(CO, name + ".isa"), "w") as f:
         f.write(isa)

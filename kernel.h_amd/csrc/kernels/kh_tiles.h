@@ -7,10 +7,17 @@
 // grid-stride step.
 #define KH_EW_UNROLL 4
 
-// Scan: workgroup size chosen by the launcher (the kernel accepts 256..1024);
-// each thread owns 16 elements, so a tile is 16 x KH_SCAN_THREADS elements.
+// Scan: workgroup size chosen by the launcher (the kernel accepts 256..1024).
+// One wave of each workgroup runs the look-back; every other thread owns
+// KH_SCAN_PER_THREAD consecutive elements, so a tile is
+// KH_SCAN_PER_THREAD x (threads - 64) elements.
+#ifndef KH_SCAN_PER_THREAD
+#define KH_SCAN_PER_THREAD 16
+#endif
 #define KH_SCAN_THREADS 1024
-#define KH_SCAN_TILE (16 * KH_SCAN_THREADS)
+#define KH_SCAN_TILE (KH_SCAN_PER_THREAD * (KH_SCAN_THREADS - 64))
+// Smallest tile any accepted launch uses (256 threads); sizes the state.
+#define KH_SCAN_MIN_TILE (KH_SCAN_PER_THREAD * (256 - 64))
 
 // GEMM block tile (rows of C x columns of C per workgroup of 256 threads).
 #define KH_GEMM_BM 128

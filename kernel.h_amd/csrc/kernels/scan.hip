@@ -9,15 +9,16 @@
 // (scan.cpp:400-452). Here `scan` alone produces the final y in one pass over
 // HBM (read x once, write y once: 8 B/element):
 //
-//   * A workgroup of W threads (256..1024, a multiple of 64) owns a tile of
-//     16 W elements (16 consecutive per thread, four dwordx4 loads). Tiles
-//     are handed out in order by an atomic ticket, so a tile only ever waits
-//     on tiles already owned by running workgroups (deadlock-free under any
-//     grid size).
-//   * Workgroups are persistent and pipelined: while a tile's prefix is
-//     being looked up, the workgroup already holds the ticket for its next
-//     tile and that tile's loads are in flight, so HBM latency overlaps the
-//     look-back.
+//   * A workgroup of W threads (256..1024, a multiple of 64) has W/64 - 1
+//     data waves and one control wave. The data waves own a tile of
+//     P (W - 64) elements (P = KH_SCAN_PER_THREAD consecutive per thread,
+//     dwordx4 loads); the control wave takes tickets and does the look-back.
+//     Tiles are handed out in order by an atomic ticket, so a tile only ever
+//     waits on tiles already owned by running workgroups (deadlock-free under
+//     any grid size).
+//   * Workgroups are persistent and pipelined: the data waves issue the next
+//     tile's loads before the current tile's look-back, and tickets run two
+//     ahead, so load, ticket and look-back latencies overlap.
 //   * Partial sums are carried in fp64. Every fp32 input is exact in fp64
 //     and, for inputs on a common 2^-e grid whose total needs <= 53 bits
 //     (every configuration the reference tests: U[0,1) on 2^-24 or
@@ -26,8 +27,8 @@
 //     template computes with double-float + 3-word expansions
 //     (scan.cpp:25-38).
 //   * Decoupled look-back (Merrill & Garland 2016): each tile publishes its
-//     aggregate as soon as it is reduced, then its inclusive prefix. Wave 0
-//     of a tile inspects 256 predecessors per step (four per lane, loads
+//     aggregate as soon as it is reduced, then its inclusive prefix. The
+//     control wave inspects 64 KH_SCAN_WINDOW predecessors per step (loads
 //     issued together) and stops at the nearest inclusive prefix.
 //
 // Look-back state lives in the caller's totals buffers (the reference ABI
@@ -41,7 +42,7 @@
 // and what was published. Slots are written and polled with relaxed
 // agent-scope atomics (coherent across the 8 XCD L2s without the L2
 // write-back/invalidate an acquire/release pair would cost on every poll).
-// Capacity: tiles of >= 4096 elements need 16 B each in totals_hi
+// Capacity: tiles of >= 192 P elements need 16 B each in totals_hi
 // (T = ceil(n/256) floats); the kernel refuses (y := NaN) anything else.
 // `scan_reset` (same code object) clears the ticket and marks every slot
 // empty; the runtime launches it first, in stream order, before every
@@ -51,14 +52,18 @@
 // result with NaN and records the failure in the ticket word's top bit, so a
 // corrupted state can never hang the device.
 #include "kh_device.h"
+#include "kh_tiles.h"
 
 namespace {
 
-constexpr int kMaxThreads = 1024;
+constexpr int kMaxThreads = KH_SCAN_THREADS;
 constexpr int kMinThreads = 256;
-constexpr int kPerThread = 16;
-constexpr int kMinTile = kMinThreads * kPerThread;  // 4096: sizes the state
-constexpr int kWindow = 4;  // predecessors polled per lane per look-back step
+constexpr int kPerThread = KH_SCAN_PER_THREAD;
+constexpr int kMinTile = KH_SCAN_MIN_TILE;  // 256 threads: sizes the look-back state
+#ifndef KH_SCAN_WINDOW
+#define KH_SCAN_WINDOW 4
+#endif
+constexpr int kWindow = KH_SCAN_WINDOW;  // predecessors polled per lane per look-back step
 constexpr uint32_t kSpinLimit = 1u << 22;
 constexpr uint32_t kFailBit = 0x80000000u;
 constexpr uint64_t kEmpty = ~0ull;
@@ -77,43 +82,81 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
   return v;
 }
 
-// Inclusive wave scan (Hillis-Steele over 64 lanes).
-__device__ __forceinline__ double wave_incl_scan_f64(double v, int lane) {
-#pragma unroll
-  for (int off = 1; off < kh::kWave; off <<= 1) {
-    const double u = __shfl_up(v, off, kh::kWave);
-    if (lane >= off) v += u;
-  }
-  return v;
+// DPP move of an fp64 value (two 32-bit halves, same control). Lanes the
+// control does not write (row_mask) or that have no source (bound_ctrl) get 0.
+template <int CTRL, int ROW_MASK, bool BOUND_CTRL>
+__device__ __forceinline__ double dpp_f64(double x) {
+  const long long b = __double_as_longlong(x);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)b, CTRL, ROW_MASK, 0xf, BOUND_CTRL);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTRL, ROW_MASK, 0xf, BOUND_CTRL);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
 }
 
-__device__ __forceinline__ void load_tile(float (&v)[kPerThread], const float *__restrict__ X, int64_t base,
-                                          int64_t n, bool vec) {
-  if (vec && base + kPerThread <= n) {
+// Inclusive scan over the 64 lanes of a wave: Hillis-Steele within each
+// 16-lane row (row_shr 1, 2, 4, 8), then row 0's total into row 1 and row
+// 2's into row 3 (row_bcast:15), then the first half's total into rows 2
+// and 3 (row_bcast:31). gfx9 DPP encodings.
+__device__ __forceinline__ double wave_incl_scan_f64(double x) {
+  x += dpp_f64<0x111, 0xf, true>(x);
+  x += dpp_f64<0x112, 0xf, true>(x);
+  x += dpp_f64<0x114, 0xf, true>(x);
+  x += dpp_f64<0x118, 0xf, true>(x);
+  x += dpp_f64<0x142, 0xa, false>(x);
+  x += dpp_f64<0x143, 0xc, false>(x);
+  return x;
+}
+
+__device__ __forceinline__ double readlane_f64(double x, int lane) {
+  const long long b = __double_as_longlong(x);
+  const int lo = __builtin_amdgcn_readlane((int)b, lane);
+  const int hi = __builtin_amdgcn_readlane((int)(b >> 32), lane);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+
+// A data wave's segment: kRows rows of 256 consecutive elements; lane l
+// holds elements [256 k + 4 l, 256 k + 4 l + 4) of row k in v[4k .. 4k+3],
+// so each row is one fully coalesced dwordx4 access per wave. VEC and a
+// segment inside [0, n): dwordx4 accesses; otherwise element accesses, loads
+// from clamped addresses (values past n read as 0).
+constexpr int kRows = kPerThread / 4;
+static_assert(kPerThread % 4 == 0, "rows of float4");
+
+template <bool VEC>
+__device__ __forceinline__ void load_seg(float (&v)[kPerThread], const float *__restrict__ X, int64_t seg,
+                                         int lane, int64_t n) {
+  if (VEC && seg + kh::kWave * kPerThread <= n) {
 #pragma unroll
-    for (int q = 0; q < kPerThread / 4; ++q) {
-      const float4 f = *reinterpret_cast<const float4 *>(X + base + 4 * q);
-      v[4 * q] = f.x;
-      v[4 * q + 1] = f.y;
-      v[4 * q + 2] = f.z;
-      v[4 * q + 3] = f.w;
+    for (int k = 0; k < kRows; ++k) {
+      const float4 f = *reinterpret_cast<const float4 *>(X + seg + 256 * k + 4 * lane);
+      v[4 * k] = f.x;
+      v[4 * k + 1] = f.y;
+      v[4 * k + 2] = f.z;
+      v[4 * k + 3] = f.w;
     }
   } else {
 #pragma unroll
-    for (int q = 0; q < kPerThread; ++q) v[q] = (base + q < n) ? X[base + q] : 0.0f;
+    for (int q = 0; q < kPerThread; ++q) {
+      const int64_t i = seg + 256 * (q / 4) + 4 * lane + (q % 4);
+      const float t = X[i < n ? i : n - 1];
+      v[q] = i < n ? t : 0.0f;
+    }
   }
 }
 
-__device__ __forceinline__ void store_tile(const float (&o)[kPerThread], float *__restrict__ Y, int64_t base,
-                                           int64_t n, bool vec) {
-  if (vec && base + kPerThread <= n) {
+template <bool VEC>
+__device__ __forceinline__ void store_seg(const float (&o)[kPerThread], float *__restrict__ Y, int64_t seg,
+                                          int lane, int64_t n) {
+  if (VEC && seg + kh::kWave * kPerThread <= n) {
 #pragma unroll
-    for (int q = 0; q < kPerThread / 4; ++q)
-      *reinterpret_cast<float4 *>(Y + base + 4 * q) = make_float4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+    for (int k = 0; k < kRows; ++k)
+      *reinterpret_cast<float4 *>(Y + seg + 256 * k + 4 * lane) =
+          make_float4(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]);
   } else {
 #pragma unroll
-    for (int q = 0; q < kPerThread; ++q)
-      if (base + q < n) Y[base + q] = o[q];
+    for (int q = 0; q < kPerThread; ++q) {
+      const int64_t i = seg + 256 * (q / 4) + 4 * lane + (q % 4);
+      if (i < n) Y[i] = o[q];
+    }
   }
 }
 
@@ -172,6 +215,135 @@ __device__ __forceinline__ double look_back(uint64_t *slots, uint32_t *state, in
   }
 }
 
+// The tile loop of one persistent workgroup, a three-stage pipeline. In
+// each iteration the workgroup
+//   * finishes tile `tc`: look-back, then y for its elements;
+//   * reduces tile `tr` and publishes its aggregate BEFORE that look-back;
+//   * has the loads of tile `tn` in flight.
+// Publishing aggregates one iteration ahead means every predecessor
+// aggregate a look-back needs went out an iteration earlier, so a look-back
+// normally completes on its first poll instead of waiting out the
+// publication latency of tiles handed out just before it.
+// The last wave is the control wave: it takes tickets and does the
+// look-back and never touches tile data; the other (data) waves load,
+// reduce and store. Vector-memory waits are in issue order per wave, so the
+// look-back's polls never wait on tile loads or stores. Each iteration takes
+// one ticket; its value is first needed at barrier B.
+// Deadlock-free: the lowest tile in look-back only needs aggregates of lower
+// tiles, and each of those is either finished or in the reduce stage of a
+// workgroup that publishes it without waiting on anything.
+template <bool VEC>
+__device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *__restrict__ Y, uint32_t *state,
+                                           uint64_t *slots, int64_t n, int64_t tr, int64_t tn, bool single,
+                                           uint32_t *s_raw, double *s_wave_total, double *s_prefix,
+                                           double *s_off) {
+  const int tid = threadIdx.x;
+  const int lane = kh::lane_id();
+  const int wave = tid / kh::kWave;
+  const int ndata = blockDim.x / kh::kWave - 1;
+  const bool ctrl = wave == ndata;
+  const int64_t tile_elems = (int64_t)ndata * kh::kWave * kPerThread;
+  const int64_t ntiles = (n + tile_elems - 1) / tile_elems;
+  const int64_t seg = (int64_t)wave * kh::kWave * kPerThread;  // data waves
+  // Per-thread row offsets of a reduced tile wait in LDS for its output
+  // stage (two buffers: reduce stage and output stage, alternating).
+  double *my_off = s_off + tid;
+
+  int64_t tc = -1;  // no tile to finish in the first iteration
+  float vc[kPerThread], vr[kPerThread];
+  double agg_c = 0.0;  // control wave: aggregate of tile tc
+  if (!ctrl) load_seg<VEC>(vr, X, tr * tile_elems + seg, lane, n);
+  int slot = 0;
+
+  for (;;) {
+    uint32_t raw = 0;
+    if (ctrl) {
+      if (lane == 0 && !single) raw = atomicAdd(state, 1u);
+    } else if (tr < ntiles) {
+      // ---- reduce tile tr: per-row lane sums (fp64), wave scans, wave total ---
+      // off[k] = (rows before k) + (lanes before this one in row k); exact,
+      // as every partial sum here is.
+      double pre = 0.0;
+#pragma unroll
+      for (int k = 0; k < kRows; ++k) {
+        const double sk = (((double)vr[4 * k] + (double)vr[4 * k + 1]) + (double)vr[4 * k + 2]) +
+                          (double)vr[4 * k + 3];
+        const double inc = wave_incl_scan_f64(sk);
+        my_off[(slot * kRows + k) * kMaxThreads] = pre + (inc - sk);
+        pre += readlane_f64(inc, kh::kWave - 1);
+      }
+      if (lane == 0) s_wave_total[wave] = pre;
+    }
+    __syncthreads();  // barrier A
+
+    float vn[kPerThread];
+    if (ctrl) {
+      // ---- publish tile tr's aggregate (tile 0: it is its inclusive) ---------
+      double agg_r = 0.0;
+      if (tr < ntiles) {
+        agg_r = wave_sum_f64(lane < ndata ? s_wave_total[lane] : 0.0);
+        if (!single && lane == 0) slot_store(&slots[2 * tr + (tr == 0 ? 1 : 0)], agg_r);
+      }
+      // ---- decoupled look-back for tile tc -------------------------------------
+      double excl = 0.0;
+      if (tc > 0) {
+        excl = look_back(slots, state, tc, lane);
+        if (lane == 0) slot_store(&slots[2 * tc + 1], excl + agg_c);
+      }
+      agg_c = agg_r;
+      if (lane == 0) {
+        *s_prefix = excl;
+        s_raw[slot] = raw;  // the raw ticket word; masked by its readers
+      }
+    } else {
+      // ---- tile tn's loads go out now and land during the look-back ----------
+      if (tn < ntiles) load_seg<VEC>(vn, X, tn * tile_elems + seg, lane, n);
+      if (tr < ntiles) {
+        double wave_excl = 0.0;
+        for (int w = 0; w < wave; ++w) wave_excl += s_wave_total[w];
+#pragma unroll
+        for (int k = 0; k < kRows; ++k) my_off[(slot * kRows + k) * kMaxThreads] += wave_excl;
+      }
+    }
+    __syncthreads();  // barrier B
+    const int64_t after = single ? ntiles : (int64_t)(s_raw[slot] & ~kFailBit);
+
+    if (!ctrl && tc >= 0) {
+      // ---- y = fl32(prefix + row offset + running sum within the float4) -----
+      const double prefix = *s_prefix;
+      float o[kPerThread];
+#pragma unroll
+      for (int k = 0; k < kRows; ++k) {
+        double run = prefix + my_off[((slot ^ 1) * kRows + k) * kMaxThreads];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          run += (double)vc[4 * k + j];
+          o[4 * k + j] = (float)run;
+        }
+      }
+      store_seg<VEC>(o, Y, tc * tile_elems + seg, lane, n);
+    }
+
+    if (tr >= ntiles) return;  // tc was this workgroup's last tile
+    tc = tr;
+    tr = tn;
+    tn = after;
+    if (!ctrl) {
+#pragma unroll
+      for (int q = 0; q < kPerThread; ++q) {
+        vc[q] = vr[q];
+        vr[q] = vn[q];
+      }
+    }
+    // s_raw[slot] was read after barrier B above and is next written two
+    // iterations later. s_wave_total and s_prefix are rewritten only after
+    // every wave has passed the next barrier A, past all their reads. A
+    // thread's row offsets are its own: buffer `slot` holds tile tr's (read
+    // as tile tc's in the next iteration, where slot has flipped).
+    slot ^= 1;
+  }
+}
+
 }  // namespace
 
 extern "C" __global__ void __launch_bounds__(kMaxThreads)
@@ -184,15 +356,14 @@ scan(KH_MEMREF1(const float, x), KH_MEMREF1(float, y), KH_MEMREF1(float, y_lo),
   uint32_t *state = reinterpret_cast<uint32_t *>(KH_PTR(totals_lo));
   uint64_t *slots = reinterpret_cast<uint64_t *>(KH_PTR(totals_hi));
   const int64_t n = x_n0;
-  const int64_t tile_elems = (int64_t)blockDim.x * kPerThread;
+  const int64_t tile_elems = (int64_t)(blockDim.x - kh::kWave) * kPerThread;
   const int64_t ntiles = (n + tile_elems - 1) / tile_elems;
   const int tid = threadIdx.x;
-  const int lane = kh::lane_id();
-  const int wave = tid / kh::kWave;
-  const int nwaves = blockDim.x / kh::kWave;
 
   __shared__ int64_t s_ticket[2];
+  __shared__ uint32_t s_raw[2];
   __shared__ double s_wave_total[kMaxThreads / kh::kWave];
+  __shared__ double s_off[2 * kRows * kMaxThreads];
   __shared__ double s_prefix;
 
   // The look-back state needs 16 B per tile in totals_hi; workgroups of at
@@ -203,78 +374,23 @@ scan(KH_MEMREF1(const float, x), KH_MEMREF1(float, y), KH_MEMREF1(float, y_lo),
       Y[i] = __builtin_nanf("");
     return;
   }
-  const bool vec = kh::aligned16(X) && kh::aligned16(Y);
   const bool single = ntiles == 1;  // one tile: block 0, no look-back state
-
   if (single) {
     if (blockIdx.x != 0) return;
     s_ticket[0] = 0;
+    s_ticket[1] = ntiles;
   } else if (tid == 0) {
     s_ticket[0] = (int64_t)(atomicAdd(state, 1u) & ~kFailBit);
+    s_ticket[1] = (int64_t)(atomicAdd(state, 1u) & ~kFailBit);
   }
   __syncthreads();
-  int64_t tile = s_ticket[0];
-  if (tile >= ntiles) return;
-
-  float v[kPerThread];
-  load_tile(v, X, tile * tile_elems + (int64_t)tid * kPerThread, n, vec);
-  int parity = 0;
-
-  for (;;) {
-    // The next ticket is fetched by the last wave while the others reduce.
-    if (wave == nwaves - 1 && lane == 0) {
-      s_ticket[parity ^ 1] = single ? ntiles : (int64_t)(atomicAdd(state, 1u) & ~kFailBit);
-    }
-
-    // ---- thread total (fp64), wave scan, block totals -----------------------
-    double acc = 0.0;
-#pragma unroll
-    for (int q = 0; q < kPerThread; ++q) acc += (double)v[q];
-    const double incl = wave_incl_scan_f64(acc, lane);
-    const double thread_excl = incl - acc;  // exact: both are exact partial sums
-    if (lane == kh::kWave - 1) s_wave_total[wave] = incl;
-    __syncthreads();
-    double wave_excl = 0.0, agg = 0.0;
-    for (int w = 0; w < nwaves; ++w) {
-      const double t = s_wave_total[w];
-      if (w < wave) wave_excl += t;
-      agg += t;
-    }
-    const int64_t next = s_ticket[parity ^ 1];
-
-    // ---- publish the aggregate, then start the next tile's loads -------------
-    // (tile 0 has no predecessors: its aggregate is its inclusive prefix.)
-    if (!single && wave == 0 && lane == 0) slot_store(&slots[2 * tile + (tile == 0 ? 1 : 0)], agg);
-    float vn[kPerThread];
-    if (next < ntiles) load_tile(vn, X, next * tile_elems + (int64_t)tid * kPerThread, n, vec);
-
-    // ---- decoupled look-back (wave 0) -----------------------------------------
-    if (wave == 0) {
-      double excl = 0.0;
-      if (tile > 0) {
-        excl = look_back(slots, state, tile, lane);
-        if (lane == 0) slot_store(&slots[2 * tile + 1], excl + agg);
-      }
-      if (lane == 0) s_prefix = excl;
-    }
-    __syncthreads();
-
-    // ---- y = fl32(prefix + wave_excl + thread_excl + running local sum) ------
-    double run = s_prefix + wave_excl + thread_excl;
-    float o[kPerThread];
-#pragma unroll
-    for (int q = 0; q < kPerThread; ++q) {
-      run += (double)v[q];
-      o[q] = (float)run;
-    }
-    store_tile(o, Y, tile * tile_elems + (int64_t)tid * kPerThread, n, vec);
-
-    if (next >= ntiles) return;
-    tile = next;
-#pragma unroll
-    for (int q = 0; q < kPerThread; ++q) v[q] = vn[q];
-    parity ^= 1;
-  }
+  const int64_t first = s_ticket[0];
+  const int64_t second = s_ticket[1];
+  if (first >= ntiles) return;
+  if (kh::aligned16(X) && kh::aligned16(Y))
+    scan_tiles<true>(X, Y, state, slots, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off);
+  else
+    scan_tiles<false>(X, Y, state, slots, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off);
 }
 
 // Clears the ticket (totals_lo[0]) and marks every tile slot in totals_hi

@@ -356,12 +356,12 @@ int kh_scan(const float *x, float *y, float *y_lo, float *totals_hi, float *tota
   if (n <= 0) return bad("scan: n must be positive");
   if (!x || !y || !totals_hi || !totals_lo) return bad("scan: null buffer");
   const int64_t T = ceil_div(n, 256);
-  const int64_t tiles = ceil_div(n, 4096);  // smallest tile the kernel accepts
+  const int64_t tiles = ceil_div(n, KH_SCAN_MIN_TILE);  // smallest tile the kernel accepts
   if (tiles > 1 && (reinterpret_cast<uintptr_t>(totals_hi) & 7u) != 0) {
     return bad("scan: totals_hi must be 8-byte aligned (it holds the fp64 look-back values)");
   }
-  // Look-back state: 16 B per 4096-element tile in totals_hi, the ticket in
-  // totals_lo[0]. T = ceil(n/256) floats always suffices for n > 4096.
+  // Look-back state: 16 B per tile in totals_hi, the ticket in totals_lo[0].
+  // T = ceil(n/256) floats always suffices once there is more than one tile.
   if (tiles > 1 && T < 4 * tiles) return bad("scan: totals buffers too small for the look-back state");
   khrt::LaunchArgs args;
   args.add_memref(x, {n});

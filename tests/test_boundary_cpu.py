@@ -259,8 +259,8 @@ def test_kernarg_segment_is_2n_plus_3_slots(name, nslots):
     ("fused_gelu", "rows=4096,cols=1024", (1024, 1, 1), (256, 1, 1)),
     ("softmax", "rows=4096,cols=1024", (1024, 1, 1), (256, 1, 1)),
     ("layernorm", "rows=4097,cols=1024", (1025, 1, 1), (256, 1, 1)),
-    ("scan", "n=1000000", (62, 1, 1), (1024, 1, 1)),
-    ("scan", "n=67108864", (4096, 1, 1), (1024, 1, 1)),
+    ("scan", "n=1000000", (66, 1, 1), (1024, 1, 1)),
+    ("scan", "n=67108864", (4370, 1, 1), (1024, 1, 1)),
     ("gemm", "m=8192,n=8192,k=8192", (4096, 1, 1), (256, 1, 1)),
     ("attention", "batch=4,heads=16,seq=4096,head_dim=64", (32, 16, 4), (256, 1, 1)),
 ])
