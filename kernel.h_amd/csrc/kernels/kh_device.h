@@ -89,4 +89,15 @@ __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Workgroup barrier that orders LDS accesses only. __syncthreads() is a
+// workgroup-scope release/acquire fence on all memory, which makes every
+// wave wait for its outstanding global loads and stores at the barrier;
+// kernels whose waves share data through LDS alone use this instead, so
+// prefetches and stores stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 }  // namespace kh

@@ -61,7 +61,7 @@ constexpr int kMinThreads = 256;
 constexpr int kPerThread = KH_SCAN_PER_THREAD;
 constexpr int kMinTile = KH_SCAN_MIN_TILE;  // 256 threads: sizes the look-back state
 #ifndef KH_SCAN_WINDOW
-#define KH_SCAN_WINDOW 4
+#define KH_SCAN_WINDOW 2
 #endif
 constexpr int kWindow = KH_SCAN_WINDOW;  // predecessors polled per lane per look-back step
 constexpr uint32_t kSpinLimit = 1u << 22;
@@ -115,47 +115,56 @@ __device__ __forceinline__ double readlane_f64(double x, int lane) {
 
 // A data wave's segment: kRows rows of 256 consecutive elements; lane l
 // holds elements [256 k + 4 l, 256 k + 4 l + 4) of row k in v[4k .. 4k+3],
-// so each row is one fully coalesced dwordx4 access per wave. VEC and a
-// segment inside [0, n): dwordx4 accesses; otherwise element accesses, loads
-// from clamped addresses (values past n read as 0).
+// so each row is one fully coalesced 16-byte access per lane.
+//
+// Tile data moves through buffer instructions over a resource that spans
+// exactly the tile's elements inside [0, n): the hardware range check makes
+// loads past n read 0 and drops stores past n. The same instructions are
+// issued for every tile, full or partial, with no data-dependent branches
+// around them, which keeps the vector-memory wait counts exact (a branch
+// with a variable number of memory operations forces waits for all of them).
+// VEC (16-byte aligned x and y, n a multiple of 4): dwordx4 accesses, each
+// wholly inside or wholly outside the range; otherwise dword accesses.
 constexpr int kRows = kPerThread / 4;
 static_assert(kPerThread % 4 == 0, "rows of float4");
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor: 32-bit data format
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const float *base, int64_t elems) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, (int)(elems * 4), kRsrcWord3);
+}
 
 template <bool VEC>
-__device__ __forceinline__ void load_seg(float (&v)[kPerThread], const float *__restrict__ X, int64_t seg,
-                                         int lane, int64_t n) {
-  if (VEC && seg + kh::kWave * kPerThread <= n) {
+__device__ __forceinline__ void load_seg(float (&v)[kPerThread], __amdgpu_buffer_rsrc_t r, int seg, int lane) {
 #pragma unroll
-    for (int k = 0; k < kRows; ++k) {
-      const float4 f = *reinterpret_cast<const float4 *>(X + seg + 256 * k + 4 * lane);
-      v[4 * k] = f.x;
-      v[4 * k + 1] = f.y;
-      v[4 * k + 2] = f.z;
-      v[4 * k + 3] = f.w;
-    }
-  } else {
+  for (int k = 0; k < kRows; ++k) {
+    const int e = seg + 256 * k + 4 * lane;
+    if (VEC) {
+      const u32x4 f = __builtin_amdgcn_raw_buffer_load_b128(r, 4 * e, 0, 0);
 #pragma unroll
-    for (int q = 0; q < kPerThread; ++q) {
-      const int64_t i = seg + 256 * (q / 4) + 4 * lane + (q % 4);
-      const float t = X[i < n ? i : n - 1];
-      v[q] = i < n ? t : 0.0f;
+      for (int j = 0; j < 4; ++j) v[4 * k + j] = __uint_as_float(f[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[4 * k + j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, 4 * (e + j), 0, 0));
     }
   }
 }
 
 template <bool VEC>
-__device__ __forceinline__ void store_seg(const float (&o)[kPerThread], float *__restrict__ Y, int64_t seg,
-                                          int lane, int64_t n) {
-  if (VEC && seg + kh::kWave * kPerThread <= n) {
+__device__ __forceinline__ void store_seg(const float (&o)[kPerThread], __amdgpu_buffer_rsrc_t r, int seg,
+                                          int lane) {
 #pragma unroll
-    for (int k = 0; k < kRows; ++k)
-      *reinterpret_cast<float4 *>(Y + seg + 256 * k + 4 * lane) =
-          make_float4(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]);
-  } else {
+  for (int k = 0; k < kRows; ++k) {
+    const int e = seg + 256 * k + 4 * lane;
+    if (VEC) {
+      u32x4 f;
 #pragma unroll
-    for (int q = 0; q < kPerThread; ++q) {
-      const int64_t i = seg + 256 * (q / 4) + 4 * lane + (q % 4);
-      if (i < n) Y[i] = o[q];
+      for (int j = 0; j < 4; ++j) f[j] = __float_as_uint(o[4 * k + j]);
+      __builtin_amdgcn_raw_buffer_store_b128(f, r, 4 * e, 0, 0);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o[4 * k + j]), r, 4 * (e + j), 0, 0);
     }
   }
 }
@@ -220,10 +229,10 @@ __device__ __forceinline__ double look_back(uint64_t *slots, uint32_t *state, in
 //   * finishes tile `tc`: look-back, then y for its elements;
 //   * reduces tile `tr` and publishes its aggregate BEFORE that look-back;
 //   * has the loads of tile `tn` in flight.
-// Publishing aggregates one iteration ahead means every predecessor
-// aggregate a look-back needs went out an iteration earlier, so a look-back
-// normally completes on its first poll instead of waiting out the
-// publication latency of tiles handed out just before it.
+// Reducing (and publishing) one iteration ahead of the look-back means every
+// predecessor aggregate a look-back needs went out an iteration earlier, so
+// a look-back normally completes on its first poll instead of waiting out
+// the publication latency of tiles handed out just before it.
 // The last wave is the control wave: it takes tickets and does the
 // look-back and never touches tile data; the other (data) waves load,
 // reduce and store. Vector-memory waits are in issue order per wave, so the
@@ -244,19 +253,26 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
   const bool ctrl = wave == ndata;
   const int64_t tile_elems = (int64_t)ndata * kh::kWave * kPerThread;
   const int64_t ntiles = (n + tile_elems - 1) / tile_elems;
-  const int64_t seg = (int64_t)wave * kh::kWave * kPerThread;  // data waves
+  const int seg = wave * kh::kWave * kPerThread;  // data waves: offset in the tile
   // Per-thread row offsets of a reduced tile wait in LDS for its output
   // stage (two buffers: reduce stage and output stage, alternating).
   double *my_off = s_off + tid;
+  auto elems = [&](int64_t t) { return n - t * tile_elems < tile_elems ? n - t * tile_elems : tile_elems; };
 
-  int64_t tc = -1;  // no tile to finish in the first iteration
-  float vc[kPerThread], vr[kPerThread];
-  double agg_c = 0.0;  // control wave: aggregate of tile tc
-  if (!ctrl) load_seg<VEC>(vr, X, tr * tile_elems + seg, lane, n);
+  int64_t tc = -1;       // no tile to finish in the first iteration
+  double agg_c = 0.0;    // control wave: aggregate of tile tc
+  double wexcl_c = 0.0;  // data waves: sum of earlier waves' totals in tile tc
   int slot = 0;
 
-  for (;;) {
-    uint32_t raw = 0;
+  // One pipeline iteration: finish tc (data in vc), reduce tr (vr), load tn
+  // (into vn). False once tc was the workgroup's last tile. The caller
+  // rotates the three register buffers instead of copying them.
+  auto step = [&](float (&vc)[kPerThread], float (&vr)[kPerThread], float (&vn)[kPerThread])
+      __attribute__((always_inline)) -> bool {
+    // Defined only where it is used (control wave, lane 0): a default value
+    // on the data path would be a register write that must wait for the
+    // pending atomic, i.e. for all of that wave's outstanding memory ops.
+    uint32_t raw;
     if (ctrl) {
       if (lane == 0 && !single) raw = atomicAdd(state, 1u);
     } else if (tr < ntiles) {
@@ -274,9 +290,9 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
       }
       if (lane == 0) s_wave_total[wave] = pre;
     }
-    __syncthreads();  // barrier A
+    kh::lds_barrier();  // barrier A
 
-    float vn[kPerThread];
+    double wexcl_r = 0.0;
     if (ctrl) {
       // ---- publish tile tr's aggregate (tile 0: it is its inclusive) ---------
       double agg_r = 0.0;
@@ -293,24 +309,21 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
       agg_c = agg_r;
       if (lane == 0) {
         *s_prefix = excl;
-        s_raw[slot] = raw;  // the raw ticket word; masked by its readers
+        s_raw[slot] = single ? 0u : raw;  // the raw ticket word; masked by its readers
       }
     } else {
       // ---- tile tn's loads go out now and land during the look-back ----------
-      if (tn < ntiles) load_seg<VEC>(vn, X, tn * tile_elems + seg, lane, n);
-      if (tr < ntiles) {
-        double wave_excl = 0.0;
-        for (int w = 0; w < wave; ++w) wave_excl += s_wave_total[w];
-#pragma unroll
-        for (int k = 0; k < kRows; ++k) my_off[(slot * kRows + k) * kMaxThreads] += wave_excl;
-      }
+      // (past the last tile the range is empty: the loads read 0.)
+      load_seg<VEC>(vn, tile_rsrc(X + tn * tile_elems, tn < ntiles ? elems(tn) : 0), seg, lane);
+      if (tr < ntiles)
+        for (int w = 0; w < wave; ++w) wexcl_r += s_wave_total[w];
     }
-    __syncthreads();  // barrier B
+    kh::lds_barrier();  // barrier B
     const int64_t after = single ? ntiles : (int64_t)(s_raw[slot] & ~kFailBit);
 
     if (!ctrl && tc >= 0) {
       // ---- y = fl32(prefix + row offset + running sum within the float4) -----
-      const double prefix = *s_prefix;
+      const double prefix = *s_prefix + wexcl_c;
       float o[kPerThread];
 #pragma unroll
       for (int k = 0; k < kRows; ++k) {
@@ -321,26 +334,29 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
           o[4 * k + j] = (float)run;
         }
       }
-      store_seg<VEC>(o, Y, tc * tile_elems + seg, lane, n);
+      store_seg<VEC>(o, tile_rsrc(Y + tc * tile_elems, elems(tc)), seg, lane);
     }
 
-    if (tr >= ntiles) return;  // tc was this workgroup's last tile
+    if (tr >= ntiles) return false;  // tc was this workgroup's last tile
     tc = tr;
     tr = tn;
     tn = after;
-    if (!ctrl) {
-#pragma unroll
-      for (int q = 0; q < kPerThread; ++q) {
-        vc[q] = vr[q];
-        vr[q] = vn[q];
-      }
-    }
+    wexcl_c = wexcl_r;
     // s_raw[slot] was read after barrier B above and is next written two
     // iterations later. s_wave_total and s_prefix are rewritten only after
     // every wave has passed the next barrier A, past all their reads. A
     // thread's row offsets are its own: buffer `slot` holds tile tr's (read
     // as tile tc's in the next iteration, where slot has flipped).
     slot ^= 1;
+    return true;
+  };
+
+  float a[kPerThread], b[kPerThread], c[kPerThread];
+  if (!ctrl) load_seg<VEC>(b, tile_rsrc(X + tr * tile_elems, elems(tr)), seg, lane);
+  for (;;) {
+    if (!step(a, b, c)) return;
+    if (!step(b, c, a)) return;
+    if (!step(c, a, b)) return;
   }
 }
 
@@ -383,11 +399,11 @@ scan(KH_MEMREF1(const float, x), KH_MEMREF1(float, y), KH_MEMREF1(float, y_lo),
     s_ticket[0] = (int64_t)(atomicAdd(state, 1u) & ~kFailBit);
     s_ticket[1] = (int64_t)(atomicAdd(state, 1u) & ~kFailBit);
   }
-  __syncthreads();
+  kh::lds_barrier();
   const int64_t first = s_ticket[0];
   const int64_t second = s_ticket[1];
   if (first >= ntiles) return;
-  if (kh::aligned16(X) && kh::aligned16(Y))
+  if (kh::aligned16(X) && kh::aligned16(Y) && (n & 3) == 0)
     scan_tiles<true>(X, Y, state, slots, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off);
   else
     scan_tiles<false>(X, Y, state, slots, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off);
