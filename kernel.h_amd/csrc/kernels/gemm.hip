@@ -8,14 +8,20 @@
 //
 //   * Workgroup = 256 threads (4 wave64s) computing a 128x128 tile of C;
 //     each wave owns a 64x64 quarter as 2x2 MFMA 32x32 accumulators
-//     (64 accumulator registers per lane).
+//     (64 accumulator registers per lane). Registers are capped for two
+//     waves per SIMD (two workgroups per CU, as LDS allows), so one
+//     workgroup's barrier and slab hand-over overlap the other's MFMAs.
 //   * K advances in 32-wide slabs staged through LDS, double-buffered: the
 //     next slab's global loads are in flight while the current slab feeds
 //     the MFMAs, one barrier per slab.
 //   * LDS holds A as [m][k] (rows padded to 36 floats: one ds_read_b128 per
 //     lane delivers four k values, every 8-lane group on distinct banks) and
 //     B as [k][n] (rows padded to 132 floats; a half-wave reads 32
-//     consecutive n with ds_read_b32). Both slabs arrive as dwordx4 loads.
+//     consecutive n with ds_read_b32). Both slabs arrive as dwordx4 loads:
+//     for aligned operands with k, n multiples of 4 as branch-free buffer
+//     loads whose range checks zero-fill the tails (the guarded per-element
+//     form of the generic path made the compiler split every load into
+//     branches and dword pieces, which cost 15% of the MFMA rate).
 //   * K order inside an MFMA: the instruction sums k over its two lane
 //     halves, and any permutation of k applied to both operands gives the
 //     same product. Lane half h reads k = 8c + 4h + {0..3}; MFMA step s of
@@ -60,6 +66,7 @@ __device__ __forceinline__ float4 load4(const float *__restrict__ P, int64_t row
   return make_float4(t[0], t[1], t[2], t[3]);
 }
 
+// Generic slab load: any shape, stride and alignment (guarded per element).
 __device__ __forceinline__ void load_slab(Slab &s, const float *__restrict__ A, const float *__restrict__ B,
                                           int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t m0,
                                           int64_t n0, int64_t k0, bool a_vec, bool b_vec, int tid) {
@@ -70,6 +77,41 @@ __device__ __forceinline__ void load_slab(Slab &s, const float *__restrict__ A, 
     const int idx = tid + kThreads * i;
     s.a[i] = load4(A, m0 + (idx >> 3), k0 + 4 * (idx & 7), lda, M, K, a_vec);
     s.b[i] = load4(B, k0 + (idx >> 5), n0 + 4 * (idx & 31), ldb, K, N, b_vec);
+  }
+}
+
+// Fast slab load for 16-byte aligned A and B with k and n multiples of 4:
+// unconditional dwordx4 buffer loads. Each resource spans the slab's rows
+// that exist (A: tile rows m0.. below M; B: slab rows k0.. below K), so
+// rows past the matrix read 0 through the hardware range check; a float4
+// past K (A) or N (B) is sent to an offset outside the resource and reads 0
+// as well. No branches, 32-bit offsets: the loop issues exactly 8 loads.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor: 32-bit data format
+constexpr uint32_t kOutside = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float *base, int64_t rows, int64_t ld) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, (int)(rows * ld * 4), kRsrcWord3);
+}
+
+__device__ __forceinline__ float4 as_float4(u32x4 u) {
+  return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+}
+
+__device__ __forceinline__ void load_slab_vec(Slab &s, const float *__restrict__ A, const float *__restrict__ B,
+                                              int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                                              int64_t m0, int64_t n0, int64_t k0, int tid) {
+  const __amdgpu_buffer_rsrc_t ra = rows_rsrc(A + m0 * lda, (M - m0) < BM ? (M - m0) : BM, lda);
+  const __amdgpu_buffer_rsrc_t rb = rows_rsrc(B + k0 * ldb, (K - k0) < BK ? (K - k0) : BK, ldb);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = tid + kThreads * i;
+    const int ar = idx >> 3, ak = 4 * (idx & 7);   // A: row in tile, k in slab
+    const int bk = idx >> 5, bn = 4 * (idx & 31);  // B: k in slab, column in tile
+    const uint32_t aoff = (k0 + ak < K) ? (uint32_t)((ar * lda + k0 + ak) * 4) : kOutside;
+    const uint32_t boff = (n0 + bn < N) ? (uint32_t)((bk * ldb + n0 + bn) * 4) : kOutside;
+    s.a[i] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(ra, aoff, 0, 0));
+    s.b[i] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(rb, boff, 0, 0));
   }
 }
 
@@ -122,25 +164,19 @@ __device__ __forceinline__ void tile_coords(int64_t pid, int64_t tiles_m, int64_
   tn = (pid % width) / gsz;
 }
 
-}  // namespace
-
-extern "C" __global__ void __launch_bounds__(kThreads)
-gemm(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
-  const float *__restrict__ Ap = KH_PTR(A);
-  const float *__restrict__ Bp = KH_PTR(B);
-  float *__restrict__ Cp = KH_PTR(C);
-  const int64_t M = A_n0, K = A_n1, N = B_n1;
-  const int64_t lda = A_s0, ldb = B_s0, ldc = C_s0;
-
-  __shared__ __attribute__((aligned(16))) float As[2][BM * LDA];
-  __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDB];
-
+// One workgroup's loop over its tiles. VEC selects the fast slab loads.
+template <bool VEC>
+__device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const float *__restrict__ Bp,
+                                           float *__restrict__ Cp, int64_t M, int64_t N, int64_t K, int64_t lda,
+                                           int64_t ldb, int64_t ldc, bool a_vec, bool b_vec, float *As,
+                                           float *Bs) {
+  // As, Bs: the two LDS stages, BM*LDA and BK*LDB floats apart. (Offsets
+  // from one base keep the pointers visibly in LDS for the compiler; an
+  // array of stage pointers would turn every LDS access into a flat one.)
   const int tid = threadIdx.x;
   const int lane = kh::lane_id();
   const int wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const bool a_vec = ((K & 3) == 0) && ((lda & 3) == 0) && kh::aligned16(Ap);
-  const bool b_vec = ((N & 3) == 0) && ((ldb & 3) == 0) && kh::aligned16(Bp);
 
   const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   const int64_t total = tiles_m * tiles_n;
@@ -160,16 +196,22 @@ gemm(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
 
+    auto load = [&](Slab &sl, int64_t k0) __attribute__((always_inline)) {
+      if (VEC)
+        load_slab_vec(sl, Ap, Bp, M, N, K, lda, ldb, m0, n0, k0, tid);
+      else
+        load_slab(sl, Ap, Bp, M, N, K, lda, ldb, m0, n0, k0, a_vec, b_vec, tid);
+    };
     Slab s;
-    load_slab(s, Ap, Bp, M, N, K, lda, ldb, m0, n0, 0, a_vec, b_vec, tid);
-    store_slab(s, As[0], Bs[0], tid);
+    load(s, 0);
+    store_slab(s, As, Bs, tid);
     __syncthreads();
     for (int64_t ks = 0; ks < nslabs; ++ks) {
       const int cur = ks & 1;
       const bool more = ks + 1 < nslabs;
-      if (more) load_slab(s, Ap, Bp, M, N, K, lda, ldb, m0, n0, (ks + 1) * BK, a_vec, b_vec, tid);
-      compute_slab(acc, As[cur], Bs[cur], wm, wn, lane);
-      if (more) store_slab(s, As[cur ^ 1], Bs[cur ^ 1], tid);
+      if (more) load(s, (ks + 1) * BK);
+      compute_slab(acc, As + cur * (BM * LDA), Bs + cur * (BK * LDB), wm, wn, lane);
+      if (more) store_slab(s, As + (cur ^ 1) * (BM * LDA), Bs + (cur ^ 1) * (BK * LDB), tid);
       __syncthreads();
     }
 
@@ -189,4 +231,27 @@ gemm(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C
       }
     }
   }
+}
+
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+gemm(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
+  const float *__restrict__ Ap = KH_PTR(A);
+  const float *__restrict__ Bp = KH_PTR(B);
+  float *__restrict__ Cp = KH_PTR(C);
+  const int64_t M = A_n0, K = A_n1, N = B_n1;
+  const int64_t lda = A_s0, ldb = B_s0, ldc = C_s0;
+
+  __shared__ __attribute__((aligned(16))) float As[2][BM * LDA];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDB];
+
+  const bool a_vec = ((K & 3) == 0) && ((lda & 3) == 0) && kh::aligned16(Ap);
+  const bool b_vec = ((N & 3) == 0) && ((ldb & 3) == 0) && kh::aligned16(Bp);
+  // The fast loads address a tile's rows with 32-bit byte offsets.
+  const bool fits32 = (int64_t)BM * lda * 4 < (1ll << 31) && (int64_t)BK * ldb * 4 < (1ll << 31);
+  if (a_vec && b_vec && fits32)
+    gemm_tiles<true>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, &As[0][0], &Bs[0][0]);
+  else
+    gemm_tiles<false>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, &As[0][0], &Bs[0][0]);
 }
