@@ -162,7 +162,10 @@ __device__ __forceinline__ void attend_tile(v16f (&o)[2], float &m, float &l, co
 
 }  // namespace
 
-extern "C" __global__ void __launch_bounds__(256)
+// Registers capped for two waves per SIMD (two workgroups per CU, as LDS
+// allows): one wave's softmax VALU work then overlaps the other's MFMAs.
+// Uncapped, the compiler takes more than 256 registers and halves that.
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 attention(KH_MEMREF4(const float, Q), KH_MEMREF4(const float, K), KH_MEMREF4(const float, V),
           KH_MEMREF4(float, O)) {
   const float *__restrict__ Qp = KH_PTR(Q);
