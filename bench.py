@@ -43,8 +43,8 @@ METRIC = "GEMM-8192 fp32 TFLOPS + softmax/scan HBM GB/s, % of MI355X roofline"
 # 2.000 and WRITE_SIZE by 1.000, the factors a copy kernel of known size
 # reads), recorded in profiles/templates_baseline_sizes_hbm_traffic.md.
 PMC_TRAFFIC_BYTES = {
-    "vecadd": 201361158, "softmax": 33630353, "layernorm": 33709000, "scan": 539694765,
-    "fused_gelu": 537445000, "gemm": 7050662585, "attention": 1208055525,
+    "vecadd": 201373696, "softmax": 33634304, "layernorm": 33726464, "scan": 539584512,
+    "fused_gelu": 537007104, "gemm": 6909112320, "attention": 1208114176,
 }
 
 
