@@ -6,22 +6,26 @@
 // 21 parameters. The reference computes one element per lane with scalar
 // FMAs out of an 8 KiB LDS tile (gemm.cpp:265-296). Here:
 //
-//   * Workgroup = 256 threads (4 wave64s) computing a 128x128 tile of C;
-//     each wave owns a 64x64 quarter as 2x2 MFMA 32x32 accumulators
-//     (64 accumulator registers per lane). Registers are capped for two
-//     waves per SIMD (two workgroups per CU, as LDS allows), so one
-//     workgroup's barrier and slab hand-over overlap the other's MFMAs.
+//   * Workgroup = 256 threads (4 wave64s, 2x2) computing a square tile of C;
+//     each wave owns a quarter as WT x WT MFMA 32x32 accumulators. Two
+//     symbols: `gemm` (WT = 2: 128x128 tiles, 64 accumulator registers per
+//     lane) and `gemm_small` (WT = 1: 64x64 tiles), which the launcher picks
+//     when the 128x128 grid would have too few tiles to fill the CUs
+//     (KH_GEMM_SMALL_TILES). Both are correct for every shape.
+//   * `gemm`'s registers are capped for two waves per SIMD (two workgroups
+//     per CU, as LDS allows), so one workgroup's barrier and slab hand-over
+//     overlap the other's MFMAs.
 //   * K advances in 32-wide slabs staged through LDS, double-buffered: the
 //     next slab's global loads are in flight while the current slab feeds
 //     the MFMAs, one barrier per slab.
 //   * LDS holds A as [m][k] (rows padded to 36 floats: one ds_read_b128 per
 //     lane delivers four k values, every 8-lane group on distinct banks) and
-//     B as [k][n] (rows padded to 132 floats; a half-wave reads 32
-//     consecutive n with ds_read_b32). Both slabs arrive as dwordx4 loads:
-//     for aligned operands with k, n multiples of 4 as branch-free buffer
-//     loads whose range checks zero-fill the tails (the guarded per-element
-//     form of the generic path made the compiler split every load into
-//     branches and dword pieces, which cost 15% of the MFMA rate).
+//     B as [k][n] (rows padded by 4 floats; a half-wave reads 32 consecutive
+//     n with ds_read_b32). Both slabs arrive as dwordx4 loads: for aligned
+//     operands with k, n multiples of 4 as branch-free buffer loads whose
+//     range checks zero-fill the tails (the guarded per-element form of the
+//     generic path made the compiler split every load into branches and
+//     dword pieces, which cost 15% of the MFMA rate).
 //   * K order inside an MFMA: the instruction sums k over its two lane
 //     halves, and any permutation of k applied to both operands gives the
 //     same product. Lane half h reads k = 8c + 4h + {0..3}; MFMA step s of
@@ -41,20 +45,32 @@
 namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BM = KH_GEMM_BM;  // 128
-constexpr int BN = KH_GEMM_BN;  // 128
 constexpr int BK = 32;
-constexpr int LDA = BK + 4;     // A in LDS: [m][k], rows padded to 36 floats
-constexpr int LDB = BN + 4;     // B in LDS: [k][n], rows padded to 132 floats
+constexpr int LDA = BK + 4;  // A in LDS: [m][k], rows padded to 36 floats
 constexpr int kThreads = 256;
 constexpr int kGroupM = 8;
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor: 32-bit data format
+constexpr uint32_t kOutside = 0x80000000u;
 
-static_assert(BM == 128 && BN == 128, "wave tiling below assumes 128x128");
+// Tile geometry for WT x WT accumulators per wave.
+template <int WT>
+struct Tile {
+  static constexpr int BM = 64 * WT;       // rows of C per workgroup
+  static constexpr int BN = 64 * WT;       // columns of C per workgroup
+  static constexpr int LDB = BN + 4;       // B in LDS: [k][n], padded rows
+  static constexpr int NA = BM * BK / 4 / kThreads;  // A float4 per thread per slab
+  static constexpr int NB = BK * BN / 4 / kThreads;  // B float4 per thread per slab
+  static constexpr int BROW = BN / 4;      // float4 per B row (lanes per B row)
+  static constexpr int A_STAGE = BM * LDA;
+  static constexpr int B_STAGE = BK * LDB;
+};
 
+template <int WT>
 struct Slab {
-  float4 a[4];  // A: 4 x (one row, 4 consecutive k)
-  float4 b[4];  // B: 4 x (one k row, 4 consecutive n)
+  float4 a[Tile<WT>::NA];  // A: one row, 4 consecutive k each
+  float4 b[Tile<WT>::NB];  // B: one k row, 4 consecutive n each
 };
 
 __device__ __forceinline__ float4 load4(const float *__restrict__ P, int64_t row, int64_t col, int64_t ld,
@@ -67,16 +83,21 @@ __device__ __forceinline__ float4 load4(const float *__restrict__ P, int64_t row
 }
 
 // Generic slab load: any shape, stride and alignment (guarded per element).
-__device__ __forceinline__ void load_slab(Slab &s, const float *__restrict__ A, const float *__restrict__ B,
+// A: 8 lanes cover a 32-k row; B: BN/4 lanes cover a row of the tile.
+template <int WT>
+__device__ __forceinline__ void load_slab(Slab<WT> &s, const float *__restrict__ A, const float *__restrict__ B,
                                           int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t m0,
                                           int64_t n0, int64_t k0, bool a_vec, bool b_vec, int tid) {
-  // A: 128 rows x 32 k = 1024 float4, four per thread; 8 lanes cover a row.
-  // B: 32 k x 128 n = 1024 float4, four per thread; 32 lanes cover a row.
+  using T = Tile<WT>;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < T::NA; ++i) {
     const int idx = tid + kThreads * i;
     s.a[i] = load4(A, m0 + (idx >> 3), k0 + 4 * (idx & 7), lda, M, K, a_vec);
-    s.b[i] = load4(B, k0 + (idx >> 5), n0 + 4 * (idx & 31), ldb, K, N, b_vec);
+  }
+#pragma unroll
+  for (int i = 0; i < T::NB; ++i) {
+    const int idx = tid + kThreads * i;
+    s.b[i] = load4(B, k0 + idx / T::BROW, n0 + 4 * (idx % T::BROW), ldb, K, N, b_vec);
   }
 }
 
@@ -85,11 +106,7 @@ __device__ __forceinline__ void load_slab(Slab &s, const float *__restrict__ A, 
 // that exist (A: tile rows m0.. below M; B: slab rows k0.. below K), so
 // rows past the matrix read 0 through the hardware range check; a float4
 // past K (A) or N (B) is sent to an offset outside the resource and reads 0
-// as well. No branches, 32-bit offsets: the loop issues exactly 8 loads.
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor: 32-bit data format
-constexpr uint32_t kOutside = 0x80000000u;
-
+// as well. No branches, 32-bit offsets.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float *base, int64_t rows, int64_t ld) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, (int)(rows * ld * 4), kRsrcWord3);
 }
@@ -98,53 +115,68 @@ __device__ __forceinline__ float4 as_float4(u32x4 u) {
   return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
 }
 
-__device__ __forceinline__ void load_slab_vec(Slab &s, const float *__restrict__ A, const float *__restrict__ B,
+template <int WT>
+__device__ __forceinline__ void load_slab_vec(Slab<WT> &s, const float *__restrict__ A, const float *__restrict__ B,
                                               int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                                               int64_t m0, int64_t n0, int64_t k0, int tid) {
-  const __amdgpu_buffer_rsrc_t ra = rows_rsrc(A + m0 * lda, (M - m0) < BM ? (M - m0) : BM, lda);
+  using T = Tile<WT>;
+  const __amdgpu_buffer_rsrc_t ra = rows_rsrc(A + m0 * lda, (M - m0) < T::BM ? (M - m0) : T::BM, lda);
   const __amdgpu_buffer_rsrc_t rb = rows_rsrc(B + k0 * ldb, (K - k0) < BK ? (K - k0) : BK, ldb);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < T::NA; ++i) {
     const int idx = tid + kThreads * i;
-    const int ar = idx >> 3, ak = 4 * (idx & 7);   // A: row in tile, k in slab
-    const int bk = idx >> 5, bn = 4 * (idx & 31);  // B: k in slab, column in tile
+    const int ar = idx >> 3, ak = 4 * (idx & 7);  // A: row in tile, k in slab
     const uint32_t aoff = (k0 + ak < K) ? (uint32_t)((ar * lda + k0 + ak) * 4) : kOutside;
-    const uint32_t boff = (n0 + bn < N) ? (uint32_t)((bk * ldb + n0 + bn) * 4) : kOutside;
     s.a[i] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(ra, aoff, 0, 0));
+  }
+#pragma unroll
+  for (int i = 0; i < T::NB; ++i) {
+    const int idx = tid + kThreads * i;
+    const int bk = idx / T::BROW, bn = 4 * (idx % T::BROW);  // B: k in slab, column in tile
+    const uint32_t boff = (n0 + bn < N) ? (uint32_t)((bk * ldb + n0 + bn) * 4) : kOutside;
     s.b[i] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(rb, boff, 0, 0));
   }
 }
 
-__device__ __forceinline__ void store_slab(const Slab &s, float *__restrict__ As, float *__restrict__ Bs, int tid) {
+template <int WT>
+__device__ __forceinline__ void store_slab(const Slab<WT> &s, float *__restrict__ As, float *__restrict__ Bs,
+                                           int tid) {
+  using T = Tile<WT>;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < T::NA; ++i) {
     const int idx = tid + kThreads * i;
     *reinterpret_cast<float4 *>(As + (idx >> 3) * LDA + 4 * (idx & 7)) = s.a[i];
-    *reinterpret_cast<float4 *>(Bs + (idx >> 5) * LDB + 4 * (idx & 31)) = s.b[i];
+  }
+#pragma unroll
+  for (int i = 0; i < T::NB; ++i) {
+    const int idx = tid + kThreads * i;
+    *reinterpret_cast<float4 *>(Bs + (idx / T::BROW) * T::LDB + 4 * (idx % T::BROW)) = s.b[i];
   }
 }
 
-__device__ __forceinline__ void compute_slab(v16f (&acc)[2][2], const float *__restrict__ As,
+template <int WT>
+__device__ __forceinline__ void compute_slab(v16f (&acc)[WT][WT], const float *__restrict__ As,
                                              const float *__restrict__ Bs, int wm, int wn, int lane) {
+  using T = Tile<WT>;
   const int r = lane & 31, h = lane >> 5;
 #pragma unroll
   for (int c = 0; c < BK / 8; ++c) {
-    float4 a[2];
-    float b[2][4];
+    float4 a[WT];
+    float b[WT][4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      a[i] = *reinterpret_cast<const float4 *>(As + (wm * 64 + i * 32 + r) * LDA + 8 * c + 4 * h);
+    for (int i = 0; i < WT; ++i)
+      a[i] = *reinterpret_cast<const float4 *>(As + (wm * 32 * WT + i * 32 + r) * LDA + 8 * c + 4 * h);
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < WT; ++j)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) b[j][s] = Bs[(8 * c + 4 * h + s) * LDB + wn * 64 + j * 32 + r];
+      for (int s = 0; s < 4; ++s) b[j][s] = Bs[(8 * c + 4 * h + s) * T::LDB + wn * 32 * WT + j * 32 + r];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < WT; ++i) {
         const float av = s == 0 ? a[i].x : s == 1 ? a[i].y : s == 2 ? a[i].z : a[i].w;
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < WT; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, b[j][s], acc[i][j], 0, 0, 0);
       }
     }
@@ -165,20 +197,21 @@ __device__ __forceinline__ void tile_coords(int64_t pid, int64_t tiles_m, int64_
 }
 
 // One workgroup's loop over its tiles. VEC selects the fast slab loads.
-template <bool VEC>
+// As, Bs: the two LDS stages, A_STAGE and B_STAGE floats apart. (Offsets
+// from one base keep the pointers visibly in LDS for the compiler; an array
+// of stage pointers would turn every LDS access into a flat one.)
+template <int WT, bool VEC>
 __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const float *__restrict__ Bp,
                                            float *__restrict__ Cp, int64_t M, int64_t N, int64_t K, int64_t lda,
                                            int64_t ldb, int64_t ldc, bool a_vec, bool b_vec, float *As,
                                            float *Bs) {
-  // As, Bs: the two LDS stages, BM*LDA and BK*LDB floats apart. (Offsets
-  // from one base keep the pointers visibly in LDS for the compiler; an
-  // array of stage pointers would turn every LDS access into a flat one.)
+  using T = Tile<WT>;
   const int tid = threadIdx.x;
   const int lane = kh::lane_id();
   const int wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int64_t tiles_m = (M + T::BM - 1) / T::BM, tiles_n = (N + T::BN - 1) / T::BN;
   const int64_t total = tiles_m * tiles_n;
   const int64_t nslabs = (K + BK - 1) / BK;
   const int64_t nblocks = (int64_t)gridDim.x * gridDim.y * gridDim.z;
@@ -188,30 +221,30 @@ __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const f
   for (int64_t pid = bid; pid < total; pid += nblocks) {
     int64_t tm, tn;
     tile_coords(pid, tiles_m, tiles_n, xcd_remap, tm, tn);
-    const int64_t m0 = tm * BM, n0 = tn * BN;
+    const int64_t m0 = tm * T::BM, n0 = tn * T::BN;
 
-    v16f acc[2][2];
+    v16f acc[WT][WT];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < WT; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
+      for (int j = 0; j < WT; ++j) acc[i][j] = v16f{};
 
-    auto load = [&](Slab &sl, int64_t k0) __attribute__((always_inline)) {
+    auto load = [&](Slab<WT> &sl, int64_t k0) __attribute__((always_inline)) {
       if (VEC)
-        load_slab_vec(sl, Ap, Bp, M, N, K, lda, ldb, m0, n0, k0, tid);
+        load_slab_vec<WT>(sl, Ap, Bp, M, N, K, lda, ldb, m0, n0, k0, tid);
       else
-        load_slab(sl, Ap, Bp, M, N, K, lda, ldb, m0, n0, k0, a_vec, b_vec, tid);
+        load_slab<WT>(sl, Ap, Bp, M, N, K, lda, ldb, m0, n0, k0, a_vec, b_vec, tid);
     };
-    Slab s;
+    Slab<WT> s;
     load(s, 0);
-    store_slab(s, As, Bs, tid);
+    store_slab<WT>(s, As, Bs, tid);
     __syncthreads();
     for (int64_t ks = 0; ks < nslabs; ++ks) {
       const int cur = ks & 1;
       const bool more = ks + 1 < nslabs;
       if (more) load(s, (ks + 1) * BK);
-      compute_slab(acc, As + cur * (BM * LDA), Bs + cur * (BK * LDB), wm, wn, lane);
-      if (more) store_slab(s, As + (cur ^ 1) * (BM * LDA), Bs + (cur ^ 1) * (BK * LDB), tid);
+      compute_slab<WT>(acc, As + cur * T::A_STAGE, Bs + cur * T::B_STAGE, wm, wn, lane);
+      if (more) store_slab<WT>(s, As + (cur ^ 1) * T::A_STAGE, Bs + (cur ^ 1) * T::B_STAGE, tid);
       __syncthreads();
     }
 
@@ -219,13 +252,13 @@ __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const f
     // column l%32 of the 32x32 block.
     const int col = lane & 31, h = lane >> 5;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < WT; ++i) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int64_t gc = n0 + wn * 64 + j * 32 + col;
+      for (int j = 0; j < WT; ++j) {
+        const int64_t gc = n0 + wn * 32 * WT + j * 32 + col;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int64_t gr = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          const int64_t gr = m0 + wm * 32 * WT + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
           if (gr < M && gc < N) Cp[gr * ldc + gc] = acc[i][j][r];
         }
       }
@@ -233,25 +266,37 @@ __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const f
   }
 }
 
-}  // namespace
-
-extern "C" __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
-gemm(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
-  const float *__restrict__ Ap = KH_PTR(A);
-  const float *__restrict__ Bp = KH_PTR(B);
-  float *__restrict__ Cp = KH_PTR(C);
-  const int64_t M = A_n0, K = A_n1, N = B_n1;
-  const int64_t lda = A_s0, ldb = B_s0, ldc = C_s0;
-
-  __shared__ __attribute__((aligned(16))) float As[2][BM * LDA];
-  __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDB];
-
+template <int WT>
+__device__ __forceinline__ void gemm_entry(const float *__restrict__ Ap, const float *__restrict__ Bp,
+                                           float *__restrict__ Cp, int64_t M, int64_t N, int64_t K, int64_t lda,
+                                           int64_t ldb, int64_t ldc) {
+  using T = Tile<WT>;
+  __shared__ __attribute__((aligned(16))) float As[2 * T::A_STAGE];
+  __shared__ __attribute__((aligned(16))) float Bs[2 * T::B_STAGE];
   const bool a_vec = ((K & 3) == 0) && ((lda & 3) == 0) && kh::aligned16(Ap);
   const bool b_vec = ((N & 3) == 0) && ((ldb & 3) == 0) && kh::aligned16(Bp);
   // The fast loads address a tile's rows with 32-bit byte offsets.
-  const bool fits32 = (int64_t)BM * lda * 4 < (1ll << 31) && (int64_t)BK * ldb * 4 < (1ll << 31);
+  const bool fits32 = (int64_t)T::BM * lda * 4 < (1ll << 31) && (int64_t)BK * ldb * 4 < (1ll << 31);
   if (a_vec && b_vec && fits32)
-    gemm_tiles<true>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, &As[0][0], &Bs[0][0]);
+    gemm_tiles<WT, true>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, As, Bs);
   else
-    gemm_tiles<false>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, &As[0][0], &Bs[0][0]);
+    gemm_tiles<WT, false>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, As, Bs);
+}
+
+}  // namespace
+
+static_assert(Tile<2>::BM == KH_GEMM_BM && Tile<2>::BN == KH_GEMM_BN, "launcher tile size");
+static_assert(Tile<1>::BM == KH_GEMM_SMALL_BM && Tile<1>::BN == KH_GEMM_SMALL_BN, "launcher tile size");
+
+// The reference symbol: 128x128 tiles.
+extern "C" __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+gemm(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
+  gemm_entry<2>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
+}
+
+// Same arguments and results with 64x64 tiles, for problems whose 128x128
+// grid would leave CUs idle.
+extern "C" __global__ void __launch_bounds__(kThreads)
+gemm_small(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
+  gemm_entry<1>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
 }

@@ -190,7 +190,9 @@ int geometry(const char *name, const Shape &s, khrt_dim3 &grid, khrt_dim3 &block
     if (!need(s, "m", m) || !need(s, "n", n) || !need(s, "k", k)) {
       return khrt::fail(KHRT_E_INVALID, "gemm: shape attributes 'm', 'n' and 'k' are required and must be positive");
     }
-    grid.x = clamp_grid(ceil_div(m, KH_GEMM_BM) * ceil_div(n, KH_GEMM_BN));
+    const int64_t tiles = ceil_div(m, KH_GEMM_BM) * ceil_div(n, KH_GEMM_BN);
+    grid.x = clamp_grid(tiles < KH_GEMM_SMALL_TILES ? ceil_div(m, KH_GEMM_SMALL_BM) * ceil_div(n, KH_GEMM_SMALL_BN)
+                                                    : tiles);
   } else if (t == "attention") {
     if (!need(s, "batch", b) || !need(s, "heads", h) || !need(s, "seq", seq) || !need(s, "head_dim", d)) {
       return khrt::fail(KHRT_E_INVALID,
@@ -219,6 +221,13 @@ const char *launch_symbol(const Template *t, const Shape &s) {
     auto it = s.find("cols");
     if (it != s.end() && it->second > 1024 && it->second <= 4096 && (it->second & 3) == 0) {
       return n == "softmax" ? "softmax_wide" : "layernorm_wide";
+    }
+  }
+  if (n == "gemm") {
+    auto m = s.find("m"), nn = s.find("n");
+    if (m != s.end() && nn != s.end() &&
+        ceil_div(m->second, KH_GEMM_BM) * ceil_div(nn->second, KH_GEMM_BN) < KH_GEMM_SMALL_TILES) {
+      return "gemm_small";
     }
   }
   return t->name;

@@ -262,6 +262,9 @@ def test_kernarg_segment_is_2n_plus_3_slots(name, nslots):
     ("scan", "n=1000000", (66, 1, 1), (1024, 1, 1)),
     ("scan", "n=67108864", (4370, 1, 1), (1024, 1, 1)),
     ("gemm", "m=8192,n=8192,k=8192", (4096, 1, 1), (256, 1, 1)),
+    ("gemm", "m=4096,n=4096,k=64", (1024, 1, 1), (256, 1, 1)),       # 128x128 tiles: 1024
+    ("gemm", "m=2048,n=2048,k=2048", (1024, 1, 1), (256, 1, 1)),     # 64x64 tiles (gemm_small)
+    ("gemm", "m=512,n=512,k=512", (64, 1, 1), (256, 1, 1)),
     ("attention", "batch=4,heads=16,seq=4096,head_dim=64", (32, 16, 4), (256, 1, 1)),
 ])
 def test_launcher_geometry(name, shape, grid, block):

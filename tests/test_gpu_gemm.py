@@ -8,6 +8,8 @@
   reference (e2e_gemm_test.cpp:281); 8192^3 is checked on a row sample.
 * Ragged shapes, the reference launch geometry, and the A*B^T negative
   control (e2e_gemm_test.cpp:289-375).
+* Both tile symbols (`gemm` 128x128, `gemm_small` 64x64) give the same
+  results at every shape, whichever the launcher would pick.
 """
 import numpy as np
 import pytest
@@ -82,3 +84,25 @@ def test_gemm_reference_geometry_and_negative_control(dev):
     assert np.array_equal(C, O.ref_gemm(A, B, m, n, k).astype(np.float32))
     wrong = O.ref_gemm(A, B, m, n, k, transpose_b=True)
     assert O.rel_frobenius(C, wrong) > 1e-5
+
+
+@pytest.mark.parametrize("symbol", ["gemm", "gemm_small"])
+@pytest.mark.parametrize("m,n,k", [(256, 256, 256), (1000, 1000, 1000), (64, 192, 4097), (129, 65, 33),
+                                   (3, 5, 7), (512, 2048, 96)])
+def test_every_gemm_symbol_at_every_shape(dev, symbol, m, n, k):
+    # Integer fill: exact in fp32, so both tilings must agree bit for bit.
+    A, B = O.gemm_int_inputs(m, n, k) if k <= 4096 else (None, None)
+    if A is None:
+        A = O.uniform(m * k, 3, -1.0, 1.0).reshape(m, k)
+        B = O.uniform(k * n, 4, -1.0, 1.0).reshape(k, n)
+    mod = kh.GpuModule(kh.code_object("gemm"))
+    f = mod.get_function(symbol)
+    dA, dB, dC = up(A), up(B), empty(m * n)
+    args = kh.LaunchArgs().add_memref(dA, [m, k]).add_memref(dB, [k, n]).add_memref(dC, [m, n])
+    say(f"{symbol} m={m} n={n} k={k}")
+    kh.kernel_launch(f, (37, 1, 1), (256, 1, 1), args)  # grid-strided: any grid
+    C = down(dC, m * n).reshape(m, n)
+    if k <= 4096:
+        assert np.array_equal(C, (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
+    else:
+        assert O.rel_frobenius(C, O.ref_gemm(A, B, m, n, k)) <= 1e-5
