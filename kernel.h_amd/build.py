@@ -6,6 +6,7 @@ Outputs under kernel.h_amd/build/:
   co/<name>.notes.json resource notes per kernel symbol
   gen/kh_embed.S       .incbin of every product code object
   gen/kh_resources.inc resource table compiled into the runtime
+  gen/kh_cli_embed.S   .incbin of the CLI-only comparator code object (hipref)
   libkhrt.so           the C-ABI runtime (include/khrt.h)
   kernelh              the CLI (compile / bench / occupancy)
 
@@ -44,6 +45,8 @@ OBJ = os.path.join(BUILD, "obj")
 PRODUCT = ["vecadd", "fused_gelu", "softmax", "layernorm", "scan", "gemm", "attention", "util", "roofline"]
 # Test-only code objects (loaded by tests through khrt_module_load_data).
 PROBES = ["mfma_probe"]
+# Bench-only comparators (csrc/cli/*.hip), embedded in the kernelh CLI.
+CLI_CODE_OBJECTS = ["hipref"]
 
 DEVICE_FLAGS = [
     "-x", "hip", f"--offload-arch={ARCH}", "--cuda-device-only", "--no-gpu-bundle-output",
@@ -79,8 +82,8 @@ def run(cmd, verbose=False, **kw):
     return r.stdout
 
 
-def compile_co(name: str, verbose: bool) -> str:
-    src = os.path.join(KDIR, name + ".hip")
+def compile_co(name: str, verbose: bool, srcdir: str = "") -> str:
+    src = os.path.join(srcdir or KDIR, name + ".hip")
     out = os.path.join(CO, name + ".hsaco")
     run([HIPCC, *DEVICE_FLAGS, *EXTRA_DEVICE_FLAGS.get(name, []), "-c", src, "-o", out], verbose)
     isa = run([OBJDUMP, "-d", f"--mcpu={ARCH}", out])
@@ -159,8 +162,10 @@ def build(jobs: int = 8, verbose: bool = False) -> None:
         os.makedirs(d, exist_ok=True)
 
     srcs = [n for n in PRODUCT + PROBES if os.path.exists(os.path.join(KDIR, n + ".hip"))]
+    cli_cos = [n for n in CLI_CODE_OBJECTS if os.path.exists(os.path.join(CLIDIR, n + ".hip"))]
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         outs = dict(zip(srcs, ex.map(lambda n: compile_co(n, verbose), srcs)))
+        cli_outs = dict(zip(cli_cos, ex.map(lambda n: compile_co(n, verbose, CLIDIR), cli_cos)))
     present = {n: p for n, p in outs.items() if n in PRODUCT}
 
     # Refuse spills into scratch in product kernels: they would silently
@@ -193,8 +198,23 @@ def build(jobs: int = 8, verbose: bool = False) -> None:
     cli_srcs = sorted(os.path.join(CLIDIR, f) for f in os.listdir(CLIDIR) if f.endswith(".cpp")) \
         if os.path.isdir(CLIDIR) else []
     if cli_srcs:
-        run([CXX, *HOST_FLAGS, "-o", os.path.join(BUILD, "kernelh"), *cli_srcs, f"-L{BUILD}", "-lkhrt",
-             "-Wl,-rpath,$ORIGIN", f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib"], verbose)
+        lines = ["/* Generated by kernel.h_amd/build.py: CLI comparator code objects. */",
+                 '\t.section .rodata.kh_cli_co,"a",@progbits']
+        for name in CLI_CODE_OBJECTS:
+            lines += ["\t.p2align 12", f"\t.globl kh_cli_co_{name}", f"\t.globl kh_cli_co_{name}_end",
+                      f"kh_cli_co_{name}:"]
+            if name in cli_outs:
+                lines.append(f'\t.incbin "{cli_outs[name]}"')
+            lines.append(f"kh_cli_co_{name}_end:")
+        lines += ["\t.byte 0", '\t.section .note.GNU-stack,"",@progbits', ""]
+        cli_embed = os.path.join(GEN, "kh_cli_embed.S")
+        with open(cli_embed, "w") as f:
+            f.write("\n".join(lines))
+        cli_embed_obj = os.path.join(OBJ, "kh_cli_embed.o")
+        run([CXX, "-c", cli_embed, "-o", cli_embed_obj], verbose)
+        run([CXX, *HOST_FLAGS, "-o", os.path.join(BUILD, "kernelh"), *cli_srcs, cli_embed_obj, f"-L{BUILD}",
+             "-lkhrt", "-ldl", "-Wl,-rpath,$ORIGIN", f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib"],
+            verbose)
     if verbose:
         print("built", lib)
 

@@ -1,0 +1,39 @@
+// Comparator rows for `kernelh bench`: the hand-written HIP baselines
+// (hipref-naive / hipref-vec, roofline_fma) from the code object embedded in
+// the CLI, and rocBLAS fp32 GEMM as the vendor comparator.
+//
+// Mirrors the reference's bench backends (bench/harness/hipref_backend.cpp,
+// rocblas_backend.cpp, roofline.cpp:100-145): same symbols, launch geometry
+// and metric formulas, so results.csv rows are comparable.
+#pragma once
+
+#include <cstdint>
+#include <functional>
+#include <map>
+#include <string>
+#include <vector>
+
+namespace khcli {
+
+// Device buffers owned by one bench row, freed when it goes out of scope.
+struct Bufs {
+  std::vector<void *> ptrs;
+  ~Bufs();
+  // `count` floats filled with `fill` (nullptr on allocation failure).
+  float *alloc(int64_t count, float fill);
+};
+
+// Prepares a hipref-naive / hipref-vec row (`variant` "naive" or "vec4").
+bool prepare_hipref(const std::string &kernel, const std::string &variant,
+                    const std::map<std::string, int64_t> &shape, Bufs &b, std::function<int()> &launch,
+                    double &work, bool &flops, std::string &error);
+
+// The vector-ALU FMA ceiling row (2^22 elements x 8192 FMAs, 2 FLOP each).
+bool prepare_roofline_fma(Bufs &b, std::function<int()> &launch, double &work, std::string &error);
+
+// rocBLAS sgemm for a row-major m x k by k x n product (dlopen'ed; an
+// error, not a crash, when librocblas is absent).
+bool prepare_rocblas_gemm(const std::map<std::string, int64_t> &shape, Bufs &b, std::function<int()> &launch,
+                          double &work, std::string &error);
+
+}  // namespace khcli

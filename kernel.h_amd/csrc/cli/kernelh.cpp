@@ -3,8 +3,8 @@
 // The reference's CLI surface for this path (tools/kernelh/main.cpp):
 //   kernelh compile --kernel <name> --shape k=v,... --target <t> --out <dir>
 //                   [--resources]                          (main.cpp:435-646)
-//   kernelh bench   --suite <roofline|kernelh|all> --out <path>
-//                   [--occupancy] [--kernel <name> --shape ...]
+//   kernelh bench   --suite <roofline|kernelh|rocblas|hipref|all> --out <path>
+//                   [--occupancy] [--kernel <name> --shape ... [--backend <b>]]
 //                                                          (main.cpp:2154-2228)
 // Exit codes as in the reference (main.cpp:125-127, run_bench.hpp:9-10):
 // 0 ok, 1 operational failure, 2 usage error, 77 skipped (no GPU).
@@ -16,12 +16,18 @@
 // the code objects read sizes from the memref descriptors at run time, so
 // one object serves every shape.
 //
+// bench backends (bench/harness/run_bench.cpp:48-66): kernelh (the gfx950
+// templates), rocblas (vendor fp32 GEMM), hipref-naive / hipref-vec
+// (hand-written HIP comparators embedded in this executable) and roofline
+// (triad bandwidth, vector FMA ceiling).
 // bench times each row with the reference's method: 5 warmup launches, then
 // the median of 20 event-timed launches (bench/harness/timer.cpp:29-67), and
 // writes the G32 results.csv schema
 // kernel,shape,backend,ms_median,gflops_or_gbps,timestamp,device
 // (bench/harness/csv.cpp:9-10).
 #include "khrt.h"
+
+#include "comparators.hpp"
 
 #include <algorithm>
 #include <chrono>
@@ -60,7 +66,9 @@ void usage(std::ostream &os) {
      << "  --out <dir>           write <dir>/<kernel>.{hsaco,isa} (created if missing)\n"
      << "  --resources           also write <dir>/resources.json\n\n"
      << "bench options:\n"
-     << "  --suite <name>        roofline, kernelh, all (default: all)\n"
+     << "  --suite <name>        roofline, kernelh, rocblas, hipref, all (default: all)\n"
+     << "  --backend <name>      with --kernel: kernelh (default), rocblas, hipref-naive,\n"
+     << "                        hipref-vec, roofline\n"
      << "  --kernel <name>       single-row mode: time one template ...\n"
      << "  --shape k=v,...       ... at this shape\n"
      << "  --out <path>          results.csv path or directory (required)\n"
@@ -245,35 +253,43 @@ int run_compile(int argc, char **argv) {
 
 struct Row {
   std::string kernel, shape;
-  double work = 0.0;  // bytes or FLOPs per launch
-  bool flops = false;
+  std::string backend = "kernelh";  // kernelh, rocblas, hipref-naive, hipref-vec, roofline
 };
 
-struct Bufs {
-  std::vector<void *> ptrs;
-  ~Bufs() {
-    for (void *p : ptrs) khrt_free(p);
-  }
-  float *alloc(int64_t count, float fill) {
-    void *p = nullptr;
-    if (khrt_malloc(&p, static_cast<size_t>(std::max<int64_t>(count, 1)) * 4) != 0) return nullptr;
-    ptrs.push_back(p);
-    khrt_fill_f32(p, fill, static_cast<size_t>(count), nullptr);
-    return static_cast<float *>(p);
-  }
-};
+using khcli::Bufs;
 
 int64_t get(const std::map<std::string, int64_t> &s, const char *k, int64_t dflt = 0) {
   auto it = s.find(k);
   return it == s.end() ? dflt : it->second;
 }
 
-// Allocates the row's buffers and returns a launcher closure.
-bool prepare(const Row &row, Bufs &b, std::function<int()> &launch, double &work, bool &flops) {
+// Allocates the row's buffers and returns a launcher closure. Rates use the
+// reference's formulas (bench/harness/metrics.cpp), so rows compare across
+// backends: bytes for the bandwidth kernels, 2mnk / 4bhs^2d FLOPs.
+bool prepare(const Row &row, Bufs &b, std::function<int()> &launch, double &work, bool &flops, std::string &error) {
   std::map<std::string, int64_t> s;
-  if (!parse_shape(row.shape, s)) return false;
+  if (!parse_shape(row.shape, s)) {
+    error = "malformed shape";
+    return false;
+  }
   const std::string &k = row.kernel;
   flops = false;
+  if (row.backend == "hipref-naive" || row.backend == "hipref-vec") {
+    return khcli::prepare_hipref(k, row.backend == "hipref-vec" ? "vec4" : "naive", s, b, launch, work, flops, error);
+  }
+  if (row.backend == "rocblas") {
+    if (k != "gemm") {
+      error = "rocblas backend only benchmarks gemm (got '" + k + "')";
+      return false;
+    }
+    flops = true;
+    return khcli::prepare_rocblas_gemm(s, b, launch, work, error);
+  }
+  if (k == "roofline_fma") {
+    flops = true;
+    return khcli::prepare_roofline_fma(b, launch, work, error);
+  }
+  error = "unknown kernel or allocation failure";
   if (k == "vecadd") {
     const int64_t n = get(s, "n");
     float *a = b.alloc(n, 1.0f), *bb = b.alloc(n, 2.0f), *c = b.alloc(n, 0.0f);
@@ -283,7 +299,7 @@ bool prepare(const Row &row, Bufs &b, std::function<int()> &launch, double &work
     const int64_t n = s.count("n") ? get(s, "n") : get(s, "rows") * get(s, "cols");
     float *x = b.alloc(n, 0.25f), *o = b.alloc(n, 0.0f);
     launch = [=] { return kh_fused_gelu(x, nullptr, o, n, nullptr); };
-    work = 8.0 * n;
+    work = 12.0 * n;  // fused_gelu_bytes counts the (dead) tmp stream too
   } else if (k == "softmax" || k == "layernorm") {
     const int64_t r = get(s, "rows"), c = get(s, "cols");
     float *x = b.alloc(r * c, 0.5f), *y = b.alloc(r * c, 0.0f);
@@ -358,28 +374,68 @@ std::string now_iso() {
   return buf;
 }
 
-std::vector<Row> suite_rows(const std::string &suite) {
+// Suites as in the reference (bench/harness/suites.cpp:22-101), with the
+// BASELINE configurations added to the kernelh suite.
+std::vector<Row> gemm_rows(const std::string &backend) {
   std::vector<Row> rows;
-  if (suite == "roofline" || suite == "all") rows.push_back({"roofline_triad", "n=268435456"});
-  if (suite == "kernelh" || suite == "all") {
-    rows.push_back({"vecadd", "n=16777216"});
-    rows.push_back({"gemm", "m=512,n=512,k=512"});
-    rows.push_back({"gemm", "m=2048,n=2048,k=2048"});
-    rows.push_back({"gemm", "m=8192,n=8192,k=8192"});
-    rows.push_back({"gemm", "m=8192,n=8192,k=256"});
-    rows.push_back({"softmax", "rows=4096,cols=1024"});
-    rows.push_back({"softmax", "rows=16384,cols=4096"});
-    rows.push_back({"layernorm", "rows=4096,cols=1024"});
-    rows.push_back({"layernorm", "rows=16384,cols=4096"});
-    rows.push_back({"scan", "n=1000000"});
-    rows.push_back({"scan", "n=67108864"});
-    rows.push_back({"fused_gelu", "n=4194304"});
-    rows.push_back({"fused_gelu", "n=67108864"});
-    rows.push_back({"attention", "batch=2,heads=8,seq=1024,head_dim=64"});
-    rows.push_back({"attention", "batch=4,heads=16,seq=1024,head_dim=64"});
-    rows.push_back({"attention", "batch=4,heads=16,seq=4096,head_dim=64"});
+  for (const int64_t n : {512, 1024, 2048, 4096, 8192}) {
+    const std::string d = std::to_string(n);
+    rows.push_back({"gemm", "m=" + d + ",n=" + d + ",k=" + d, backend});
   }
   return rows;
+}
+
+std::vector<Row> kernelh_rows() {
+  std::vector<Row> rows = gemm_rows("kernelh");
+  rows.push_back({"gemm", "m=8192,n=8192,k=256"});
+  rows.push_back({"vecadd", "n=16777216"});
+  for (const char *shape : {"rows=4096,cols=1024", "rows=16384,cols=4096"}) {
+    rows.push_back({"softmax", shape});
+    rows.push_back({"layernorm", shape});
+  }
+  for (const char *n : {"n=100000", "n=1000000", "n=67108864"}) rows.push_back({"scan", n});
+  for (const char *n : {"n=1048576", "n=4194304", "n=67108864"}) rows.push_back({"fused_gelu", n});
+  for (const char *shape : {"batch=2,heads=8,seq=512,head_dim=64", "batch=2,heads=8,seq=1024,head_dim=64",
+                            "batch=4,heads=16,seq=1024,head_dim=64", "batch=4,heads=16,seq=4096,head_dim=64"})
+    rows.push_back({"attention", shape});
+  return rows;
+}
+
+std::vector<Row> hipref_rows() {
+  std::vector<Row> rows;
+  for (const char *shape : {"rows=4096,cols=1024", "rows=16384,cols=4096"}) {
+    for (const char *k : {"softmax", "layernorm"}) {
+      rows.push_back({k, shape, "hipref-naive"});
+      rows.push_back({k, shape, "hipref-vec"});
+    }
+  }
+  for (const char *n : {"n=100000", "n=1000000"}) {
+    rows.push_back({"scan", n, "hipref-naive"});
+    rows.push_back({"scan", n, "hipref-vec"});
+  }
+  for (const char *n : {"n=1048576", "n=4194304"}) {
+    rows.push_back({"fused_gelu", n, "hipref-naive"});
+    rows.push_back({"fused_gelu", n, "hipref-vec"});
+  }
+  rows.push_back({"gemm", "m=512,n=512,k=512", "hipref-naive"});
+  rows.push_back({"gemm", "m=1024,n=1024,k=1024", "hipref-naive"});
+  return rows;
+}
+
+std::vector<Row> suite_rows(const std::string &suite) {
+  std::vector<Row> rows;
+  auto add = [&rows](const std::vector<Row> &more) { rows.insert(rows.end(), more.begin(), more.end()); };
+  if (suite == "roofline" || suite == "all") {
+    add({{"roofline_triad", "n=268435456", "roofline"}, {"roofline_fma", "n=4194304", "roofline"}});
+  }
+  if (suite == "kernelh" || suite == "all") add(kernelh_rows());
+  if (suite == "rocblas" || suite == "all") add(gemm_rows("rocblas"));
+  if (suite == "hipref" || suite == "all") add(hipref_rows());
+  return rows;
+}
+
+bool known_suite(const std::string &s) {
+  return s == "all" || s == "roofline" || s == "kernelh" || s == "rocblas" || s == "hipref";
 }
 
 int write_occupancy(const fs::path &dir, const std::vector<std::string> &kernels) {
@@ -426,7 +482,7 @@ int write_occupancy(const fs::path &dir, const std::vector<std::string> &kernels
 }
 
 int run_bench(int argc, char **argv) {
-  std::string suite = "all", out, kernel, shape, v;
+  std::string suite = "all", out, kernel, shape, backend = "kernelh", v;
   int warmup = 5, iters = 20;
   bool occupancy = false;
   for (int i = 2; i < argc; ++i) {
@@ -442,6 +498,8 @@ int run_bench(int argc, char **argv) {
       kernel = v;
     } else if (take(argc, argv, i, arg, "--shape", v)) {
       shape = v;
+    } else if (take(argc, argv, i, arg, "--backend", v)) {
+      backend = v;
     } else if (take(argc, argv, i, arg, "--warmup", v)) {
       warmup = std::atoi(v.c_str());
     } else if (take(argc, argv, i, arg, "--iters", v)) {
@@ -453,9 +511,12 @@ int run_bench(int argc, char **argv) {
       return kExitUsage;
     }
   }
-  if (out.empty() || (suite != "all" && suite != "roofline" && suite != "kernelh") || iters < 1 || warmup < 0 ||
+  const bool known_backend = backend == "kernelh" || backend == "rocblas" || backend == "hipref-naive" ||
+                             backend == "hipref-vec" || backend == "roofline";
+  if (out.empty() || !known_suite(suite) || !known_backend || iters < 1 || warmup < 0 ||
       (!kernel.empty() && shape.empty())) {
-    std::cerr << "error: bench needs --out, a suite of roofline|kernelh|all, and --shape with --kernel\n";
+    std::cerr << "error: bench needs --out, a suite of roofline|kernelh|rocblas|hipref|all, a backend of "
+                 "kernelh|rocblas|hipref-naive|hipref-vec|roofline, and --shape with --kernel\n";
     return kExitUsage;
   }
   fs::path csv = out;
@@ -476,7 +537,7 @@ int run_bench(int argc, char **argv) {
   khrt_device_info info{};
   khrt_get_device_info(&info);
   const std::string device = std::string(info.name[0] ? info.name : "AMD Instinct MI355X") + " (" + info.arch + ")";
-  std::vector<Row> rows = kernel.empty() ? suite_rows(suite) : std::vector<Row>{{kernel, shape}};
+  std::vector<Row> rows = kernel.empty() ? suite_rows(suite) : std::vector<Row>{{kernel, shape, backend}};
   const bool fresh = !fs::exists(csv);
   std::ofstream f(csv, std::ios::app);
   if (fresh) f << "kernel,shape,backend,ms_median,gflops_or_gbps,timestamp,device\n";
@@ -487,19 +548,25 @@ int run_bench(int argc, char **argv) {
     double work = 0.0;
     bool flops = false;
     double ms = 0.0;
-    if (!prepare(row, b, launch, work, flops) || !time_row(launch, warmup, iters, ms)) {
-      std::cerr << "error: " << row.kernel << " " << row.shape << ": " << khrt_last_error() << "\n";
+    std::string error;
+    if (!prepare(row, b, launch, work, flops, error)) {
+      std::cerr << "error: " << row.backend << " " << row.kernel << " " << row.shape << ": " << error << "\n";
+      ++failures;
+      continue;
+    }
+    if (!time_row(launch, warmup, iters, ms)) {
+      std::cerr << "error: " << row.backend << " " << row.kernel << " " << row.shape << ": " << khrt_last_error()
+                << "\n";
       ++failures;
       continue;
     }
     const double rate = work * 1000.0 / ms / 1e9;  // GFLOP/s or GB/s (metrics.cpp:5-12)
-    const std::string backend = row.kernel.rfind("roofline", 0) == 0 ? "roofline" : "kernelh-gfx950";
     std::string shp = row.shape;
     std::replace(shp.begin(), shp.end(), ',', ';');
-    f << row.kernel << "," << shp << "," << backend << "," << ms << "," << rate << "," << now_iso() << ",\""
+    f << row.kernel << "," << shp << "," << row.backend << "," << ms << "," << rate << "," << now_iso() << ",\""
       << device << "\"\n";
-    std::printf("%-15s %-40s %10.4f ms %12.1f %s\n", row.kernel.c_str(), row.shape.c_str(), ms, rate,
-                flops ? "GFLOP/s" : "GB/s");
+    std::printf("%-13s %-15s %-40s %10.4f ms %12.1f %s\n", row.backend.c_str(), row.kernel.c_str(),
+                row.shape.c_str(), ms, rate, flops ? "GFLOP/s" : "GB/s");
   }
   std::cout << "wrote " << csv.string() << "\n";
   if (occupancy) {

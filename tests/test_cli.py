@@ -55,6 +55,9 @@ def test_usage_errors_exit_2(tmp_path):
     assert run("compile", "--kernel", "vecadd", "--out", str(tmp_path)).returncode == 2  # no --shape
     assert run("compile", "--kernel", "vecadd", "--shape", "n", "--out", str(tmp_path)).returncode == 2
     assert run("bench").returncode == 2  # no --out
+    assert run("bench", "--suite", "cuda-cross", "--out", str(tmp_path)).returncode == 2  # not built here
+    assert run("bench", "--kernel", "gemm", "--shape", "m=8,n=8,k=8", "--backend", "cublas",
+               "--out", str(tmp_path)).returncode == 2
     assert run("--help").returncode == 0
 
 
@@ -80,8 +83,26 @@ def test_bench_single_row_results_csv(dev, tmp_path):
     assert r.returncode == 0, r.stdout
     rows = list(csv.DictReader(open(tmp_path / "results.csv")))
     assert list(rows[0].keys()) == ["kernel", "shape", "backend", "ms_median", "gflops_or_gbps", "timestamp", "device"]
-    assert rows[0]["kernel"] == "vecadd" and rows[0]["backend"] == "kernelh-gfx950"
+    assert rows[0]["kernel"] == "vecadd" and rows[0]["backend"] == "kernelh"
     assert float(rows[0]["ms_median"]) > 0 and float(rows[0]["gflops_or_gbps"]) > 100
     assert "gfx950" in rows[0]["device"]
     occ = (tmp_path / "occupancy.md").read_text()
     assert "| vecadd |" in occ
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kernel,shape,backend", [
+    ("gemm", "m=512,n=512,k=512", "rocblas"),
+    ("gemm", "m=512,n=512,k=512", "hipref-naive"),
+    ("softmax", "rows=4096,cols=1024", "hipref-vec"),
+    ("scan", "n=100000", "hipref-naive"),
+    ("roofline_fma", "n=4194304", "roofline"),
+])
+def test_bench_comparator_rows(dev, tmp_path, kernel, shape, backend):
+    # The reference's comparator backends (bench/harness/run_bench.cpp:48-66)
+    # produce rows in the same results.csv.
+    print(f"[gpu-case] kernelh bench --kernel {kernel} --backend {backend}", flush=True)
+    r = run("bench", "--kernel", kernel, "--shape", shape, "--backend", backend, "--out", str(tmp_path))
+    assert r.returncode == 0, r.stdout
+    rows = list(csv.DictReader(open(tmp_path / "results.csv")))
+    assert rows[0]["backend"] == backend and float(rows[0]["gflops_or_gbps"]) > 0
