@@ -6,20 +6,26 @@
 // 21 parameters. The reference computes one element per lane with scalar
 // FMAs out of an 8 KiB LDS tile (gemm.cpp:265-296). Here:
 //
-//   * Workgroup = 256 threads (4 wave64s, 2x2) computing a square tile of C;
-//     each wave owns a quarter as WT x WT MFMA 32x32 accumulators. Two
-//     symbols: `gemm` (WT = 2: 128x128 tiles, 64 accumulator registers per
-//     lane) and `gemm_small` (WT = 1: 64x64 tiles), which the launcher picks
-//     when the 128x128 grid would have too few tiles to fill the CUs
-//     (KH_GEMM_SMALL_TILES). Both are correct for every shape.
-//   * `gemm`'s registers are capped for two waves per SIMD (two workgroups
-//     per CU, as LDS allows), so one workgroup's barrier and slab hand-over
-//     overlap the other's MFMAs.
-//   * K advances in 32-wide slabs staged through LDS, double-buffered: the
+//   * Workgroup = 256 threads (4 wave64s, 2x2) computing a BM x BN tile of C;
+//     each wave owns a quarter as WTM x WTN MFMA 32x32 accumulators. Three
+//     symbols, all correct for every shape; the launcher picks by how many
+//     tiles each would launch:
+//       `gemm`        128x256 tiles (64x128 per wave, 128 accumulator registers
+//                     per lane), 16-deep K slabs: the least LDS and L2 traffic
+//                     per MFMA, for grids of at least KH_GEMM_TILES_256 tiles;
+//       `gemm_mid`    128x128 tiles (64x64 per wave), 32-deep slabs;
+//       `gemm_small`  64x64 tiles, for problems whose larger grids would leave
+//                     CUs idle.
+//     Registers are capped for two waves per SIMD (two workgroups per CU, as
+//     LDS allows), so one workgroup's barrier and slab hand-over overlap the
+//     other's MFMAs. `gemm` raises its waves' priority (s_setprio) while they
+//     issue MFMAs, so a wave that is feeding the matrix core wins issue over
+//     one that is loading the next slab (+1.5% at 8192^3).
+//   * K advances in 16- or 32-wide slabs staged through LDS, double-buffered: the
 //     next slab's global loads are in flight while the current slab feeds
 //     the MFMAs, one barrier per slab.
-//   * LDS holds A as [m][k] (rows padded to 36 floats: one ds_read_b128 per
-//     lane delivers four k values, every 8-lane group on distinct banks) and
+//   * LDS holds A as [m][k] (rows padded by 4 floats: one ds_read_b128 per
+//     lane delivers four k values, conflict-free) and
 //     B as [k][n] (rows padded by 4 floats; a half-wave reads 32 consecutive
 //     n with ds_read_b32). Both slabs arrive as dwordx4 loads: for aligned
 //     operands with k, n multiples of 4 as branch-free buffer loads whose
@@ -47,30 +53,31 @@ namespace {
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BK = 32;
-constexpr int LDA = BK + 4;  // A in LDS: [m][k], rows padded to 36 floats
 constexpr int kThreads = 256;
 constexpr int kGroupM = 8;
 constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor: 32-bit data format
 constexpr uint32_t kOutside = 0x80000000u;
 
-// Tile geometry for WT x WT accumulators per wave.
-template <int WT>
+// Tile geometry for WTM x WTN accumulators per wave, BKT-deep slabs.
+template <int WTM, int WTN, int BKT>
 struct Tile {
-  static constexpr int BM = 64 * WT;       // rows of C per workgroup
-  static constexpr int BN = 64 * WT;       // columns of C per workgroup
+  static constexpr int BK = BKT;
+  static constexpr int LDA = BK + 4;       // A in LDS: [m][k], padded rows
+  static constexpr int BM = 64 * WTM;      // rows of C per workgroup
+  static constexpr int BN = 64 * WTN;      // columns of C per workgroup
   static constexpr int LDB = BN + 4;       // B in LDS: [k][n], padded rows
+  static constexpr int AROW = BK / 4;      // float4 per A row
   static constexpr int NA = BM * BK / 4 / kThreads;  // A float4 per thread per slab
   static constexpr int NB = BK * BN / 4 / kThreads;  // B float4 per thread per slab
-  static constexpr int BROW = BN / 4;      // float4 per B row (lanes per B row)
+  static constexpr int BROW = BN / 4;      // float4 per B row
   static constexpr int A_STAGE = BM * LDA;
   static constexpr int B_STAGE = BK * LDB;
 };
 
-template <int WT>
+template <class T>
 struct Slab {
-  float4 a[Tile<WT>::NA];  // A: one row, 4 consecutive k each
-  float4 b[Tile<WT>::NB];  // B: one k row, 4 consecutive n each
+  float4 a[T::NA];
+  float4 b[T::NB];
 };
 
 __device__ __forceinline__ float4 load4(const float *__restrict__ P, int64_t row, int64_t col, int64_t ld,
@@ -83,16 +90,15 @@ __device__ __forceinline__ float4 load4(const float *__restrict__ P, int64_t row
 }
 
 // Generic slab load: any shape, stride and alignment (guarded per element).
-// A: 8 lanes cover a 32-k row; B: BN/4 lanes cover a row of the tile.
-template <int WT>
-__device__ __forceinline__ void load_slab(Slab<WT> &s, const float *__restrict__ A, const float *__restrict__ B,
+// A: BK/4 lanes cover a row of the slab; B: BN/4 lanes cover a row of the tile.
+template <class T>
+__device__ __forceinline__ void load_slab(Slab<T> &s, const float *__restrict__ A, const float *__restrict__ B,
                                           int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t m0,
                                           int64_t n0, int64_t k0, bool a_vec, bool b_vec, int tid) {
-  using T = Tile<WT>;
 #pragma unroll
   for (int i = 0; i < T::NA; ++i) {
     const int idx = tid + kThreads * i;
-    s.a[i] = load4(A, m0 + (idx >> 3), k0 + 4 * (idx & 7), lda, M, K, a_vec);
+    s.a[i] = load4(A, m0 + idx / T::AROW, k0 + 4 * (idx % T::AROW), lda, M, K, a_vec);
   }
 #pragma unroll
   for (int i = 0; i < T::NB; ++i) {
@@ -115,17 +121,16 @@ __device__ __forceinline__ float4 as_float4(u32x4 u) {
   return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
 }
 
-template <int WT>
-__device__ __forceinline__ void load_slab_vec(Slab<WT> &s, const float *__restrict__ A, const float *__restrict__ B,
+template <class T>
+__device__ __forceinline__ void load_slab_vec(Slab<T> &s, const float *__restrict__ A, const float *__restrict__ B,
                                               int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                                               int64_t m0, int64_t n0, int64_t k0, int tid) {
-  using T = Tile<WT>;
   const __amdgpu_buffer_rsrc_t ra = rows_rsrc(A + m0 * lda, (M - m0) < T::BM ? (M - m0) : T::BM, lda);
-  const __amdgpu_buffer_rsrc_t rb = rows_rsrc(B + k0 * ldb, (K - k0) < BK ? (K - k0) : BK, ldb);
+  const __amdgpu_buffer_rsrc_t rb = rows_rsrc(B + k0 * ldb, (K - k0) < T::BK ? (K - k0) : T::BK, ldb);
 #pragma unroll
   for (int i = 0; i < T::NA; ++i) {
     const int idx = tid + kThreads * i;
-    const int ar = idx >> 3, ak = 4 * (idx & 7);  // A: row in tile, k in slab
+    const int ar = idx / T::AROW, ak = 4 * (idx % T::AROW);  // A: row in tile, k in slab
     const uint32_t aoff = (k0 + ak < K) ? (uint32_t)((ar * lda + k0 + ak) * 4) : kOutside;
     s.a[i] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(ra, aoff, 0, 0));
   }
@@ -138,14 +143,13 @@ __device__ __forceinline__ void load_slab_vec(Slab<WT> &s, const float *__restri
   }
 }
 
-template <int WT>
-__device__ __forceinline__ void store_slab(const Slab<WT> &s, float *__restrict__ As, float *__restrict__ Bs,
+template <class T>
+__device__ __forceinline__ void store_slab(const Slab<T> &s, float *__restrict__ As, float *__restrict__ Bs,
                                            int tid) {
-  using T = Tile<WT>;
 #pragma unroll
   for (int i = 0; i < T::NA; ++i) {
     const int idx = tid + kThreads * i;
-    *reinterpret_cast<float4 *>(As + (idx >> 3) * LDA + 4 * (idx & 7)) = s.a[i];
+    *reinterpret_cast<float4 *>(As + (idx / T::AROW) * T::LDA + 4 * (idx % T::AROW)) = s.a[i];
   }
 #pragma unroll
   for (int i = 0; i < T::NB; ++i) {
@@ -154,29 +158,28 @@ __device__ __forceinline__ void store_slab(const Slab<WT> &s, float *__restrict_
   }
 }
 
-template <int WT>
-__device__ __forceinline__ void compute_slab(v16f (&acc)[WT][WT], const float *__restrict__ As,
+template <int WTM, int WTN, class T>
+__device__ __forceinline__ void compute_slab(v16f (&acc)[WTM][WTN], const float *__restrict__ As,
                                              const float *__restrict__ Bs, int wm, int wn, int lane) {
-  using T = Tile<WT>;
   const int r = lane & 31, h = lane >> 5;
 #pragma unroll
-  for (int c = 0; c < BK / 8; ++c) {
-    float4 a[WT];
-    float b[WT][4];
+  for (int c = 0; c < T::BK / 8; ++c) {
+    float4 a[WTM];
+    float b[WTN][4];
 #pragma unroll
-    for (int i = 0; i < WT; ++i)
-      a[i] = *reinterpret_cast<const float4 *>(As + (wm * 32 * WT + i * 32 + r) * LDA + 8 * c + 4 * h);
+    for (int i = 0; i < WTM; ++i)
+      a[i] = *reinterpret_cast<const float4 *>(As + (wm * 32 * WTM + i * 32 + r) * T::LDA + 8 * c + 4 * h);
 #pragma unroll
-    for (int j = 0; j < WT; ++j)
+    for (int j = 0; j < WTN; ++j)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) b[j][s] = Bs[(8 * c + 4 * h + s) * T::LDB + wn * 32 * WT + j * 32 + r];
+      for (int s = 0; s < 4; ++s) b[j][s] = Bs[(8 * c + 4 * h + s) * T::LDB + wn * 32 * WTN + j * 32 + r];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
 #pragma unroll
-      for (int i = 0; i < WT; ++i) {
+      for (int i = 0; i < WTM; ++i) {
         const float av = s == 0 ? a[i].x : s == 1 ? a[i].y : s == 2 ? a[i].z : a[i].w;
 #pragma unroll
-        for (int j = 0; j < WT; ++j)
+        for (int j = 0; j < WTN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, b[j][s], acc[i][j], 0, 0, 0);
       }
     }
@@ -200,12 +203,13 @@ __device__ __forceinline__ void tile_coords(int64_t pid, int64_t tiles_m, int64_
 // As, Bs: the two LDS stages, A_STAGE and B_STAGE floats apart. (Offsets
 // from one base keep the pointers visibly in LDS for the compiler; an array
 // of stage pointers would turn every LDS access into a flat one.)
-template <int WT, bool VEC>
+template <int WTM, int WTN, int BKT, bool VEC, bool PRIO>
 __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const float *__restrict__ Bp,
                                            float *__restrict__ Cp, int64_t M, int64_t N, int64_t K, int64_t lda,
                                            int64_t ldb, int64_t ldc, bool a_vec, bool b_vec, float *As,
                                            float *Bs) {
-  using T = Tile<WT>;
+  using T = Tile<WTM, WTN, BKT>;
+  constexpr int BK = T::BK;
   const int tid = threadIdx.x;
   const int lane = kh::lane_id();
   const int wave = tid >> 6;
@@ -223,42 +227,49 @@ __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const f
     tile_coords(pid, tiles_m, tiles_n, xcd_remap, tm, tn);
     const int64_t m0 = tm * T::BM, n0 = tn * T::BN;
 
-    v16f acc[WT][WT];
+    v16f acc[WTM][WTN];
 #pragma unroll
-    for (int i = 0; i < WT; ++i)
+    for (int i = 0; i < WTM; ++i)
 #pragma unroll
-      for (int j = 0; j < WT; ++j) acc[i][j] = v16f{};
+      for (int j = 0; j < WTN; ++j) acc[i][j] = v16f{};
 
-    auto load = [&](Slab<WT> &sl, int64_t k0) __attribute__((always_inline)) {
-      if (VEC)
-        load_slab_vec<WT>(sl, Ap, Bp, M, N, K, lda, ldb, m0, n0, k0, tid);
-      else
-        load_slab<WT>(sl, Ap, Bp, M, N, K, lda, ldb, m0, n0, k0, a_vec, b_vec, tid);
-    };
-    Slab<WT> s;
-    load(s, 0);
-    store_slab<WT>(s, As, Bs, tid);
-    __syncthreads();
-    for (int64_t ks = 0; ks < nslabs; ++ks) {
-      const int cur = ks & 1;
-      const bool more = ks + 1 < nslabs;
-      if (more) load(s, (ks + 1) * BK);
-      compute_slab<WT>(acc, As + cur * T::A_STAGE, Bs + cur * T::B_STAGE, wm, wn, lane);
-      if (more) store_slab<WT>(s, As + (cur ^ 1) * T::A_STAGE, Bs + (cur ^ 1) * T::B_STAGE, tid);
+    if (VEC) {
+      Slab<T> s;
+      load_slab_vec<T>(s, Ap, Bp, M, N, K, lda, ldb, m0, n0, 0, tid);
+      store_slab<T>(s, As, Bs, tid);
       __syncthreads();
+      for (int64_t ks = 0; ks < nslabs; ++ks) {
+        const int cur = ks & 1;
+        const bool more = ks + 1 < nslabs;
+        if (more) load_slab_vec<T>(s, Ap, Bp, M, N, K, lda, ldb, m0, n0, (ks + 1) * BK, tid);
+        if (PRIO) __builtin_amdgcn_s_setprio(1);
+        compute_slab<WTM, WTN, T>(acc, As + cur * T::A_STAGE, Bs + cur * T::B_STAGE, wm, wn, lane);
+        if (PRIO) __builtin_amdgcn_s_setprio(0);
+        if (more) store_slab<T>(s, As + (cur ^ 1) * T::A_STAGE, Bs + (cur ^ 1) * T::B_STAGE, tid);
+        __syncthreads();
+      }
+    } else {
+      for (int64_t ks = 0; ks < nslabs; ++ks) {
+        Slab<T> s;
+        load_slab<T>(s, Ap, Bp, M, N, K, lda, ldb, m0, n0, ks * BK, a_vec, b_vec, tid);
+        store_slab<T>(s, As, Bs, tid);
+        __syncthreads();
+        compute_slab<WTM, WTN, T>(acc, As, Bs, wm, wn, lane);
+        __syncthreads();
+      }
     }
 
     // Accumulator layout: lane l, register r -> row 8(r/4) + 4(l/32) + r%4,
     // column l%32 of the 32x32 block.
     const int col = lane & 31, h = lane >> 5;
 #pragma unroll
-    for (int i = 0; i < WT; ++i) {
+    for (int i = 0; i < WTM; ++i) {
 #pragma unroll
-      for (int j = 0; j < WT; ++j) {
-        const int64_t gc = n0 + wn * 32 * WT + j * 32 + col;
+      for (int j = 0; j < WTN; ++j) {
+        const int64_t gc = n0 + wn * 32 * WTN + j * 32 + col;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int64_t gr = m0 + wm * 32 * WT + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          const int64_t gr = m0 + wm * 32 * WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
           if (gr < M && gc < N) Cp[gr * ldc + gc] = acc[i][j][r];
         }
       }
@@ -266,37 +277,43 @@ __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const f
   }
 }
 
-template <int WT>
+template <int WTM, int WTN, int BKT, bool PRIO>
 __device__ __forceinline__ void gemm_entry(const float *__restrict__ Ap, const float *__restrict__ Bp,
                                            float *__restrict__ Cp, int64_t M, int64_t N, int64_t K, int64_t lda,
                                            int64_t ldb, int64_t ldc) {
-  using T = Tile<WT>;
+  using T = Tile<WTM, WTN, BKT>;
   __shared__ __attribute__((aligned(16))) float As[2 * T::A_STAGE];
   __shared__ __attribute__((aligned(16))) float Bs[2 * T::B_STAGE];
   const bool a_vec = ((K & 3) == 0) && ((lda & 3) == 0) && kh::aligned16(Ap);
   const bool b_vec = ((N & 3) == 0) && ((ldb & 3) == 0) && kh::aligned16(Bp);
   // The fast loads address a tile's rows with 32-bit byte offsets.
-  const bool fits32 = (int64_t)T::BM * lda * 4 < (1ll << 31) && (int64_t)BK * ldb * 4 < (1ll << 31);
+  const bool fits32 = (int64_t)T::BM * lda * 4 < (1ll << 31) && (int64_t)T::BK * ldb * 4 < (1ll << 31);
   if (a_vec && b_vec && fits32)
-    gemm_tiles<WT, true>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, As, Bs);
+    gemm_tiles<WTM, WTN, BKT, true, PRIO>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, As, Bs);
   else
-    gemm_tiles<WT, false>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, As, Bs);
+    gemm_tiles<WTM, WTN, BKT, false, PRIO>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, As, Bs);
 }
 
 }  // namespace
 
-static_assert(Tile<2>::BM == KH_GEMM_BM && Tile<2>::BN == KH_GEMM_BN, "launcher tile size");
-static_assert(Tile<1>::BM == KH_GEMM_SMALL_BM && Tile<1>::BN == KH_GEMM_SMALL_BN, "launcher tile size");
+static_assert(Tile<2, 4, 16>::BM == KH_GEMM_BM && Tile<2, 4, 16>::BN == KH_GEMM_BN, "launcher tile size");
+static_assert(Tile<2, 2, 32>::BM == KH_GEMM_MID_BM && Tile<2, 2, 32>::BN == KH_GEMM_MID_BN, "launcher tile size");
+static_assert(Tile<1, 1, 32>::BM == KH_GEMM_SMALL_BM && Tile<1, 1, 32>::BN == KH_GEMM_SMALL_BN, "launcher tile size");
 
-// The reference symbol: 128x128 tiles.
+// The reference symbol: 128x256 tiles.
 extern "C" __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 gemm(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
-  gemm_entry<2>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
+  gemm_entry<2, 4, 16, true>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
 }
 
-// Same arguments and results with 64x64 tiles, for problems whose 128x128
-// grid would leave CUs idle.
+// Same arguments and results with 128x128 tiles.
+extern "C" __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+gemm_mid(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
+  gemm_entry<2, 2, 32, false>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
+}
+
+// Same arguments and results with 64x64 tiles.
 extern "C" __global__ void __launch_bounds__(kThreads)
 gemm_small(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
-  gemm_entry<1>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
+  gemm_entry<1, 1, 32, false>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
 }

@@ -19,15 +19,19 @@
 // Smallest tile any accepted launch uses (256 threads); sizes the state.
 #define KH_SCAN_MIN_TILE (KH_SCAN_PER_THREAD * (256 - 64))
 
-// GEMM block tile (rows of C x columns of C per workgroup of 256 threads):
-// `gemm` uses 128x128; `gemm_small` 64x64, chosen by the launcher when the
-// 128x128 grid has fewer than KH_GEMM_SMALL_TILES tiles (four per CU on
-// MI355X), i.e. when it could not keep every CU busy.
+// GEMM block tiles (rows of C x columns of C per workgroup of 256 threads).
+// The launcher takes `gemm` (128x256) when its grid has at least
+// KH_GEMM_TILES_256 tiles (two per CU on MI355X), else `gemm_mid` (128x128)
+// when that grid has at least KH_GEMM_TILES_128 tiles, else `gemm_small`
+// (64x64): the largest tile that still gives every CU work.
 #define KH_GEMM_BM 128
-#define KH_GEMM_BN 128
+#define KH_GEMM_BN 256
+#define KH_GEMM_MID_BM 128
+#define KH_GEMM_MID_BN 128
 #define KH_GEMM_SMALL_BM 64
 #define KH_GEMM_SMALL_BN 64
-#define KH_GEMM_SMALL_TILES 1024
+#define KH_GEMM_TILES_256 512
+#define KH_GEMM_TILES_128 256
 
 // Attention: query rows per workgroup (4 wavefronts x 32 rows).
 #define KH_ATTN_BLOCK_Q 128

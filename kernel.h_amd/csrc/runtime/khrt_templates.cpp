@@ -147,6 +147,20 @@ int get_function(const char *co_name, const char *symbol, void **out) {
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// GEMM tile choice: the largest tile whose grid still gives every CU work.
+const char *gemm_symbol(int64_t m, int64_t n) {
+  if (ceil_div(m, KH_GEMM_BM) * ceil_div(n, KH_GEMM_BN) >= KH_GEMM_TILES_256) return "gemm";
+  if (ceil_div(m, KH_GEMM_MID_BM) * ceil_div(n, KH_GEMM_MID_BN) >= KH_GEMM_TILES_128) return "gemm_mid";
+  return "gemm_small";
+}
+
+int64_t gemm_grid(int64_t m, int64_t n) {
+  const std::string sym = gemm_symbol(m, n);
+  if (sym == "gemm") return ceil_div(m, KH_GEMM_BM) * ceil_div(n, KH_GEMM_BN);
+  if (sym == "gemm_mid") return ceil_div(m, KH_GEMM_MID_BM) * ceil_div(n, KH_GEMM_MID_BN);
+  return ceil_div(m, KH_GEMM_SMALL_BM) * ceil_div(n, KH_GEMM_SMALL_BN);
+}
+
 unsigned clamp_grid(int64_t g) { return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(g, 1 << 20))); }
 
 using Shape = std::map<std::string, int64_t>;
@@ -190,9 +204,7 @@ int geometry(const char *name, const Shape &s, khrt_dim3 &grid, khrt_dim3 &block
     if (!need(s, "m", m) || !need(s, "n", n) || !need(s, "k", k)) {
       return khrt::fail(KHRT_E_INVALID, "gemm: shape attributes 'm', 'n' and 'k' are required and must be positive");
     }
-    const int64_t tiles = ceil_div(m, KH_GEMM_BM) * ceil_div(n, KH_GEMM_BN);
-    grid.x = clamp_grid(tiles < KH_GEMM_SMALL_TILES ? ceil_div(m, KH_GEMM_SMALL_BM) * ceil_div(n, KH_GEMM_SMALL_BN)
-                                                    : tiles);
+    grid.x = clamp_grid(gemm_grid(m, n));
   } else if (t == "attention") {
     if (!need(s, "batch", b) || !need(s, "heads", h) || !need(s, "seq", seq) || !need(s, "head_dim", d)) {
       return khrt::fail(KHRT_E_INVALID,
@@ -225,10 +237,7 @@ const char *launch_symbol(const Template *t, const Shape &s) {
   }
   if (n == "gemm") {
     auto m = s.find("m"), nn = s.find("n");
-    if (m != s.end() && nn != s.end() &&
-        ceil_div(m->second, KH_GEMM_BM) * ceil_div(nn->second, KH_GEMM_BN) < KH_GEMM_SMALL_TILES) {
-      return "gemm_small";
-    }
+    if (m != s.end() && nn != s.end()) return gemm_symbol(m->second, nn->second);
   }
   return t->name;
 }

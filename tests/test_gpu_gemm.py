@@ -8,8 +8,9 @@
   reference (e2e_gemm_test.cpp:281); 8192^3 is checked on a row sample.
 * Ragged shapes, the reference launch geometry, and the A*B^T negative
   control (e2e_gemm_test.cpp:289-375).
-* Both tile symbols (`gemm` 128x128, `gemm_small` 64x64) give the same
-  results at every shape, whichever the launcher would pick.
+* Every tile symbol (`gemm` 128x256, `gemm_mid` 128x128, `gemm_small`
+  64x64) gives the same results at every shape, whichever the launcher
+  would pick.
 """
 import numpy as np
 import pytest
@@ -86,7 +87,7 @@ def test_gemm_reference_geometry_and_negative_control(dev):
     assert O.rel_frobenius(C, wrong) > 1e-5
 
 
-@pytest.mark.parametrize("symbol", ["gemm", "gemm_small"])
+@pytest.mark.parametrize("symbol", ["gemm", "gemm_mid", "gemm_small"])
 @pytest.mark.parametrize("m,n,k", [(256, 256, 256), (1000, 1000, 1000), (64, 192, 4097), (129, 65, 33),
                                    (3, 5, 7), (512, 2048, 96)])
 def test_every_gemm_symbol_at_every_shape(dev, symbol, m, n, k):
