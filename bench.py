@@ -43,8 +43,8 @@ METRIC = "GEMM-8192 fp32 TFLOPS + softmax/scan HBM GB/s, % of MI355X roofline"
 # 2.000 and WRITE_SIZE by 1.000, the factors a copy kernel of known size
 # reads), recorded in profiles/templates_baseline_sizes_hbm_traffic.md.
 PMC_TRAFFIC_BYTES = {
-    "vecadd": 201373696, "softmax": 33634304, "layernorm": 33726464, "scan": 539584512,
-    "fused_gelu": 537007104, "gemm": 6909112320, "attention": 1208114176,
+    "vecadd": 201373696, "softmax": 33635328, "layernorm": 33726464, "scan": 539568128,
+    "fused_gelu": 537011200, "gemm": 4492365824, "attention": 1208116224,
 }
 
 
@@ -125,7 +125,9 @@ def measure_ceilings(kh, stream, reps=5):
     """Measured roofline denominators: triad and copy over 2^28 floats per
     buffer (3 GiB / 2 GiB moved per launch, beyond the 256 MB MALL, as the
     reference's roofline_triad, bench/harness/roofline.cpp:60-84) and the
-    fp32 MFMA microbenchmark (8 independent chains per wave)."""
+    fp32 MFMA microbenchmark (8 independent chains per wave, two waves per
+    SIMD, ~2 ms per launch: shorter launches under-measure it, as the clock
+    has not settled and launch gaps count)."""
     n = 1 << 28
     a, b, c = kh.Buffer(4 * n), kh.Buffer(4 * n), kh.Buffer(4 * n)
     a.fill(1.0, stream)
@@ -145,7 +147,7 @@ def measure_ceilings(kh, stream, reps=5):
     t_triad = timed(lambda: kh.roofline_triad(a, b, c, n, stream))
     t_copy = timed(lambda: kh.roofline_copy(a, c, n, stream))
     cu = kh.device_info()["cu_count"]
-    blocks, iters = cu * 8, 64
+    blocks, iters = cu * 2, 4096
     out = kh.Buffer(4 * blocks * 256)
     flops = float(blocks) * 4 * iters * 8 * 4096
     t_mfma = timed(lambda: kh.roofline_mfma(out, blocks, iters, stream))
