@@ -6,7 +6,7 @@ Outputs under kernel.h_amd/build/:
   co/<name>.notes.json resource notes per kernel symbol
   gen/kh_embed.S       .incbin of every product code object
   gen/kh_resources.inc resource table compiled into the runtime
-  gen/kh_cli_embed.S   .incbin of the CLI-only comparator code object (hipref)
+  gen/kh_cli_embed.S   .incbin of the CLI-only code objects (hipref, gemm_tune)
   libkhrt.so           the C-ABI runtime (include/khrt.h)
   kernelh              the CLI (compile / bench / occupancy)
 
@@ -45,8 +45,10 @@ OBJ = os.path.join(BUILD, "obj")
 PRODUCT = ["vecadd", "fused_gelu", "softmax", "layernorm", "scan", "gemm", "attention", "util", "roofline"]
 # Test-only code objects (loaded by tests through khrt_module_load_data).
 PROBES = ["mfma_probe"]
-# Bench-only comparators (csrc/cli/*.hip), embedded in the kernelh CLI.
-CLI_CODE_OBJECTS = ["hipref"]
+# CLI-only code objects, embedded in the kernelh executable: the bench
+# comparators (csrc/cli/hipref.hip) and the GEMM tune candidates
+# (csrc/kernels/gemm_tune.hip, built from the product's GEMM templates).
+CLI_CODE_OBJECTS = {"hipref": "cli", "gemm_tune": "kernels"}
 
 DEVICE_FLAGS = [
     "-x", "hip", f"--offload-arch={ARCH}", "--cuda-device-only", "--no-gpu-bundle-output",
@@ -162,10 +164,11 @@ def build(jobs: int = 8, verbose: bool = False) -> None:
         os.makedirs(d, exist_ok=True)
 
     srcs = [n for n in PRODUCT + PROBES if os.path.exists(os.path.join(KDIR, n + ".hip"))]
-    cli_cos = [n for n in CLI_CODE_OBJECTS if os.path.exists(os.path.join(CLIDIR, n + ".hip"))]
+    cli_dirs = {n: (CLIDIR if d == "cli" else KDIR) for n, d in CLI_CODE_OBJECTS.items()}
+    cli_cos = [n for n in CLI_CODE_OBJECTS if os.path.exists(os.path.join(cli_dirs[n], n + ".hip"))]
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         outs = dict(zip(srcs, ex.map(lambda n: compile_co(n, verbose), srcs)))
-        cli_outs = dict(zip(cli_cos, ex.map(lambda n: compile_co(n, verbose, CLIDIR), cli_cos)))
+        cli_outs = dict(zip(cli_cos, ex.map(lambda n: compile_co(n, verbose, cli_dirs[n]), cli_cos)))
     present = {n: p for n, p in outs.items() if n in PRODUCT}
 
     # Refuse spills into scratch in product kernels: they would silently

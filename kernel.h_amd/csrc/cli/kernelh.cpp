@@ -3,6 +3,8 @@
 // The reference's CLI surface for this path (tools/kernelh/main.cpp):
 //   kernelh compile --kernel <name> --shape k=v,... --target <t> --out <dir>
 //                   [--resources]                          (main.cpp:435-646)
+//   kernelh tune    --kernel gemm --shape m=..,n=..,k=.. --out <dir> [...]
+//                                                          (main.cpp:649-1420)
 //   kernelh bench   --suite <roofline|kernelh|rocblas|hipref|all> --out <path>
 //                   [--occupancy] [--kernel <name> --shape ... [--backend <b>]]
 //                                                          (main.cpp:2154-2228)
@@ -28,6 +30,7 @@
 #include "khrt.h"
 
 #include "comparators.hpp"
+#include "tune.hpp"
 
 #include <algorithm>
 #include <chrono>
@@ -56,7 +59,7 @@ constexpr int kExitSkip = 77;
 
 void usage(std::ostream &os) {
   os << "kernelh - kernel.h templates on AMD Instinct MI355X (gfx950)\n\n"
-     << "usage: kernelh <compile|bench|info> [options]\n\n"
+     << "usage: kernelh <compile|bench|tune|info> [options]\n\n"
      << "compile options:\n"
      << "  --kernel <name>       template: vecadd, gemm, softmax, layernorm, scan,\n"
      << "                        scan_totals, fused_gelu, attention\n"
@@ -65,6 +68,9 @@ void usage(std::ostream &os) {
      << "  --target <t>          amdgcn-gfx950 (default; the only code-object target)\n"
      << "  --out <dir>           write <dir>/<kernel>.{hsaco,isa} (created if missing)\n"
      << "  --resources           also write <dir>/resources.json\n\n"
+     << "tune options (GEMM only): kernelh tune --help\n"
+     << "  --shape m=..,n=..,k=.. --out <dir> [--max-candidates n] [--timeout s]\n"
+     << "  [--cache path]; writes <dir>/tune-results.csv, prints the best config\n\n"
      << "bench options:\n"
      << "  --suite <name>        roofline, kernelh, rocblas, hipref, all (default: all)\n"
      << "  --backend <name>      with --kernel: kernelh (default), rocblas, hipref-naive,\n"
@@ -619,6 +625,8 @@ int main(int argc, char **argv) {
     return run_compile(argc, argv);
   }
   if (cmd == "bench") return run_bench(argc, argv);
+  if (cmd == "tune") return khcli::run_tune(argc, argv);
+  if (cmd == "tune-eval") return khcli::run_tune_eval(argc, argv);
   if (cmd == "info") return run_info();
   std::cerr << "error: unknown command '" << cmd << "'\n";
   usage(std::cerr);

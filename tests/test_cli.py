@@ -106,3 +106,37 @@ def test_bench_comparator_rows(dev, tmp_path, kernel, shape, backend):
     assert r.returncode == 0, r.stdout
     rows = list(csv.DictReader(open(tmp_path / "results.csv")))
     assert rows[0]["backend"] == backend and float(rows[0]["gflops_or_gbps"]) > 0
+
+
+def test_tune_usage_and_refusals(tmp_path):
+    # kernelh tune (tools/kernelh/main.cpp:649-760, 1320-1350): usage errors
+    # exit 2, unsupported kernel / target exit 1, no device exits 77.
+    assert run("tune", "--out", str(tmp_path)).returncode == 2                       # no --shape
+    assert run("tune", "--shape", "m=8,n=8,k=8").returncode == 2                     # no --out
+    assert run("tune", "--shape", "m=8,n=8,k=8", "--out", str(tmp_path), "--max-candidates", "0").returncode == 2
+    assert run("tune", "--shape", "m=8,n=8,k=8", "--out", str(tmp_path), "--timeout", "9999").returncode == 2
+    r = run("tune", "--kernel", "softmax", "--shape", "m=8,n=8,k=8", "--out", str(tmp_path))
+    assert r.returncode == 1 and "only the 'gemm' kernel" in r.stdout
+    r = run("tune", "--shape", "m=8,n=8,k=8", "--out", str(tmp_path), "--target", "amdgcn-gfx1101")
+    assert r.returncode == 1 and "amdgcn-gfx950" in r.stdout
+    if kh.device_count() == 0:
+        assert run("tune", "--shape", "m=8,n=8,k=8", "--out", str(tmp_path)).returncode == 77
+
+
+@pytest.mark.gpu
+def test_tune_evaluates_candidates_and_caches(dev, tmp_path):
+    print("[gpu-case] kernelh tune gemm m=n=k=512, 6 candidates", flush=True)
+    cache = str(tmp_path / "cache.json")
+    args = ("tune", "--shape", "m=512,n=512,k=512", "--out", str(tmp_path), "--max-candidates", "6",
+            "--timeout", "60", "--cache", cache)
+    r = run(*args)
+    assert r.returncode == 0, r.stdout
+    assert "best config: gemm_t" in r.stdout and "tune ok" in r.stdout
+    rows = list(csv.DictReader(open(tmp_path / "tune-results.csv")))
+    assert len(rows) == 6
+    assert list(rows[0].keys())[:11] == ["kernel", "shape", "bm", "bn", "bk", "waves", "unroll", "vec", "ms_median",
+                                          "accepted", "reason"]
+    assert all(row["accepted"] == "true" and row["reason"] == "ok" for row in rows), rows
+    assert all(float(row["ms_median"]) > 0 for row in rows)
+    r2 = run(*args)
+    assert r2.returncode == 0 and "cache-hit" in r2.stdout and "served from cache" in r2.stdout
