@@ -169,36 +169,45 @@ __device__ __forceinline__ void store_seg(const float (&o)[kPerThread], __amdgpu
   }
 }
 
+// One look-back window: predecessors end, end-1, ..., end - 64 kWindow + 1;
+// lane l, slot j holds distance d = l + 64 j behind `end`. Slots before tile
+// 0 act as an inclusive prefix of value 0.
+struct Window {
+  uint64_t inc[kWindow], ag[kWindow];
+};
+
+__device__ __forceinline__ void poll_window(Window &w, uint64_t *slots, int64_t end, int lane) {
+#pragma unroll
+  for (int j = 0; j < kWindow; ++j) {
+    const int64_t idx = end - lane - kh::kWave * j;
+    w.inc[j] = (idx >= 0) ? slot_load(&slots[2 * idx + 1]) : 0ull;
+    w.ag[j] = (idx >= 0) ? slot_load(&slots[2 * idx]) : kEmpty;
+  }
+}
+
 // Exclusive prefix of `tile` from its predecessors' published slots (run by
-// one whole wave; the result is wave-uniform). NaN if the bounded wait ran
-// out.
-__device__ __forceinline__ double look_back(uint64_t *slots, uint32_t *state, int64_t tile, int lane) {
+// one whole wave; the result is wave-uniform), starting from window `w`,
+// already polled for end = tile - 1. Slots only ever go from unpublished to
+// their final value, so an early poll is a valid (if possibly incomplete)
+// observation. NaN if the bounded wait ran out.
+__device__ __forceinline__ double look_back(uint64_t *slots, uint32_t *state, int64_t tile, int lane, Window w) {
   double excl = 0.0;
   int64_t end = tile - 1;  // newest predecessor still to account for
   uint32_t spins = 0;
   for (;;) {
-    // Lane l, slot j covers distance d = l + 64 j behind `end`.
-    uint64_t inc[kWindow], ag[kWindow];
-#pragma unroll
-    for (int j = 0; j < kWindow; ++j) {
-      const int64_t idx = end - lane - kh::kWave * j;
-      // Slots before tile 0 act as an inclusive prefix of value 0.
-      inc[j] = (idx >= 0) ? slot_load(&slots[2 * idx + 1]) : 0ull;
-      ag[j] = (idx >= 0) ? slot_load(&slots[2 * idx]) : kEmpty;
-    }
     // Nearest inclusive prefix, and whether every nearer predecessor has at
     // least published its aggregate.
     int first = kWindow * kh::kWave;
 #pragma unroll
     for (int j = kWindow - 1; j >= 0; --j) {
-      const uint64_t m = __ballot(inc[j] != kEmpty);
+      const uint64_t m = __ballot(w.inc[j] != kEmpty);
       if (m) first = kh::kWave * j + __builtin_ctzll(m);
     }
     bool pending = false;
 #pragma unroll
     for (int j = 0; j < kWindow; ++j) {
       const int d = lane + kh::kWave * j;
-      if (d < first && ag[j] == kEmpty) pending = true;
+      if (d < first && w.ag[j] == kEmpty) pending = true;
     }
     if (__ballot(pending) != 0) {
       if (++spins > kSpinLimit) {
@@ -206,6 +215,7 @@ __device__ __forceinline__ double look_back(uint64_t *slots, uint32_t *state, in
         return __builtin_nan("");
       }
       __builtin_amdgcn_s_sleep(1);
+      poll_window(w, slots, end, lane);
       continue;
     }
     double contrib = 0.0;
@@ -213,14 +223,15 @@ __device__ __forceinline__ double look_back(uint64_t *slots, uint32_t *state, in
     for (int j = 0; j < kWindow; ++j) {
       const int d = lane + kh::kWave * j;
       if (d < first) {
-        contrib += __longlong_as_double((long long)ag[j]);
+        contrib += __longlong_as_double((long long)w.ag[j]);
       } else if (d == first) {
-        contrib += __longlong_as_double((long long)inc[j]);
+        contrib += __longlong_as_double((long long)w.inc[j]);
       }
     }
     excl += wave_sum_f64(contrib);
     if (first < kWindow * kh::kWave) return excl;
     end -= kWindow * kh::kWave;
+    poll_window(w, slots, end, lane);
   }
 }
 
@@ -273,8 +284,14 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
     // on the data path would be a register write that must wait for the
     // pending atomic, i.e. for all of that wave's outstanding memory ops.
     uint32_t raw;
+    // The first look-back poll for tile tc goes out now, before the barrier:
+    // tc was reduced (and its predecessors' aggregates published) in earlier
+    // iterations, so its round trip overlaps the data waves' reduction.
+    // Defined on the control wave only, like `raw`.
+    Window w;
     if (ctrl) {
       if (lane == 0 && !single) raw = atomicAdd(state, 1u);
+      if (tc > 0) poll_window(w, slots, tc - 1, lane);
     } else if (tr < ntiles) {
       // ---- reduce tile tr: per-row lane sums (fp64), wave scans, wave total ---
       // off[k] = (rows before k) + (lanes before this one in row k); exact,
@@ -303,7 +320,7 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
       // ---- decoupled look-back for tile tc -------------------------------------
       double excl = 0.0;
       if (tc > 0) {
-        excl = look_back(slots, state, tc, lane);
+        excl = look_back(slots, state, tc, lane, w);
         if (lane == 0) slot_store(&slots[2 * tc + 1], excl + agg_c);
       }
       agg_c = agg_r;
