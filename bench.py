@@ -43,8 +43,8 @@ METRIC = "GEMM-8192 fp32 TFLOPS + softmax/scan HBM GB/s, % of MI355X roofline"
 # 2.000 and WRITE_SIZE by 1.000, the factors a copy kernel of known size
 # reads), recorded in profiles/templates_baseline_sizes_hbm_traffic.md.
 PMC_TRAFFIC_BYTES = {
-    "vecadd": 201373696, "softmax": 33635328, "layernorm": 33726464, "scan": 539568128,
-    "fused_gelu": 537011200, "gemm": 4492365824, "attention": 1208116224,
+    "vecadd": 201374106, "softmax": 33634176, "layernorm": 33726643, "scan": 539478867,
+    "fused_gelu": 537009843, "gemm": 4479760026, "attention": 1208113510,
 }
 
 
