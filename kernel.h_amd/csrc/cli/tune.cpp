@@ -9,7 +9,7 @@
 //     capped at 128) against an fp64 host product, relative Frobenius
 //     <= 1e-5, then times it at the tuning shape: warmup 3, median of 10;
 //   * results go to <out>/tune-results.csv (the reference's columns, then
-//     symbol, wave_tile, prio, gflops) and to a cache file keyed by
+//     symbol, wave_tile, prio, lds_dma, gflops) and to a cache file keyed by
 //     kernel|shape|device, so a second run with the same key is served from
 //     the cache.
 // Differences, each stated in the usage text: the space is a fixed set of
@@ -54,7 +54,7 @@ namespace {
 namespace fs = std::filesystem;
 
 struct Candidate {
-  int wtm, wtn, bk, prio;
+  int wtm, wtn, bk, prio, dma;
   const char *symbol;
   int bm() const { return 64 * wtm; }
   int bn() const { return 64 * wtn; }
@@ -62,7 +62,8 @@ struct Candidate {
 
 #define KH_STR2(x) #x
 #define KH_STR(x) KH_STR2(x)
-#define KH_TUNE_ROW(WTM, WTN, BK, PRIO) {WTM, WTN, BK, PRIO, KH_STR(KH_GEMM_TUNE_SYMBOL(WTM, WTN, BK, PRIO))},
+#define KH_TUNE_ROW(WTM, WTN, BK, PRIO, DMA) \
+  {WTM, WTN, BK, PRIO, DMA, KH_STR(KH_GEMM_TUNE_SYMBOL(WTM, WTN, BK, PRIO, DMA))},
 const Candidate kCandidates[] = {KH_GEMM_TUNE_CONFIGS(KH_TUNE_ROW)};
 #undef KH_TUNE_ROW
 
@@ -257,8 +258,9 @@ void usage_tune(std::ostream &os) {
      << "  --cache <path>        cache file (default build/tune-cache.json), keyed\n"
      << "                        FNV-1a(kernel|shape|device)\n"
      << "The space (KH_GEMM_TUNE_CONFIGS) is a fixed set of precompiled gfx950\n"
-     << "instantiations: wave tile WTM x WTN of 32x32 MFMAs, slab depth BK and MFMA\n"
-     << "wave priority; it is evaluated exhaustively, not sampled.\n";
+     << "instantiations: wave tile WTM x WTN of 32x32 MFMAs, slab depth BK, MFMA\n"
+     << "wave priority and slab pipeline (register-staged, or direct-to-LDS with three\n"
+     << "stages); it is evaluated exhaustively, not sampled.\n";
 }
 
 // ---------------------------------------------------------------- child
@@ -512,12 +514,13 @@ int run_tune(int argc, char **argv) {
   }
 
   std::ostringstream csv;
-  csv << "kernel,shape,bm,bn,bk,waves,unroll,vec,ms_median,accepted,reason,symbol,wave_tile,prio,gflops\n";
+  csv << "kernel,shape,bm,bn,bk,waves,unroll,vec,ms_median,accepted,reason,symbol,wave_tile,prio,lds_dma,gflops\n";
   const Result *best = nullptr;
   for (const Result &r : results) {
     csv << kernel << "," << csv_escape(shape_text) << "," << r.c->bm() << "," << r.c->bn() << "," << r.c->bk
         << ",4,1,4," << r.ms << "," << (r.accepted ? "true" : "false") << "," << csv_escape(r.reason) << ","
-        << r.c->symbol << "," << r.c->wtm * 32 << "x" << r.c->wtn * 32 << "," << r.c->prio << "," << r.gflops
+        << r.c->symbol << "," << r.c->wtm * 32 << "x" << r.c->wtn * 32 << "," << r.c->prio << "," << r.c->dma << ","
+        << r.gflops
         << "\n";
     if (r.accepted && (best == nullptr || r.ms < best->ms)) best = &r;
   }
@@ -527,8 +530,9 @@ int run_tune(int argc, char **argv) {
     std::cout << "best config: none (no candidate passed all gates)\ntune ok\n";
     return 0;
   }
-  std::printf("best config: %s bm=%d bn=%d bk=%d prio=%d ms_median=%.4f (%.1f GFLOP/s)\n", best->c->symbol,
-              best->c->bm(), best->c->bn(), best->c->bk, best->c->prio, best->ms, best->gflops);
+  std::printf("best config: %s bm=%d bn=%d bk=%d prio=%d lds_dma=%d ms_median=%.4f (%.1f GFLOP/s)\n",
+              best->c->symbol, best->c->bm(), best->c->bn(), best->c->bk, best->c->prio, best->c->dma, best->ms,
+              best->gflops);
   cache_store(cache, key, best->c->symbol, csv.str());
   std::cout << "tune ok\n";
   return 0;

@@ -20,17 +20,25 @@
 //     LDS allows), so one workgroup's barrier and slab hand-over overlap the
 //     other's MFMAs. `gemm` raises its waves' priority (s_setprio) while they
 //     issue MFMAs, so a wave that is feeding the matrix core wins issue over
-//     one that is loading the next slab (+1.5% at 8192^3).
-//   * K advances in 16- or 32-wide slabs staged through LDS, double-buffered: the
-//     next slab's global loads are in flight while the current slab feeds
-//     the MFMAs, one barrier per slab.
-//   * LDS holds A as [m][k] (rows padded by 4 floats: one ds_read_b128 per
-//     lane delivers four k values, conflict-free) and
-//     B as [k][n] (rows padded by 4 floats; a half-wave reads 32 consecutive
-//     n with ds_read_b32). Both slabs arrive as dwordx4 loads: for aligned
-//     operands with k, n multiples of 4 as branch-free buffer loads whose
-//     range checks zero-fill the tails (the guarded per-element form of the
-//     generic path made the compiler split every load into branches and
+//     one that is between slabs (+2% at 8192^3).
+//   * K advances in slabs staged through LDS. `gemm` loads its slabs straight
+//     into LDS (buffer_load_dwordx4 ... lds) through three stages: slab ks+2
+//     is in flight while slab ks is consumed, and the one barrier per slab sits
+//     after the slab's first 8-deep chunk, so the next slab's first fragments
+//     are read while the rest of this one feeds the MFMAs. Against staging the
+//     slab through registers and ds_write (still used by `gemm_mid` and
+//     `gemm_small`, where it measured as fast) that is +2% at 8192^3: the
+//     stores and the wait for them sat between a wave's last MFMA of one slab
+//     and its first of the next.
+//   * LDS holds A as [m][k] (one ds_read_b128 per lane delivers four k
+//     values) and B as [k][n] (a half-wave reads 32 consecutive n with
+//     ds_read_b32), both conflict-free: rows padded by 4 floats when slabs are
+//     staged through registers; for direct-to-LDS slabs, whose loads write 64
+//     float4s contiguously, A's rows are unpadded with their float4s
+//     XOR-swizzled and B's rows padded per group a wave loads. Slab loads are
+//     branch-free buffer loads for aligned operands with k, n multiples of 4;
+//     their range checks zero-fill the tails (the guarded per-element form of
+//     the generic path made the compiler split every load into branches and
 //     dword pieces, which cost 15% of the MFMA rate).
 //   * K order inside an MFMA: the instruction sums k over its two lane
 //     halves, and any permutation of k applied to both operands gives the
@@ -51,24 +59,26 @@ using khg::Tile;
 using khg::gemm_entry;
 using khg::kThreads;
 
-static_assert(Tile<2, 4, 16>::BM == KH_GEMM_BM && Tile<2, 4, 16>::BN == KH_GEMM_BN, "launcher tile size");
-static_assert(Tile<2, 2, 32>::BM == KH_GEMM_MID_BM && Tile<2, 2, 32>::BN == KH_GEMM_MID_BN, "launcher tile size");
-static_assert(Tile<1, 1, 32>::BM == KH_GEMM_SMALL_BM && Tile<1, 1, 32>::BN == KH_GEMM_SMALL_BN, "launcher tile size");
+static_assert(Tile<2, 4, 16, true>::BM == KH_GEMM_BM && Tile<2, 4, 16, true>::BN == KH_GEMM_BN, "launcher tile size");
+static_assert(Tile<2, 2, 32, false>::BM == KH_GEMM_MID_BM && Tile<2, 2, 32, false>::BN == KH_GEMM_MID_BN,
+              "launcher tile size");
+static_assert(Tile<1, 1, 32, false>::BM == KH_GEMM_SMALL_BM && Tile<1, 1, 32, false>::BN == KH_GEMM_SMALL_BN,
+              "launcher tile size");
 
 // The reference symbol: 128x256 tiles.
 extern "C" __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 gemm(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
-  gemm_entry<2, 4, 16, true>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
+  gemm_entry<2, 4, 16, true, true>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
 }
 
 // Same arguments and results with 128x128 tiles.
 extern "C" __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_mid(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
-  gemm_entry<2, 2, 32, false>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
+  gemm_entry<2, 2, 32, false, false>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
 }
 
 // Same arguments and results with 64x64 tiles.
 extern "C" __global__ void __launch_bounds__(kThreads)
 gemm_small(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
-  gemm_entry<1, 1, 32, false>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
+  gemm_entry<1, 1, 32, false, false>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
 }

@@ -17,23 +17,46 @@ constexpr int kGroupM = 8;
 constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor: 32-bit data format
 constexpr uint32_t kOutside = 0x80000000u;
 
-// Tile geometry for WTM x WTN accumulators per wave, BKT-deep slabs.
-template <int WTM, int WTN, int BKT>
+// Tile geometry for WTM x WTN accumulators per wave, BKT-deep slabs, and the
+// LDS layout of one stage, which depends on how the stage is filled (DMA):
+//
+//   Register-staged (DMA false): A as [m][k] with rows padded by 4 floats
+//   (one ds_read_b128 per lane delivers four k values, conflict-free) and B
+//   as [k][n] with rows padded by 4 floats (a half-wave reads 32 consecutive
+//   n with ds_read_b32). Fragment addresses are affine in the lane, so each
+//   is one base register plus immediate offsets.
+//
+//   Direct-to-LDS (DMA true): a wave's load writes 64 float4s contiguously,
+//   so rows cannot be padded inside one load. A is [m][k] unpadded with the
+//   float4 holding k = 4Q..4Q+3 of row R at quad Q ^ aswz(R), an XOR swizzle
+//   that keeps every 8-lane (128 B) and 16-lane (256 B) phase of the
+//   fragment reads on distinct banks; B is [k][n] grouped by the RPI rows one
+//   wave's 1 KiB load covers, groups padded by 4 floats (the two lane halves
+//   of a fragment read, rows 4 apart, land on different banks).
+template <int WTM, int WTN, int BKT, bool DMA>
 struct Tile {
   static constexpr int BK = BKT;
-  static constexpr int LDA = BK + 4;       // A in LDS: [m][k], padded rows
   static constexpr int BM = 64 * WTM;      // rows of C per workgroup
   static constexpr int BN = 64 * WTN;      // columns of C per workgroup
-  static constexpr int LDB = BN + 4;       // B in LDS: [k][n], padded rows
-  static constexpr int AROW = BK / 4;      // float4 per A row
+  static constexpr int QP = BK / 4;        // float4 per A row
+  static constexpr int BROW = BN / 4;      // float4 per B row
+  static constexpr int RPI = DMA ? (BROW >= 64 ? 1 : 64 / BROW) : 1;  // B rows per padded group
+  static constexpr int LDA = DMA ? BK : BK + 4;
+  static constexpr int LDG = RPI * BN + 4; // floats per padded group of B rows
   static constexpr int NA = BM * BK / 4 / kThreads;  // A float4 per thread per slab
   static constexpr int NB = BK * BN / 4 / kThreads;  // B float4 per thread per slab
-  static constexpr int BROW = BN / 4;      // float4 per B row
   static constexpr int A_STAGE = BM * LDA;
-  static constexpr int B_STAGE = BK * LDB;
+  static constexpr int B_STAGE = (BK / RPI) * LDG;
+  static constexpr int SWZ_SHIFT = QP == 2 ? 2 : QP == 4 ? 1 : 0;
   static_assert(NA * kThreads * 4 == BM * BK && NB * kThreads * 4 == BK * BN,
                 "a slab must split into whole float4s over the 256 threads");
-  static_assert(BK % 8 == 0, "slabs are consumed in 8-deep chunks");
+  static_assert(BK % 8 == 0 && QP <= 8, "slabs are consumed in 8-deep chunks");
+  static_assert(BROW <= 64 || BROW % 64 == 0, "a wave's B load covers whole rows");
+  static_assert(BK % RPI == 0, "B row groups split the slab");
+  __device__ static constexpr int aswz(int row) { return DMA ? ((row >> SWZ_SHIFT) ^ (row >> 3)) & (QP - 1) : 0; }
+  // Float offset of A (row, logical quad q) and of B (row, column) in a stage.
+  __device__ static constexpr int a_at(int row, int q) { return row * LDA + 4 * (q ^ aswz(row)); }
+  __device__ static constexpr int b_at(int row, int col) { return (row / RPI) * LDG + (row % RPI) * BN + col; }
 };
 
 template <class T>
@@ -52,7 +75,7 @@ __device__ __forceinline__ float4 load4(const float *__restrict__ P, int64_t row
 }
 
 // Generic slab load: any shape, stride and alignment (guarded per element).
-// A: BK/4 lanes cover a row of the slab; B: BN/4 lanes cover a row of the tile.
+// A: QP lanes cover a row of the slab; B: BROW lanes cover a row of the tile.
 template <class T>
 __device__ __forceinline__ void load_slab(Slab<T> &s, const float *__restrict__ A, const float *__restrict__ B,
                                           int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t m0,
@@ -60,7 +83,7 @@ __device__ __forceinline__ void load_slab(Slab<T> &s, const float *__restrict__ 
 #pragma unroll
   for (int i = 0; i < T::NA; ++i) {
     const int idx = tid + kThreads * i;
-    s.a[i] = load4(A, m0 + idx / T::AROW, k0 + 4 * (idx % T::AROW), lda, M, K, a_vec);
+    s.a[i] = load4(A, m0 + idx / T::QP, k0 + 4 * (idx % T::QP), lda, M, K, a_vec);
   }
 #pragma unroll
   for (int i = 0; i < T::NB; ++i) {
@@ -69,20 +92,26 @@ __device__ __forceinline__ void load_slab(Slab<T> &s, const float *__restrict__ 
   }
 }
 
-// Fast slab load for 16-byte aligned A and B with k and n multiples of 4:
-// unconditional dwordx4 buffer loads. Each resource spans the slab's rows
-// that exist (A: tile rows m0.. below M; B: slab rows k0.. below K), so
-// rows past the matrix read 0 through the hardware range check; a float4
-// past K (A) or N (B) is sent to an offset outside the resource and reads 0
-// as well. No branches, 32-bit offsets.
+// Buffer resource over the slab rows that exist (A: tile rows m0.. below M;
+// B: slab rows k0.. below K): rows past the matrix read 0 through the
+// hardware range check; a float4 past K (A) or N (B) is sent to an offset
+// outside the resource and reads 0 as well. 32-bit offsets.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float *base, int64_t rows, int64_t ld) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, (int)(rows * ld * 4), kRsrcWord3);
+}
+
+// The same resource as four dwords, for the direct-to-LDS loads below.
+__device__ __forceinline__ u32x4 rows_desc(const float *base, int64_t rows, int64_t ld) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  return u32x4{(uint32_t)b, (uint32_t)(b >> 32) & 0xffffu, (uint32_t)(rows * ld * 4), (uint32_t)kRsrcWord3};
 }
 
 __device__ __forceinline__ float4 as_float4(u32x4 u) {
   return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
 }
 
+// Register-staged slab load for 16-byte aligned A and B with k and n
+// multiples of 4: unconditional dwordx4 buffer loads, no branches.
 template <class T>
 __device__ __forceinline__ void load_slab_vec(Slab<T> &s, const float *__restrict__ A, const float *__restrict__ B,
                                               int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
@@ -92,7 +121,7 @@ __device__ __forceinline__ void load_slab_vec(Slab<T> &s, const float *__restric
 #pragma unroll
   for (int i = 0; i < T::NA; ++i) {
     const int idx = tid + kThreads * i;
-    const int ar = idx / T::AROW, ak = 4 * (idx % T::AROW);  // A: row in tile, k in slab
+    const int ar = idx / T::QP, ak = 4 * (idx % T::QP);  // A: row in tile, k in slab
     const uint32_t aoff = (k0 + ak < K) ? (uint32_t)((ar * lda + k0 + ak) * 4) : kOutside;
     s.a[i] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(ra, aoff, 0, 0));
   }
@@ -105,46 +134,134 @@ __device__ __forceinline__ void load_slab_vec(Slab<T> &s, const float *__restric
   }
 }
 
+// Register-staged (or generic) slab into LDS, in the tile's layout.
 template <class T>
 __device__ __forceinline__ void store_slab(const Slab<T> &s, float *__restrict__ As, float *__restrict__ Bs,
                                            int tid) {
 #pragma unroll
   for (int i = 0; i < T::NA; ++i) {
     const int idx = tid + kThreads * i;
-    *reinterpret_cast<float4 *>(As + (idx / T::AROW) * T::LDA + 4 * (idx % T::AROW)) = s.a[i];
+    *reinterpret_cast<float4 *>(As + T::a_at(idx / T::QP, idx % T::QP)) = s.a[i];
   }
 #pragma unroll
   for (int i = 0; i < T::NB; ++i) {
     const int idx = tid + kThreads * i;
-    *reinterpret_cast<float4 *>(Bs + (idx / T::BROW) * T::LDB + 4 * (idx % T::BROW)) = s.b[i];
+    *reinterpret_cast<float4 *>(Bs + T::b_at(idx / T::BROW, 4 * (idx % T::BROW))) = s.b[i];
   }
+}
+
+// One wave-wide direct-to-LDS float4 load (buffer_load_dwordx4 ... lds):
+// lane l's 16 bytes from rsrc at byte offset voff land at LDS byte address
+// lds + 16 l. M0 carries the LDS address; it is saved and restored around
+// the load, with the one wait state the hardware needs between writing M0
+// and an LDS-destination load. The load is inline assembly on purpose: the
+// compiler cannot prove the LDS stages disjoint, and for its own form of
+// this load it would wait for the load before every later LDS read. Here
+// the caller orders it with vm_barrier.
+__device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t voff, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(voff), "s"(rsrc)
+      : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const float *p) { return (uint32_t)reinterpret_cast<uintptr_t>(p); }
+
+// Direct-to-LDS slab load for 16-byte aligned A and B with k and n multiples
+// of 4. Each wave's instruction lands 64 float4s contiguously, so the lane ->
+// global mapping realises the layout: in A, lane l of a wave fills physical
+// quad l % QP of its row and so fetches logical quad (l % QP) ^ aswz(row); B
+// is row-major within a group. Callers fetch slabs with k0 < K (or k0 = 0
+// when K = 0, which reads nothing). `wave` must be wave-uniform.
+template <class T>
+__device__ __forceinline__ void dma_slab(const float *__restrict__ A, const float *__restrict__ B, int64_t M,
+                                         int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t m0, int64_t n0,
+                                         int64_t k0, float *As, float *Bs, int wave, int lane) {
+  const u32x4 ra = rows_desc(A + m0 * lda, (M - m0) < T::BM ? (M - m0) : T::BM, lda);
+  const u32x4 rb = rows_desc(B + k0 * ldb, (K - k0) < T::BK ? (K - k0) : T::BK, ldb);
+#pragma unroll
+  for (int i = 0; i < T::NA; ++i) {
+    const int idx0 = 64 * wave + kThreads * i;  // first float4 of this wave's instruction
+    const int idx = idx0 + lane;
+    const int ar = idx / T::QP, ak = 4 * ((idx % T::QP) ^ T::aswz(ar));
+    const uint32_t aoff = (k0 + ak < K) ? (uint32_t)((ar * lda + k0 + ak) * 4) : kOutside;
+    dma16(ra, aoff, lds_addr(As + 4 * idx0));
+  }
+#pragma unroll
+  for (int i = 0; i < T::NB; ++i) {
+    const int idx0 = 64 * wave + kThreads * i;
+    const int idx = idx0 + lane;
+    const int bk = idx / T::BROW, bn = 4 * (idx % T::BROW);
+    const uint32_t boff = (n0 + bn < N) ? (uint32_t)((bk * ldb + n0 + bn) * 4) : kOutside;
+    dma16(rb, boff, lds_addr(Bs + T::b_at(idx0 / T::BROW, 4 * (idx0 % T::BROW))));
+  }
+}
+
+// Wait until at most N vector-memory operations of this wave are in flight
+// and all its LDS operations are done, then meet the workgroup. Loads retire
+// in order, so N = the loads issued after the ones awaited. The wait is the
+// s_waitcnt builtin, so the compiler's own bookkeeping knows that LDS reads
+// issued before it are complete; the empty asm before it and the barrier
+// asm after it (both memory clobbers) keep every LDS access on its side.
+template <int N>
+__device__ __forceinline__ void vm_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14].
+  constexpr int kImm = (N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kImm);
+  asm volatile("s_barrier" ::: "memory");
+}
+
+// Fragments of 8-deep chunk c of a stage: the MFMA sums k over its two lane
+// halves, and any permutation of k applied to both operands gives the same
+// product, so lane half h takes k = 8c + 4h + {0..3} (one ds_read_b128 for
+// A) and MFMA step s consumes k = 8c + s (half 0) and 8c + 4 + s (half 1).
+template <int WTM>
+struct Frag {
+  float4 a[WTM];
+  float b[4][4];
+};
+
+template <int WTM, int WTN, class T>
+__device__ __forceinline__ void read_frag(Frag<WTM> &f, const float *__restrict__ As, const float *__restrict__ Bs,
+                                          int c, int wm, int wn, int lane) {
+  const int r = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < WTM; ++i)
+    f.a[i] = *reinterpret_cast<const float4 *>(As + T::a_at(wm * 32 * WTM + i * 32 + r, 2 * c + h));
+#pragma unroll
+  for (int j = 0; j < WTN; ++j)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) f.b[j][s] = Bs[T::b_at(8 * c + 4 * h + s, wn * 32 * WTN + j * 32 + r)];
+}
+
+template <int WTM, int WTN>
+__device__ __forceinline__ void mfma_frag(v16f (&acc)[WTM][WTN], const Frag<WTM> &f) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int i = 0; i < WTM; ++i) {
+      const float av = s == 0 ? f.a[i].x : s == 1 ? f.a[i].y : s == 2 ? f.a[i].z : f.a[i].w;
+#pragma unroll
+      for (int j = 0; j < WTN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, f.b[j][s], acc[i][j], 0, 0, 0);
+    }
 }
 
 template <int WTM, int WTN, class T>
 __device__ __forceinline__ void compute_slab(v16f (&acc)[WTM][WTN], const float *__restrict__ As,
                                              const float *__restrict__ Bs, int wm, int wn, int lane) {
-  const int r = lane & 31, h = lane >> 5;
 #pragma unroll
   for (int c = 0; c < T::BK / 8; ++c) {
-    float4 a[WTM];
-    float b[WTN][4];
-#pragma unroll
-    for (int i = 0; i < WTM; ++i)
-      a[i] = *reinterpret_cast<const float4 *>(As + (wm * 32 * WTM + i * 32 + r) * T::LDA + 8 * c + 4 * h);
-#pragma unroll
-    for (int j = 0; j < WTN; ++j)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) b[j][s] = Bs[(8 * c + 4 * h + s) * T::LDB + wn * 32 * WTN + j * 32 + r];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-#pragma unroll
-      for (int i = 0; i < WTM; ++i) {
-        const float av = s == 0 ? a[i].x : s == 1 ? a[i].y : s == 2 ? a[i].z : a[i].w;
-#pragma unroll
-        for (int j = 0; j < WTN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, b[j][s], acc[i][j], 0, 0, 0);
-      }
-    }
+    Frag<WTM> f;
+    read_frag<WTM, WTN, T>(f, As, Bs, c, wm, wn, lane);
+    mfma_frag<WTM, WTN>(acc, f);
   }
 }
 
@@ -161,17 +278,109 @@ __device__ __forceinline__ void tile_coords(int64_t pid, int64_t tiles_m, int64_
   tn = (pid % width) / gsz;
 }
 
-// One workgroup's loop over its tiles. VEC selects the fast slab loads.
-// As, Bs: the two LDS stages, A_STAGE and B_STAGE floats apart. (Offsets
-// from one base keep the pointers visibly in LDS for the compiler; an array
-// of stage pointers would turn every LDS access into a flat one.)
-template <int WTM, int WTN, int BKT, bool VEC, bool PRIO>
+// Pipelines over the K slabs of one tile, accumulating into acc.
+//
+// DMA (direct-to-LDS, three stages; slab j in stage j % 3): the barrier sits
+// after each slab's first 8-deep chunk. Once it passes, slab ks+1 has landed
+// and every wave is done with slab ks-1, so slab ks+2's loads go into ks-1's
+// stage and slab ks+1's first fragments are read while this slab's later
+// chunks, already in registers, feed the MFMAs: no wave waits on LDS data
+// right after a barrier, and each slab has one slab-time to arrive.
+template <int WTM, int WTN, class T, bool PRIO>
+__device__ __forceinline__ void k_loop_dma(v16f (&acc)[WTM][WTN], const float *__restrict__ Ap,
+                                           const float *__restrict__ Bp, int64_t M, int64_t N, int64_t K,
+                                           int64_t lda, int64_t ldb, int64_t m0, int64_t n0, int64_t nslabs,
+                                           float *As, float *Bs, int wave, int wm, int wn, int lane) {
+  constexpr int BK = T::BK;
+  constexpr int C = BK / 8;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  dma_slab<T>(Ap, Bp, M, N, K, lda, ldb, m0, n0, 0, As, Bs, wv, lane);
+  if (nslabs > 1) {
+    dma_slab<T>(Ap, Bp, M, N, K, lda, ldb, m0, n0, BK, As + T::A_STAGE, Bs + T::B_STAGE, wv, lane);
+    vm_barrier<T::NA + T::NB>();
+  } else {
+    vm_barrier<0>();
+  }
+  Frag<WTM> f0, f1;
+  read_frag<WTM, WTN, T>(f0, As, Bs, 0, wm, wn, lane);
+  int cur = 0;
+  for (int64_t ks = 0; ks < nslabs; ++ks) {
+    const int nxt = cur == 2 ? 0 : cur + 1;
+    const int fut = nxt == 2 ? 0 : nxt + 1;
+    const float *sA = As + cur * T::A_STAGE, *sB = Bs + cur * T::B_STAGE;
+    if constexpr (C > 1) read_frag<WTM, WTN, T>(f1, sA, sB, 1, wm, wn, lane);
+    if (PRIO) __builtin_amdgcn_s_setprio(1);
+    mfma_frag<WTM, WTN>(acc, f0);
+    if (PRIO) __builtin_amdgcn_s_setprio(0);
+    vm_barrier<0>();
+    if (ks + 2 < nslabs)
+      dma_slab<T>(Ap, Bp, M, N, K, lda, ldb, m0, n0, (ks + 2) * BK, As + fut * T::A_STAGE, Bs + fut * T::B_STAGE,
+                  wv, lane);
+    if (ks + 1 < nslabs) read_frag<WTM, WTN, T>(f0, As + nxt * T::A_STAGE, Bs + nxt * T::B_STAGE, 0, wm, wn, lane);
+    if (PRIO) __builtin_amdgcn_s_setprio(1);
+    if constexpr (C > 1) mfma_frag<WTM, WTN>(acc, f1);
+#pragma unroll
+    for (int c = 2; c < C; ++c) {
+      read_frag<WTM, WTN, T>(f1, sA, sB, c, wm, wn, lane);
+      mfma_frag<WTM, WTN>(acc, f1);
+    }
+    if (PRIO) __builtin_amdgcn_s_setprio(0);
+    cur = nxt;
+  }
+  // The next tile's first loads reuse stages 0 and 1.
+  vm_barrier<0>();
+}
+
+// Register-staged (two stages): the next slab's global loads are in flight
+// while the current slab feeds the MFMAs, one barrier per slab.
+template <int WTM, int WTN, class T, bool PRIO>
+__device__ __forceinline__ void k_loop_regs(v16f (&acc)[WTM][WTN], const float *__restrict__ Ap,
+                                            const float *__restrict__ Bp, int64_t M, int64_t N, int64_t K,
+                                            int64_t lda, int64_t ldb, int64_t m0, int64_t n0, int64_t nslabs,
+                                            float *As, float *Bs, int tid, int wm, int wn, int lane) {
+  Slab<T> s;
+  load_slab_vec<T>(s, Ap, Bp, M, N, K, lda, ldb, m0, n0, 0, tid);
+  store_slab<T>(s, As, Bs, tid);
+  __syncthreads();
+  for (int64_t ks = 0; ks < nslabs; ++ks) {
+    const int cur = ks & 1;
+    const bool more = ks + 1 < nslabs;
+    if (more) load_slab_vec<T>(s, Ap, Bp, M, N, K, lda, ldb, m0, n0, (ks + 1) * T::BK, tid);
+    if (PRIO) __builtin_amdgcn_s_setprio(1);
+    compute_slab<WTM, WTN, T>(acc, As + cur * T::A_STAGE, Bs + cur * T::B_STAGE, wm, wn, lane);
+    if (PRIO) __builtin_amdgcn_s_setprio(0);
+    if (more) store_slab<T>(s, As + (cur ^ 1) * T::A_STAGE, Bs + (cur ^ 1) * T::B_STAGE, tid);
+    __syncthreads();
+  }
+}
+
+// Generic (any shape, stride, alignment): synchronous, one stage.
+template <int WTM, int WTN, class T>
+__device__ __forceinline__ void k_loop_generic(v16f (&acc)[WTM][WTN], const float *__restrict__ Ap,
+                                               const float *__restrict__ Bp, int64_t M, int64_t N, int64_t K,
+                                               int64_t lda, int64_t ldb, int64_t m0, int64_t n0, int64_t nslabs,
+                                               bool a_vec, bool b_vec, float *As, float *Bs, int tid, int wm, int wn,
+                                               int lane) {
+  for (int64_t ks = 0; ks < nslabs; ++ks) {
+    Slab<T> s;
+    load_slab<T>(s, Ap, Bp, M, N, K, lda, ldb, m0, n0, ks * T::BK, a_vec, b_vec, tid);
+    store_slab<T>(s, As, Bs, tid);
+    __syncthreads();
+    compute_slab<WTM, WTN, T>(acc, As, Bs, wm, wn, lane);
+    __syncthreads();
+  }
+}
+
+// One workgroup's loop over its tiles. PATH: 0 generic, 1 register-staged,
+// 2 direct-to-LDS. As, Bs: the LDS stages, A_STAGE and B_STAGE floats apart.
+// (Offsets from one base keep the pointers visibly in LDS for the compiler;
+// an array of stage pointers would turn every LDS access into a flat one.)
+template <int WTM, int WTN, int BKT, int PATH, bool PRIO>
 __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const float *__restrict__ Bp,
                                            float *__restrict__ Cp, int64_t M, int64_t N, int64_t K, int64_t lda,
                                            int64_t ldb, int64_t ldc, bool a_vec, bool b_vec, float *As,
                                            float *Bs) {
-  using T = Tile<WTM, WTN, BKT>;
-  constexpr int BK = T::BK;
+  using T = Tile<WTM, WTN, BKT, PATH == 2>;
   const int tid = threadIdx.x;
   const int lane = kh::lane_id();
   const int wave = tid >> 6;
@@ -179,7 +388,7 @@ __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const f
 
   const int64_t tiles_m = (M + T::BM - 1) / T::BM, tiles_n = (N + T::BN - 1) / T::BN;
   const int64_t total = tiles_m * tiles_n;
-  const int64_t nslabs = (K + BK - 1) / BK;
+  const int64_t nslabs = (K + T::BK - 1) / T::BK;
   const int64_t nblocks = (int64_t)gridDim.x * gridDim.y * gridDim.z;
   const int64_t bid = blockIdx.x + (int64_t)gridDim.x * (blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
   const bool xcd_remap = (nblocks == total) && ((total & 7) == 0);
@@ -195,31 +404,13 @@ __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const f
 #pragma unroll
       for (int j = 0; j < WTN; ++j) acc[i][j] = v16f{};
 
-    if (VEC) {
-      Slab<T> s;
-      load_slab_vec<T>(s, Ap, Bp, M, N, K, lda, ldb, m0, n0, 0, tid);
-      store_slab<T>(s, As, Bs, tid);
-      __syncthreads();
-      for (int64_t ks = 0; ks < nslabs; ++ks) {
-        const int cur = ks & 1;
-        const bool more = ks + 1 < nslabs;
-        if (more) load_slab_vec<T>(s, Ap, Bp, M, N, K, lda, ldb, m0, n0, (ks + 1) * BK, tid);
-        if (PRIO) __builtin_amdgcn_s_setprio(1);
-        compute_slab<WTM, WTN, T>(acc, As + cur * T::A_STAGE, Bs + cur * T::B_STAGE, wm, wn, lane);
-        if (PRIO) __builtin_amdgcn_s_setprio(0);
-        if (more) store_slab<T>(s, As + (cur ^ 1) * T::A_STAGE, Bs + (cur ^ 1) * T::B_STAGE, tid);
-        __syncthreads();
-      }
-    } else {
-      for (int64_t ks = 0; ks < nslabs; ++ks) {
-        Slab<T> s;
-        load_slab<T>(s, Ap, Bp, M, N, K, lda, ldb, m0, n0, ks * BK, a_vec, b_vec, tid);
-        store_slab<T>(s, As, Bs, tid);
-        __syncthreads();
-        compute_slab<WTM, WTN, T>(acc, As, Bs, wm, wn, lane);
-        __syncthreads();
-      }
-    }
+    if constexpr (PATH == 2)
+      k_loop_dma<WTM, WTN, T, PRIO>(acc, Ap, Bp, M, N, K, lda, ldb, m0, n0, nslabs, As, Bs, wave, wm, wn, lane);
+    else if constexpr (PATH == 1)
+      k_loop_regs<WTM, WTN, T, PRIO>(acc, Ap, Bp, M, N, K, lda, ldb, m0, n0, nslabs, As, Bs, tid, wm, wn, lane);
+    else
+      k_loop_generic<WTM, WTN, T>(acc, Ap, Bp, M, N, K, lda, ldb, m0, n0, nslabs, a_vec, b_vec, As, Bs, tid, wm,
+                                  wn, lane);
 
     // Accumulator layout: lane l, register r -> row 8(r/4) + 4(l/32) + r%4,
     // column l%32 of the 32x32 block.
@@ -239,21 +430,31 @@ __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const f
   }
 }
 
-template <int WTM, int WTN, int BKT, bool PRIO>
+// Stages of LDS the fast path of a tile uses (the generic path uses one).
+template <bool DMA>
+constexpr int kStages = DMA ? 3 : 2;
+
+// Kernel body. DMA selects the direct-to-LDS pipeline for the fast path
+// (aligned operands, k and n multiples of 4, 32-bit tile offsets); otherwise
+// the register-staged one. Other operands take the generic path.
+template <int WTM, int WTN, int BKT, bool PRIO, bool DMA>
 __device__ __forceinline__ void gemm_entry(const float *__restrict__ Ap, const float *__restrict__ Bp,
                                            float *__restrict__ Cp, int64_t M, int64_t N, int64_t K, int64_t lda,
                                            int64_t ldb, int64_t ldc) {
-  using T = Tile<WTM, WTN, BKT>;
-  __shared__ __attribute__((aligned(16))) float As[2 * T::A_STAGE];
-  __shared__ __attribute__((aligned(16))) float Bs[2 * T::B_STAGE];
+  using T = Tile<WTM, WTN, BKT, DMA>;
+  using G = Tile<WTM, WTN, BKT, false>;  // the generic path's layout
+  constexpr int kA = kStages<DMA> * T::A_STAGE > G::A_STAGE ? kStages<DMA> * T::A_STAGE : G::A_STAGE;
+  constexpr int kB = kStages<DMA> * T::B_STAGE > G::B_STAGE ? kStages<DMA> * T::B_STAGE : G::B_STAGE;
+  __shared__ __attribute__((aligned(16))) float As[kA];
+  __shared__ __attribute__((aligned(16))) float Bs[kB];
   const bool a_vec = ((K & 3) == 0) && ((lda & 3) == 0) && kh::aligned16(Ap);
   const bool b_vec = ((N & 3) == 0) && ((ldb & 3) == 0) && kh::aligned16(Bp);
   // The fast loads address a tile's rows with 32-bit byte offsets.
   const bool fits32 = (int64_t)T::BM * lda * 4 < (1ll << 31) && (int64_t)T::BK * ldb * 4 < (1ll << 31);
   if (a_vec && b_vec && fits32)
-    gemm_tiles<WTM, WTN, BKT, true, PRIO>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, As, Bs);
+    gemm_tiles<WTM, WTN, BKT, DMA ? 2 : 1, PRIO>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, As, Bs);
   else
-    gemm_tiles<WTM, WTN, BKT, false, PRIO>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, As, Bs);
+    gemm_tiles<WTM, WTN, BKT, 0, PRIO>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, As, Bs);
 }
 
 }  // namespace khg
