@@ -43,8 +43,8 @@ METRIC = "GEMM-8192 fp32 TFLOPS + softmax/scan HBM GB/s, % of MI355X roofline"
 # 2.000 and WRITE_SIZE by 1.000, the factors a copy kernel of known size
 # reads), recorded in profiles/templates_baseline_sizes_hbm_traffic.md.
 PMC_TRAFFIC_BYTES = {
-    "vecadd": 201374106, "softmax": 33634176, "layernorm": 33726643, "scan": 539478867,
-    "fused_gelu": 537009843, "gemm": 4479760026, "attention": 1208113510,
+    "vecadd": 201374029, "softmax": 33634381, "layernorm": 33726720, "scan": 539689555,
+    "fused_gelu": 537025664, "gemm": 3962909261, "attention": 1208112794,
 }
 
 
