@@ -26,11 +26,23 @@
 //   exchange per tile, its sum one at the end; O^T's rows are head-dim
 //   elements, so the final store is four dwordx4 per lane per 32 columns.
 //
+// Pipelining: within one wave, tile t's softmax needs tile t's S^T, and its
+// PV MFMAs need the softmax, but tile t+1's S^T needs only K. So K runs one
+// tile ahead of V through the two LDS buffers, and each iteration issues
+// tile t+1's S^T MFMAs alongside tile t's softmax VALU work; the exp, max
+// and scaling then run while the wave's own MFMAs execute instead of only in
+// the other wave's shadow (131 -> 135 TFLOP/s at b4 h16 s4096). The loop
+// covers the tiles that have a successor, all full, with no branches inside
+// (K/V arrive by range-checked buffer loads); the last tile, the only one
+// that can be partial, is masked and finished after it.
+//
 // Tails: query rows >= seq are computed from zeros and not stored; key rows
 // >= seq get S = -inf and V = 0. Query tiles are grid-strided in x, so any
 // grid is correct, including the reference's (seq, heads, batch) x 64
 // geometry (kernelh_backend.cpp:420-422). Workgroups of exactly 256 threads
-// double-buffer the K/V tiles; other sizes stage them synchronously.
+// over 16-byte aligned rows of at least 64 floats take the pipelined path;
+// other launches stage each tile synchronously, and rows that are not
+// 16-byte aligned are read and written a float at a time.
 #include "kh_device.h"
 #include "kh_tiles.h"
 
@@ -46,38 +58,6 @@ constexpr int LDV = TK + 4;    // V^T tile in LDS: [d][key], padded rows
 constexpr int kFastThreads = 256;
 constexpr float kNegBig = -1e30f;  // finite "minus infinity" seed for m
 
-struct KVRegs {
-  float4 k[4];
-  float4 v[4];
-};
-
-// Fast path (256 threads): thread t moves 4 float4 of K and 4 of V.
-// K: key = t/16 + 16i, d4 = t%16 (16 lanes per key row, coalesced).
-// V: key = t%64, d4 = t/64 + 4i (written transposed, consecutive lanes hit
-// consecutive keys of one V^T row).
-__device__ __forceinline__ void load_kv(KVRegs &r, const float *__restrict__ Kg, const float *__restrict__ Vg,
-                                        int64_t ks, int64_t key0, int64_t seq, int tid) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t kk = key0 + (tid >> 4) + 16 * i;
-    r.k[i] = kk < seq ? *reinterpret_cast<const float4 *>(Kg + kk * ks + 4 * (tid & 15)) : make_float4(0, 0, 0, 0);
-    const int64_t vk = key0 + (tid & 63);
-    r.v[i] = vk < seq ? *reinterpret_cast<const float4 *>(Vg + vk * ks + 4 * ((tid >> 6) + 4 * i))
-                      : make_float4(0, 0, 0, 0);
-  }
-}
-
-__device__ __forceinline__ void store_kv(const KVRegs &r, float *__restrict__ Ks, float *__restrict__ Vt, int tid) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    *reinterpret_cast<float4 *>(Ks + ((tid >> 4) + 16 * i) * LDK + 4 * (tid & 15)) = r.k[i];
-    const int d = 4 * ((tid >> 6) + 4 * i), key = tid & 63;
-    Vt[(d + 0) * LDV + key] = r.v[i].x;
-    Vt[(d + 1) * LDV + key] = r.v[i].y;
-    Vt[(d + 2) * LDV + key] = r.v[i].z;
-    Vt[(d + 3) * LDV + key] = r.v[i].w;
-  }
-}
 
 // Any workgroup size: synchronous strided staging of one tile.
 __device__ __forceinline__ void stage_kv_generic(float *__restrict__ Ks, float *__restrict__ Vt,
@@ -95,12 +75,9 @@ __device__ __forceinline__ float comp(const float4 &v, int s) {
   return s == 0 ? v.x : s == 1 ? v.y : s == 2 ? v.z : v.w;
 }
 
-// One key tile for one wave: S^T, online softmax update, O^T accumulation.
-__device__ __forceinline__ void attend_tile(v16f (&o)[2], float &m, float &l, const float4 (&q)[8],
-                                            const float *__restrict__ Ks, const float *__restrict__ Vt,
-                                            int64_t key0, int64_t seq, int lane) {
+// S^T of one key tile for one wave (64 MFMAs).
+__device__ __forceinline__ void qk_tile(v16f (&s)[2], const float4 (&q)[8], const float *__restrict__ Ks, int lane) {
   const int r = lane & 31, h = lane >> 5;
-  v16f s[2];
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt) {
     s[kt] = v16f{};
@@ -112,8 +89,15 @@ __device__ __forceinline__ void attend_tile(v16f (&o)[2], float &m, float &l, co
         s[kt] = __builtin_amdgcn_mfma_f32_32x32x2f32(comp(a, st), comp(q[c], st), s[kt], 0, 0, 0);
     }
   }
+}
+
+// Online-softmax update of one tile's S^T (into P, in place), then O^T += V^T P^T.
+template <bool MASK>
+__device__ __forceinline__ void softmax_pv(v16f (&o)[2], float &m, float &l, v16f (&s)[2],
+                                           const float *__restrict__ Vt, int64_t key0, int64_t seq, int lane) {
+  const int r = lane & 31, h = lane >> 5;
   // Mask keys past the end (only in the last, partial tile).
-  if (key0 + TK > seq) {
+  if (MASK && key0 + TK > seq) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -160,6 +144,147 @@ __device__ __forceinline__ void attend_tile(v16f (&o)[2], float &m, float &l, co
   }
 }
 
+// Fast-path K and V staging, split so K can run a tile ahead of V. Branch-free
+// buffer loads over the slice's rows: rows at or past seq read 0 through
+// the hardware range check.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 as_f4(u32x4 u) {
+  return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+}
+__device__ __forceinline__ void load_k(float4 (&k)[4], __amdgpu_buffer_rsrc_t rk, int64_t ks, int64_t key0, int tid) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t off = (uint32_t)(((key0 + (tid >> 4) + 16 * i) * ks + 4 * (tid & 15)) * 4);
+    k[i] = as_f4(__builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+  }
+}
+__device__ __forceinline__ void load_v(float4 (&v)[4], __amdgpu_buffer_rsrc_t rv, int64_t ks, int64_t key0, int tid) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t off = (uint32_t)(((key0 + (tid & 63)) * ks + 4 * ((tid >> 6) + 4 * i)) * 4);
+    v[i] = as_f4(__builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+  }
+}
+__device__ __forceinline__ void store_k(const float4 (&k)[4], float *__restrict__ Ks, int tid) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) *reinterpret_cast<float4 *>(Ks + ((tid >> 4) + 16 * i) * LDK + 4 * (tid & 15)) = k[i];
+}
+__device__ __forceinline__ void store_v(const float4 (&v)[4], float *__restrict__ Vt, int tid) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = 4 * ((tid >> 6) + 4 * i), key = tid & 63;
+    Vt[(d + 0) * LDV + key] = v[i].x;
+    Vt[(d + 1) * LDV + key] = v[i].y;
+    Vt[(d + 2) * LDV + key] = v[i].z;
+    Vt[(d + 3) * LDV + key] = v[i].w;
+  }
+}
+
+// One workgroup's query tiles of one (b, h) slice. VEC4: rows of Q, K, V and
+// O are 16-byte aligned (float4 access, and the pipelined path for 256-thread
+// workgroups); otherwise Q and O move a float at a time and tiles are staged
+// synchronously. Ks, Vt: two LDS tile buffers each, one tile apart.
+template <bool VEC4>
+__device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, const float *__restrict__ Kg,
+                                                const float *__restrict__ Vg, float *__restrict__ Og, int64_t qs,
+                                                int64_t ks, int64_t os, int64_t seq, float *Ks, float *Vt) {
+  const int tid = threadIdx.x;
+  const int lane = kh::lane_id();
+  const int wave = tid / kh::kWave;
+  const int nwaves = blockDim.x / kh::kWave;
+  const int r = lane & 31, h = lane >> 5;
+  const int64_t rows_per_block = (int64_t)QW * nwaves;
+  const int64_t nqt = (seq + rows_per_block - 1) / rows_per_block;
+  const int64_t ntiles = (seq + TK - 1) / TK;
+  // The fast path's buffer loads address the slice with 32-bit offsets and
+  // bound it by seq rows of ks floats, so every row must hold its D floats.
+  const bool fast = VEC4 && blockDim.x == kFastThreads && ks >= D && (seq + 2 * TK) * ks * 4 < (1ll << 31);
+  // log2(e)/sqrt(d): S^T comes out in log2 units, so exp(S - m) = 2^(S' - m').
+  const float qscale = kh::kLog2e * 0.125f;
+
+  for (int64_t qt = blockIdx.x; qt < nqt; qt += gridDim.x) {
+    const int64_t q_row = qt * rows_per_block + (int64_t)wave * QW + r;
+    float4 q[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      float4 v = make_float4(0, 0, 0, 0);
+      if (q_row < seq) {
+        const float *p = Qg + q_row * qs + 8 * c + 4 * h;
+        v = VEC4 ? *reinterpret_cast<const float4 *>(p) : make_float4(p[0], p[1], p[2], p[3]);
+      }
+      q[c] = make_float4(v.x * qscale, v.y * qscale, v.z * qscale, v.w * qscale);
+    }
+    v16f o[2] = {v16f{}, v16f{}};
+    float m = kNegBig, l = 0.0f;
+
+    if (fast) {
+      // K runs a tile ahead of V: iteration t computes S^T of tile t+1 while
+      // tile t's softmax and PV run, so one wave's VALU work overlaps its own
+      // MFMAs. Buffer j % 2 of Ks holds K of tile j, of Vt V of tile j. The
+      // loop covers the tiles that have a successor (all full); the last
+      // tile, the only one that can be partial, is finished after it.
+      const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(Kg), (short)0,
+                                                                          (int)(seq * ks * 4), 0x00020000);
+      const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(Vg), (short)0,
+                                                                          (int)(seq * ks * 4), 0x00020000);
+      float4 kr[4], vr[4];
+      load_k(kr, rk, ks, 0, tid);
+      load_v(vr, rv, ks, 0, tid);
+      store_k(kr, Ks, tid);
+      store_v(vr, Vt, tid);
+      load_k(kr, rk, ks, TK, tid);
+      store_k(kr, Ks + TK * LDK, tid);
+      __syncthreads();
+      v16f sc[2], sn[2];
+      qk_tile(sc, q, Ks, lane);
+      for (int64_t t = 0; t + 1 < ntiles; ++t) {
+        const int cur = t & 1;
+        load_k(kr, rk, ks, (t + 2) * TK, tid);
+        load_v(vr, rv, ks, (t + 1) * TK, tid);
+        qk_tile(sn, q, Ks + (cur ^ 1) * TK * LDK, lane);
+        softmax_pv<false>(o, m, l, sc, Vt + cur * D * LDV, t * TK, seq, lane);
+        store_k(kr, Ks + cur * TK * LDK, tid);
+        store_v(vr, Vt + (cur ^ 1) * D * LDV, tid);
+        __syncthreads();
+        sc[0] = sn[0];
+        sc[1] = sn[1];
+      }
+      softmax_pv<true>(o, m, l, sc, Vt + ((ntiles - 1) & 1) * D * LDV, (ntiles - 1) * TK, seq, lane);
+    } else {
+      for (int64_t t = 0; t < ntiles; ++t) {
+        stage_kv_generic(Ks, Vt, Kg, Vg, ks, t * TK, seq);
+        __syncthreads();
+        v16f sg[2];
+        qk_tile(sg, q, Ks, lane);
+        softmax_pv<true>(o, m, l, sg, Vt, t * TK, seq, lane);
+        __syncthreads();
+      }
+    }
+
+    // O = acc / l; both halves of a lane pair hold partial sums of l.
+    const float lt = l + __shfl_xor(l, 32, kh::kWave);
+    const float inv = 1.0f / lt;
+    if (q_row < seq) {
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int k4 = 0; k4 < 4; ++k4) {
+          const float4 v = make_float4(o[dt][4 * k4] * inv, o[dt][4 * k4 + 1] * inv, o[dt][4 * k4 + 2] * inv,
+                                       o[dt][4 * k4 + 3] * inv);
+          float *p = Og + q_row * os + dt * 32 + 8 * k4 + 4 * h;
+          if (VEC4) {
+            *reinterpret_cast<float4 *>(p) = v;
+          } else {
+            p[0] = v.x;
+            p[1] = v.y;
+            p[2] = v.z;
+            p[3] = v.w;
+          }
+        }
+    }
+  }
+}
+
 }  // namespace
 
 // Registers capped for two waves per SIMD (two workgroups per CU, as LDS
@@ -180,69 +305,15 @@ attention(KH_MEMREF4(const float, Q), KH_MEMREF4(const float, K), KH_MEMREF4(con
   const float *__restrict__ Kg = Kp + bb * K_s0 + hb * K_s1;
   const float *__restrict__ Vg = Vp + bb * V_s0 + hb * V_s1;
   float *__restrict__ Og = Op + bb * O_s0 + hb * O_s1;
-  const int64_t qs = Q_s2, ks = K_s2, os = O_s2;
 
-  __shared__ __attribute__((aligned(16))) float Ks[2][TK * LDK];
-  __shared__ __attribute__((aligned(16))) float Vt[2][D * LDV];
+  __shared__ __attribute__((aligned(16))) float Ks[2 * TK * LDK];
+  __shared__ __attribute__((aligned(16))) float Vt[2 * D * LDV];
 
-  const int tid = threadIdx.x;
-  const int lane = kh::lane_id();
-  const int wave = tid / kh::kWave;
-  const int nwaves = blockDim.x / kh::kWave;
-  const int r = lane & 31, h = lane >> 5;
-  const int64_t rows_per_block = (int64_t)QW * nwaves;
-  const int64_t nqt = (seq + rows_per_block - 1) / rows_per_block;
-  const int64_t ntiles = (seq + TK - 1) / TK;
-  const bool fast = blockDim.x == kFastThreads;
-  // log2(e)/sqrt(d): S^T comes out in log2 units, so exp(S - m) = 2^(S' - m').
-  const float qscale = kh::kLog2e * 0.125f;
-
-  for (int64_t qt = blockIdx.x; qt < nqt; qt += gridDim.x) {
-    const int64_t q_row = qt * rows_per_block + (int64_t)wave * QW + r;
-    float4 q[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      float4 v = q_row < seq ? *reinterpret_cast<const float4 *>(Qg + q_row * qs + 8 * c + 4 * h)
-                             : make_float4(0, 0, 0, 0);
-      q[c] = make_float4(v.x * qscale, v.y * qscale, v.z * qscale, v.w * qscale);
-    }
-    v16f o[2] = {v16f{}, v16f{}};
-    float m = kNegBig, l = 0.0f;
-
-    if (fast) {
-      KVRegs kv;
-      load_kv(kv, Kg, Vg, ks, 0, seq, tid);
-      store_kv(kv, Ks[0], Vt[0], tid);
-      __syncthreads();
-      for (int64_t t = 0; t < ntiles; ++t) {
-        const int cur = t & 1;
-        const bool more = t + 1 < ntiles;
-        if (more) load_kv(kv, Kg, Vg, ks, (t + 1) * TK, seq, tid);
-        attend_tile(o, m, l, q, Ks[cur], Vt[cur], t * TK, seq, lane);
-        if (more) store_kv(kv, Ks[cur ^ 1], Vt[cur ^ 1], tid);
-        __syncthreads();
-      }
-    } else {
-      for (int64_t t = 0; t < ntiles; ++t) {
-        stage_kv_generic(Ks[0], Vt[0], Kg, Vg, ks, t * TK, seq);
-        __syncthreads();
-        attend_tile(o, m, l, q, Ks[0], Vt[0], t * TK, seq, lane);
-        __syncthreads();
-      }
-    }
-
-    // O = acc / l; both halves of a lane pair hold partial sums of l.
-    const float lt = l + __shfl_xor(l, 32, kh::kWave);
-    const float inv = 1.0f / lt;
-    if (q_row < seq) {
-#pragma unroll
-      for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-        for (int k4 = 0; k4 < 4; ++k4) {
-          const float4 v = make_float4(o[dt][4 * k4] * inv, o[dt][4 * k4 + 1] * inv, o[dt][4 * k4 + 2] * inv,
-                                       o[dt][4 * k4 + 3] * inv);
-          *reinterpret_cast<float4 *>(Og + q_row * os + dt * 32 + 8 * k4 + 4 * h) = v;
-        }
-    }
-  }
+  // float4 access to Q, K, V and O needs 16-byte aligned rows.
+  const bool vec4 = kh::aligned16(Qp) && kh::aligned16(Kp) && kh::aligned16(Vp) && kh::aligned16(Op) &&
+                    ((Q_s0 | Q_s1 | Q_s2 | K_s0 | K_s1 | K_s2 | V_s0 | V_s1 | V_s2 | O_s0 | O_s1 | O_s2) & 3) == 0;
+  if (vec4)
+    attention_slice<true>(Qg, Kg, Vg, Og, Q_s2, K_s2, O_s2, seq, Ks, Vt);
+  else
+    attention_slice<false>(Qg, Kg, Vg, Og, Q_s2, K_s2, O_s2, seq, Ks, Vt);
 }

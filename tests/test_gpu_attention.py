@@ -78,6 +78,39 @@ def test_attention_ragged_sequences(dev, b, h, s):
     _check(Q, K, V, _attention(Q, K, V, b, h, s), b, h, s)
 
 
+@pytest.mark.parametrize("pitch", [80, 68, 66])
+def test_attention_padded_row_stride(dev, pitch):
+    """[b, h, s, d] slices whose rows are `pitch` floats apart (d = 64 used):
+    the kernel takes the row stride from the memref (attention.cpp reads
+    s2 through the descriptor). 80 and 68 keep rows 16-byte aligned (the
+    pipelined float4 path); 66 does not (the element-wise path). The padding
+    holds NaN, so a read past a row's 64 floats shows up as a non-finite
+    output."""
+    b, h, s = 2, 2, 200
+    n = b * h * s * D
+    Q = O.normal(n, 11, 0.0, 1.0)
+    K = O.normal(n, 12, 0.0, 1.0)
+    V = O.normal(n, 13, 0.0, 1.0)
+
+    def padded(x):
+        p = np.full((b * h * s, pitch), np.nan, np.float32)
+        p[:, :D] = x.reshape(b * h * s, D)
+        return up(p.ravel())
+
+    dq, dk, dv, do = padded(Q), padded(K), padded(V), up(np.zeros(b * h * s * pitch, np.float32))
+    args = kh.LaunchArgs()
+    for buf in (dq, dk, dv, do):
+        args.add_memref(buf, [b, h, s, D])
+    # Rank-4 descriptor: ptr, ptr, offset, 4 sizes, 4 strides (slots 7..10).
+    for i in range(4):
+        base = 11 * i
+        args.slots[base + 7:base + 11] = [h * s * pitch, s * pitch, pitch, 1]
+    say(f"attention padded rows pitch={pitch} b={b} h={h} s={s}")
+    kh.kernel_launch(kh.template_function("attention"), ((s + 127) // 128, h, b), (256, 1, 1), args)
+    got = down(do, b * h * s * pitch).reshape(b * h, s, pitch)[:, :, :D]
+    _check(Q, K, V, np.ascontiguousarray(got), b, h, s)
+
+
 def test_attention_reference_geometry_and_negative_control(dev):
     b, h, s = 1, 2, 256
     n = b * h * s * D
