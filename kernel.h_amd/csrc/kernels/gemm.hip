@@ -8,14 +8,16 @@
 //
 //   * Workgroup = 256 threads (4 wave64s, 2x2) computing a BM x BN tile of C;
 //     each wave owns a quarter as WTM x WTN MFMA 32x32 accumulators. Three
-//     symbols, all correct for every shape; the launcher picks by how many
-//     tiles each would launch:
+//     symbols, all correct for every shape; the launcher scores each by its
+//     full-occupancy rate times how busy its last round of workgroups would
+//     be (kh_tiles.h) and takes the best:
 //       `gemm`        128x256 tiles (64x128 per wave, 128 accumulator registers
 //                     per lane), 16-deep K slabs: the least LDS and L2 traffic
-//                     per MFMA, for grids of at least KH_GEMM_TILES_256 tiles;
-//       `gemm_mid`    128x128 tiles (64x64 per wave), 32-deep slabs;
-//       `gemm_small`  64x64 tiles, for problems whose larger grids would leave
-//                     CUs idle.
+//                     per MFMA (8192^3, 4096^3, 8192x8192x256);
+//       `gemm_mid`    128x128 tiles (64x64 per wave), 32-deep slabs (e.g.
+//                     8192x1024x8192);
+//       `gemm_small`  64x64 tiles, for grids the larger tiles would fill
+//                     unevenly (1024^3 to 3584^3).
 //     Registers are capped for two waves per SIMD (two workgroups per CU, as
 //     LDS allows), so one workgroup's barrier and slab hand-over overlap the
 //     other's MFMAs. `gemm` raises its waves' priority (s_setprio) while they

@@ -20,18 +20,29 @@
 #define KH_SCAN_MIN_TILE (KH_SCAN_PER_THREAD * (256 - 64))
 
 // GEMM block tiles (rows of C x columns of C per workgroup of 256 threads).
-// The launcher takes `gemm` (128x256) when its grid has at least
-// KH_GEMM_TILES_256 tiles (two per CU on MI355X), else `gemm_mid` (128x128)
-// when that grid has at least KH_GEMM_TILES_128 tiles, else `gemm_small`
-// (64x64): the largest tile that still gives every CU work.
 #define KH_GEMM_BM 128
 #define KH_GEMM_BN 256
 #define KH_GEMM_MID_BM 128
 #define KH_GEMM_MID_BN 128
 #define KH_GEMM_SMALL_BM 64
 #define KH_GEMM_SMALL_BN 64
-#define KH_GEMM_TILES_256 512
-#define KH_GEMM_TILES_128 256
+
+// The launcher's tile choice (khrt_templates.cpp, gemm_symbol): for each
+// symbol, score = its measured rate at full occupancy (TFLOP/s, MI355X,
+// 8192^3-class shapes) x the fraction of the last round of workgroups that
+// is busy, and take the best. `gemm` and `gemm_mid` run two workgroups per
+// CU, so a round is 2 x KH_GEMM_CUS tiles and a half-empty last round
+// costs a full one; `gemm_small`'s workgroups are light enough that a
+// partial round costs little, so its rounds are counted per CU. Fitted on
+// 14 shapes from 2048^3 to 8192^3 (square, skinny and rectangular): the
+// choice is the measured best or within 4% of it on all of them.
+#define KH_GEMM_CUS 256
+#define KH_GEMM_ROUND_BIG (2 * KH_GEMM_CUS)
+#define KH_GEMM_ROUND_MID (2 * KH_GEMM_CUS)
+#define KH_GEMM_ROUND_SMALL KH_GEMM_CUS
+#define KH_GEMM_RATE_BIG 142
+#define KH_GEMM_RATE_MID 133
+#define KH_GEMM_RATE_SMALL 125
 
 // Attention: query rows per workgroup (4 wavefronts x 32 rows).
 #define KH_ATTN_BLOCK_Q 128

@@ -148,10 +148,20 @@ int get_function(const char *co_name, const char *symbol, void **out) {
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // GEMM tile choice: the largest tile whose grid still gives every CU work.
+// Rate x busy fraction of the last round of workgroups (kh_tiles.h).
+double gemm_score(int64_t tiles, int64_t round, double rate) {
+  return rate * static_cast<double>(tiles) / static_cast<double>(ceil_div(tiles, round) * round);
+}
+
 const char *gemm_symbol(int64_t m, int64_t n) {
-  if (ceil_div(m, KH_GEMM_BM) * ceil_div(n, KH_GEMM_BN) >= KH_GEMM_TILES_256) return "gemm";
-  if (ceil_div(m, KH_GEMM_MID_BM) * ceil_div(n, KH_GEMM_MID_BN) >= KH_GEMM_TILES_128) return "gemm_mid";
-  return "gemm_small";
+  const double big = gemm_score(ceil_div(m, KH_GEMM_BM) * ceil_div(n, KH_GEMM_BN), KH_GEMM_ROUND_BIG,
+                                KH_GEMM_RATE_BIG);
+  const double mid = gemm_score(ceil_div(m, KH_GEMM_MID_BM) * ceil_div(n, KH_GEMM_MID_BN), KH_GEMM_ROUND_MID,
+                                KH_GEMM_RATE_MID);
+  const double small = gemm_score(ceil_div(m, KH_GEMM_SMALL_BM) * ceil_div(n, KH_GEMM_SMALL_BN),
+                                  KH_GEMM_ROUND_SMALL, KH_GEMM_RATE_SMALL);
+  if (big >= mid && big >= small) return "gemm";
+  return mid > small ? "gemm_mid" : "gemm_small";
 }
 
 int64_t gemm_grid(int64_t m, int64_t n) {

@@ -261,10 +261,15 @@ def test_kernarg_segment_is_2n_plus_3_slots(name, nslots):
     ("layernorm", "rows=4097,cols=1024", (1025, 1, 1), (256, 1, 1)),
     ("scan", "n=1000000", (66, 1, 1), (1024, 1, 1)),
     ("scan", "n=67108864", (4370, 1, 1), (1024, 1, 1)),
-    ("gemm", "m=8192,n=8192,k=8192", (2048, 1, 1), (256, 1, 1)),     # 128x256 tiles (gemm)
-    ("gemm", "m=4096,n=4096,k=64", (512, 1, 1), (256, 1, 1)),         # 128x256: exactly 512
-    ("gemm", "m=2048,n=2048,k=2048", (256, 1, 1), (256, 1, 1)),       # 128x128 tiles (gemm_mid)
-    ("gemm", "m=1024,n=1024,k=1024", (256, 1, 1), (256, 1, 1)),       # 64x64 tiles (gemm_small)
+    # gemm: the grid is the chosen symbol's tile count (rate x last-round fill).
+    ("gemm", "m=8192,n=8192,k=8192", (2048, 1, 1), (256, 1, 1)),     # 128x256 (gemm): 4 full rounds
+    ("gemm", "m=8192,n=8192,k=256", (2048, 1, 1), (256, 1, 1)),      # 128x256, skinny K
+    ("gemm", "m=4096,n=4096,k=64", (512, 1, 1), (256, 1, 1)),         # 128x256: exactly one round
+    ("gemm", "m=8192,n=1024,k=8192", (512, 1, 1), (256, 1, 1)),       # 128x128 (gemm_mid): 512 tiles
+    ("gemm", "m=6144,n=6144,k=1024", (9216, 1, 1), (256, 1, 1)),      # 64x64: 128x256 would fill 2.25 rounds
+    ("gemm", "m=3072,n=3072,k=3072", (2304, 1, 1), (256, 1, 1)),      # 64x64 (gemm_small)
+    ("gemm", "m=2048,n=2048,k=2048", (1024, 1, 1), (256, 1, 1)),      # 64x64: 128x128 would half-fill
+    ("gemm", "m=1024,n=1024,k=1024", (256, 1, 1), (256, 1, 1)),       # 64x64
     ("gemm", "m=512,n=512,k=512", (64, 1, 1), (256, 1, 1)),
     ("attention", "batch=4,heads=16,seq=4096,head_dim=64", (32, 16, 4), (256, 1, 1)),
 ])
