@@ -10,7 +10,8 @@
   control (e2e_gemm_test.cpp:289-375).
 * Every tile symbol (`gemm` 128x256, `gemm_mid` 128x128, `gemm_small`
   64x64) gives the same results at every shape, whichever the launcher
-  would pick.
+  would pick; and the launcher's own full-grid launch (one workgroup per
+  tile, XCD-remapped) is checked at a large shape it sends to each symbol.
 """
 import numpy as np
 import pytest
@@ -107,3 +108,26 @@ def test_every_gemm_symbol_at_every_shape(dev, symbol, m, n, k):
         assert np.array_equal(C, (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
     else:
         assert O.rel_frobenius(C, O.ref_gemm(A, B, m, n, k)) <= 1e-5
+
+
+@pytest.mark.parametrize("m,n,k,grid", [
+    (6144, 6144, 1024, 9216),   # gemm_small: 128x256 tiles would fill 2.25 rounds
+    (3072, 3072, 3072, 2304),   # gemm_small
+    (8192, 1024, 8192, 512),    # gemm_mid: 512 tiles of 128x128
+    (4096, 4096, 4096, 512),    # gemm: one full round of 128x256
+])
+def test_gemm_launcher_choice_at_scale(dev, m, n, k, grid):
+    assert kh.geometry("gemm", f"m={m},n={n},k={k}")[0] == (grid, 1, 1)
+    rows = np.concatenate([np.arange(0, m, 61), [m - 1]])
+    if k <= 4096:
+        A, B = O.gemm_int_inputs(m, n, k)
+        C = _gemm(A, B, m, n, k)
+        ref = (A[rows].astype(np.float64) @ B.astype(np.float64)).astype(np.float32)  # exact integers
+        assert np.array_equal(C[rows], ref)
+    else:
+        A = O.uniform(m * k, 0xC0 + m, -1.0, 1.0).reshape(m, k)
+        B = O.uniform(k * n, 0xC1 + n, -1.0, 1.0).reshape(k, n)
+        C = _gemm(A, B, m, n, k)
+        err = O.rel_frobenius(C[rows], A[rows].astype(np.float64) @ B.astype(np.float64))
+        print(f"gemm {m}x{n}x{k} rel-frobenius (rows sampled)={err:.3e}")
+        assert err <= 1e-5
