@@ -1,8 +1,12 @@
 """The `kernelh` CLI contract (tools/kernelh/main.cpp; test/lit/cli/compile.test):
 compile writes <kernel>.hsaco (ELF, symbol = kernel name) and .isa, prints
 `wrote ...` lines and `compile ok`; a bogus --target exits 1 listing the valid
-targets; no arguments exits 2; bench without a GPU skips with 77. The GPU
-test runs one timed row and checks the G32 results.csv schema."""
+targets; no arguments exits 2; bench without a GPU skips with 77. Each
+compiled artifact carries the instructions its kernel's design depends on
+(MFMA, direct-to-LDS loads, DPP reductions, exp/rsq) and no spills. On the
+GPU: one timed row and the G32 results.csv schema, comparator rows, tune,
+and the reference's e2e flow (compile through the CLI, load the written
+.hsaco, launch with the reference geometry, compare with the fp64 oracle)."""
 import csv
 import os
 import subprocess
@@ -35,6 +39,32 @@ def test_compile_writes_artifacts(tmp_path, kernel, shape):
     assert "s_waitcnt" in isa and kernel in isa
     res = (tmp_path / "resources.json").read_text()
     assert '"wavefront_size": 64' in res and '"target": "amdgcn-gfx950"' in res
+
+
+# What each kernel's design depends on, probed in the compiled artifact the
+# way the reference's degraded-mode e2e tests probe theirs for ds_ / exp_f32
+# / rsq (e2e_gemm_test.cpp:211-231, e2e_layernorm_test.cpp:274-292).
+DESIGN_INSTRUCTIONS = {
+    "vecadd": ("n=16777216", ["global_load_dwordx4", "global_store_dwordx4"]),
+    "fused_gelu": ("n=67108864", ["v_exp_f32", "v_rcp_f32", "global_load_dwordx4"]),
+    "softmax": ("rows=4096,cols=1024", ["v_exp_f32", "row_ror:8", "global_load_dwordx4"]),
+    "layernorm": ("rows=4096,cols=1024", ["v_rsq_f32", "row_ror:8", "global_load_dwordx4"]),
+    "scan": ("n=67108864", ["row_shr:8", "row_bcast:31", "global_atomic_add", "buffer_load_dwordx4"]),
+    "gemm": ("m=8192,n=8192,k=8192", ["v_mfma_f32_32x32x2_f32", "offen lds", "ds_read_b128", "s_setprio"]),
+    "attention": ("batch=4,heads=16,seq=4096,head_dim=64", ["v_mfma_f32_32x32x2_f32", "v_exp_f32", "ds_read_b128"]),
+}
+
+
+@pytest.mark.parametrize("kernel", sorted(DESIGN_INSTRUCTIONS))
+def test_compiled_isa_carries_the_design_instructions(tmp_path, kernel):
+    shape, needles = DESIGN_INSTRUCTIONS[kernel]
+    r = run("compile", "--kernel", kernel, "--shape", shape, "--out", str(tmp_path), "--resources")
+    assert r.returncode == 0, r.stdout
+    isa = (tmp_path / f"{kernel}.isa").read_text()
+    missing = [n for n in needles if n not in isa]
+    assert not missing, f"{kernel}.isa lacks {missing}"
+    res = (tmp_path / "resources.json").read_text()
+    assert '"scratch_bytes": 0' in res  # no register spills
 
 
 def test_compile_bogus_target_exit_1(tmp_path):
@@ -140,3 +170,53 @@ def test_tune_evaluates_candidates_and_caches(dev, tmp_path):
     assert all(float(row["ms_median"]) > 0 for row in rows)
     r2 = run(*args)
     assert r2.returncode == 0 and "cache-hit" in r2.stdout and "served from cache" in r2.stdout
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kernel", ["vecadd", "softmax", "gemm", "scan"])
+def test_cli_compiled_code_object_runs_under_reference_geometry(dev, tmp_path, kernel):
+    """The reference's e2e flow (e2e_*_test.cpp): compile through the CLI,
+    load the written <kernel>.hsaco with hipModuleLoadData, launch it with
+    the reference's own geometry and check it against the fp64 reference."""
+    import numpy as np
+    import oracle as O
+    from khtest import down, empty, up
+    shapes = {"vecadd": "n=100000", "softmax": "rows=257,cols=1000", "gemm": "m=300,n=200,k=100", "scan": "n=100000"}
+    r = run("compile", "--kernel", kernel, "--shape", shapes[kernel], "--out", str(tmp_path))
+    assert r.returncode == 0, r.stdout
+    mod = kh.GpuModule((tmp_path / f"{kernel}.hsaco").read_bytes())
+    f = mod.get_function(kernel)
+    print(f"[gpu-case] {kernel} from kernelh compile, reference geometry", flush=True)
+    if kernel == "vecadd":
+        n = 100000
+        a, b = O.vecadd_inputs(n)
+        da, db, dc = up(a), up(b), empty(n)
+        args = kh.LaunchArgs().add_memref(da, [n]).add_memref(db, [n]).add_memref(dc, [n])
+        kh.kernel_launch(f, ((n + 255) // 256, 1, 1), (256, 1, 1), args)
+        assert np.array_equal(down(dc, n), O.ref_vecadd(a, b))
+    elif kernel == "softmax":
+        rows, cols = 257, 1000
+        x, _ = O.lcg_fill(rows * cols, 0x27AB13)
+        dx, dy = up(x), empty(rows * cols)
+        args = kh.LaunchArgs().add_memref(dx, [rows, cols]).add_memref(dy, [rows, cols])
+        kh.kernel_launch(f, (rows, 1, 1), (256, 1, 1), args)
+        assert np.max(np.abs(down(dy, rows * cols) - O.ref_softmax(x, rows, cols).ravel())) <= 1e-4
+    elif kernel == "gemm":
+        m, n, k = 300, 200, 100
+        A, B = O.gemm_int_inputs(m, n, k)
+        dA, dB, dC = up(A), up(B), empty(m * n)
+        args = kh.LaunchArgs().add_memref(dA, [m, k]).add_memref(dB, [k, n]).add_memref(dC, [m, n])
+        kh.kernel_launch(f, ((m + 31) // 32, 1, 1), (256, 1, 1), args)
+        ref = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)  # exact integers
+        assert np.array_equal(down(dC, m * n).reshape(m, n), ref)
+    else:
+        n = 100000
+        T = (n + 255) // 256
+        x = O.mt19937_fill(n, 0x29C0FFEE)
+        dx, dy, dyl = up(x), empty(n), empty(n)
+        dth, dtl = empty(T), empty(T)
+        args = kh.LaunchArgs()
+        for buf, c in ((dx, n), (dy, n), (dyl, n), (dth, T), (dtl, T)):
+            args.add_memref(buf, [c])
+        kh.kernel_launch(f, (T, 1, 1), (256, 1, 1), args)  # the template's pass-1 geometry
+        assert np.array_equal(down(dy, n), O.ref_scan(x).astype(np.float32))
