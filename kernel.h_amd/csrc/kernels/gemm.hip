@@ -20,9 +20,9 @@
 //                     unevenly (1024^3 to 3584^3).
 //     Registers are capped for two waves per SIMD (two workgroups per CU, as
 //     LDS allows), so one workgroup's barrier and slab hand-over overlap the
-//     other's MFMAs. `gemm` raises its waves' priority (s_setprio) while they
-//     issue MFMAs, so a wave that is feeding the matrix core wins issue over
-//     one that is between slabs (+2% at 8192^3).
+//     other's MFMAs. `gemm` and `gemm_mid` raise their waves' priority
+//     (s_setprio) while they issue MFMAs, so a wave that is feeding the
+//     matrix core wins issue over one that is between slabs (+2% each).
 //   * K advances in slabs staged through LDS. `gemm` loads its slabs straight
 //     into LDS (buffer_load_dwordx4 ... lds) through three stages: slab ks+2
 //     is in flight while slab ks is consumed, and the one barrier per slab sits
@@ -76,7 +76,7 @@ gemm(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C
 // Same arguments and results with 128x128 tiles.
 extern "C" __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_mid(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
-  gemm_entry<2, 2, 32, false, false>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
+  gemm_entry<2, 2, 32, true, false>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
 }
 
 // Same arguments and results with 64x64 tiles.

@@ -41,7 +41,7 @@
 #define KH_GEMM_ROUND_MID (2 * KH_GEMM_CUS)
 #define KH_GEMM_ROUND_SMALL KH_GEMM_CUS
 #define KH_GEMM_RATE_BIG 142
-#define KH_GEMM_RATE_MID 133
+#define KH_GEMM_RATE_MID 135
 #define KH_GEMM_RATE_SMALL 125
 
 // Attention: query rows per workgroup (4 wavefronts x 32 rows).
