@@ -17,7 +17,10 @@
 //       `gemm_mid`    128x128 tiles (64x64 per wave), 32-deep slabs (e.g.
 //                     8192x1024x8192);
 //       `gemm_small`  64x64 tiles, for grids the larger tiles would fill
-//                     unevenly (1024^3 to 3584^3).
+//                     unevenly (512^3, 1024^3);
+//       `gemm_small_pf2` the same tiles with two-ahead prefetch, when they
+//                     number at least KH_GEMM_SMALL_PF2_TILES (2048^3 to
+//                     3584^3, 6144x6144x1024).
 //     Registers are capped for two waves per SIMD (two workgroups per CU, as
 //     LDS allows), so one workgroup's barrier and slab hand-over overlap the
 //     other's MFMAs. `gemm` and `gemm_mid` raise their waves' priority
@@ -64,8 +67,9 @@ using khg::kThreads;
 static_assert(Tile<2, 4, 16, true>::BM == KH_GEMM_BM && Tile<2, 4, 16, true>::BN == KH_GEMM_BN, "launcher tile size");
 static_assert(Tile<2, 2, 32, false>::BM == KH_GEMM_MID_BM && Tile<2, 2, 32, false>::BN == KH_GEMM_MID_BN,
               "launcher tile size");
-static_assert(Tile<1, 1, 32, false>::BM == KH_GEMM_SMALL_BM && Tile<1, 1, 32, false>::BN == KH_GEMM_SMALL_BN,
-              "launcher tile size");
+static_assert(Tile<1, 1, 32, false>::BM == KH_GEMM_SMALL_BM && Tile<1, 1, 32, false>::BN == KH_GEMM_SMALL_BN &&
+                  Tile<1, 1, 16, false>::BM == KH_GEMM_SMALL_BM && Tile<1, 1, 16, false>::BN == KH_GEMM_SMALL_BN,
+              "launcher tile size (gemm_small and gemm_small_pf2)");
 
 // The reference symbol: 128x256 tiles.
 extern "C" __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
@@ -83,4 +87,16 @@ gemm_mid(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(floa
 extern "C" __global__ void __launch_bounds__(kThreads)
 gemm_small(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
   gemm_entry<1, 1, 32, false, false>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
+}
+
+// Same arguments and results with 64x64 tiles, 16-deep slabs prefetched two
+// ahead through registers: more loads in flight per CU, for grids of many
+// tiles (+5-7% over `gemm_small` from six tiles per CU, 2560^3 to
+// 6144x6144x1024). With one or two tiles per CU the fewer barriers of
+// `gemm_small`'s 32-deep slabs win (1024^3: 77 vs 71 TFLOP/s). A kernel of its
+// own: compiled into `gemm_small` behind a size test, both pipelines lost 4%.
+extern "C" __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+gemm_small_pf2(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
+  khg::gemm_entry_pipe<1, 1, 16, false, khg::kPipePrefetch2>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0,
+                                                             B_s0, C_s0);
 }

@@ -1,5 +1,5 @@
 // fp32 MFMA GEMM building blocks for gfx950, shared by the product kernels
-// (gemm.hip: `gemm`, `gemm_mid`, `gemm_small`) and the tune candidates
+// (gemm.hip: `gemm`, `gemm_mid`, `gemm_small`, `gemm_small_pf2`) and the tune candidates
 // (gemm_tune.hip, used by `kernelh tune`). The design is described at the
 // top of gemm.hip.
 #pragma once
@@ -354,6 +354,45 @@ __device__ __forceinline__ void k_loop_regs(v16f (&acc)[WTM][WTN], const float *
   }
 }
 
+// Register-staged with two staging sets: slab ks+2's global loads are in
+// flight while slab ks computes and slab ks+1 goes to LDS, so each load has
+// two slab-times to arrive. The barriers fence LDS only (a full
+// __syncthreads() would wait for those loads). The loop is unrolled by two
+// so the staging sets swap roles without copies.
+template <int WTM, int WTN, class T, bool PRIO>
+__device__ __forceinline__ void prefetch2_step(v16f (&acc)[WTM][WTN], Slab<T> &free_set, Slab<T> &next_set,
+                                               const float *__restrict__ Ap, const float *__restrict__ Bp,
+                                               int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                                               int64_t m0, int64_t n0, int64_t nslabs, int64_t ks, float *As,
+                                               float *Bs, int tid, int wm, int wn, int lane) {
+  const int cur = ks & 1;
+  if (ks + 2 < nslabs) load_slab_vec<T>(free_set, Ap, Bp, M, N, K, lda, ldb, m0, n0, (ks + 2) * T::BK, tid);
+  if (PRIO) __builtin_amdgcn_s_setprio(1);
+  compute_slab<WTM, WTN, T>(acc, As + cur * T::A_STAGE, Bs + cur * T::B_STAGE, wm, wn, lane);
+  if (PRIO) __builtin_amdgcn_s_setprio(0);
+  if (ks + 1 < nslabs) store_slab<T>(next_set, As + (cur ^ 1) * T::A_STAGE, Bs + (cur ^ 1) * T::B_STAGE, tid);
+  kh::lds_barrier();
+}
+
+template <int WTM, int WTN, class T, bool PRIO>
+__device__ __forceinline__ void k_loop_prefetch2(v16f (&acc)[WTM][WTN], const float *__restrict__ Ap,
+                                                 const float *__restrict__ Bp, int64_t M, int64_t N, int64_t K,
+                                                 int64_t lda, int64_t ldb, int64_t m0, int64_t n0, int64_t nslabs,
+                                                 float *As, float *Bs, int tid, int wm, int wn, int lane) {
+  Slab<T> s0, s1;
+  load_slab_vec<T>(s0, Ap, Bp, M, N, K, lda, ldb, m0, n0, 0, tid);
+  if (nslabs > 1) load_slab_vec<T>(s1, Ap, Bp, M, N, K, lda, ldb, m0, n0, T::BK, tid);
+  store_slab<T>(s0, As, Bs, tid);
+  kh::lds_barrier();
+  for (int64_t ks = 0; ks < nslabs; ks += 2) {
+    prefetch2_step<WTM, WTN, T, PRIO>(acc, s0, s1, Ap, Bp, M, N, K, lda, ldb, m0, n0, nslabs, ks, As, Bs, tid, wm,
+                                      wn, lane);
+    if (ks + 1 < nslabs)
+      prefetch2_step<WTM, WTN, T, PRIO>(acc, s1, s0, Ap, Bp, M, N, K, lda, ldb, m0, n0, nslabs, ks + 1, As, Bs,
+                                        tid, wm, wn, lane);
+  }
+}
+
 // Generic (any shape, stride, alignment): synchronous, one stage.
 template <int WTM, int WTN, class T>
 __device__ __forceinline__ void k_loop_generic(v16f (&acc)[WTM][WTN], const float *__restrict__ Ap,
@@ -371,8 +410,12 @@ __device__ __forceinline__ void k_loop_generic(v16f (&acc)[WTM][WTN], const floa
   }
 }
 
-// One workgroup's loop over its tiles. PATH: 0 generic, 1 register-staged,
-// 2 direct-to-LDS. As, Bs: the LDS stages, A_STAGE and B_STAGE floats apart.
+// Fast-path pipelines (gemm_body's PIPE).
+constexpr int kPipeRegs = 1;       // register-staged, one slab ahead
+constexpr int kPipeDma = 2;        // direct-to-LDS, three stages
+constexpr int kPipePrefetch2 = 3;  // register-staged, two slabs ahead
+
+// One workgroup's loop over its tiles. PATH: 0 generic, else a kPipe*. As, Bs: the LDS stages, A_STAGE and B_STAGE floats apart.
 // (Offsets from one base keep the pointers visibly in LDS for the compiler;
 // an array of stage pointers would turn every LDS access into a flat one.)
 template <int WTM, int WTN, int BKT, int PATH, bool PRIO>
@@ -380,7 +423,7 @@ __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const f
                                            float *__restrict__ Cp, int64_t M, int64_t N, int64_t K, int64_t lda,
                                            int64_t ldb, int64_t ldc, bool a_vec, bool b_vec, float *As,
                                            float *Bs) {
-  using T = Tile<WTM, WTN, BKT, PATH == 2>;
+  using T = Tile<WTM, WTN, BKT, PATH == kPipeDma>;
   const int tid = threadIdx.x;
   const int lane = kh::lane_id();
   const int wave = tid >> 6;
@@ -404,10 +447,13 @@ __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const f
 #pragma unroll
       for (int j = 0; j < WTN; ++j) acc[i][j] = v16f{};
 
-    if constexpr (PATH == 2)
+    if constexpr (PATH == kPipeDma)
       k_loop_dma<WTM, WTN, T, PRIO>(acc, Ap, Bp, M, N, K, lda, ldb, m0, n0, nslabs, As, Bs, wave, wm, wn, lane);
-    else if constexpr (PATH == 1)
+    else if constexpr (PATH == kPipeRegs)
       k_loop_regs<WTM, WTN, T, PRIO>(acc, Ap, Bp, M, N, K, lda, ldb, m0, n0, nslabs, As, Bs, tid, wm, wn, lane);
+    else if constexpr (PATH == kPipePrefetch2)
+      k_loop_prefetch2<WTM, WTN, T, PRIO>(acc, Ap, Bp, M, N, K, lda, ldb, m0, n0, nslabs, As, Bs, tid, wm, wn,
+                                          lane);
     else
       k_loop_generic<WTM, WTN, T>(acc, Ap, Bp, M, N, K, lda, ldb, m0, n0, nslabs, a_vec, b_vec, As, Bs, tid, wm,
                                   wn, lane);
@@ -430,31 +476,53 @@ __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const f
   }
 }
 
-// Stages of LDS the fast path of a tile uses (the generic path uses one).
-template <bool DMA>
-constexpr int kStages = DMA ? 3 : 2;
+// LDS floats a configuration needs for A and for B: the fast pipeline's
+// stages (three for direct-to-LDS, two otherwise) or the generic path's one.
+template <int WTM, int WTN, int BKT, int PIPE>
+struct LdsNeed {
+  using T = Tile<WTM, WTN, BKT, PIPE == kPipeDma>;
+  using G = Tile<WTM, WTN, BKT, false>;
+  static constexpr int kStages = PIPE == kPipeDma ? 3 : 2;
+  static constexpr int A = kStages * T::A_STAGE > G::A_STAGE ? kStages * T::A_STAGE : G::A_STAGE;
+  static constexpr int B = kStages * T::B_STAGE > G::B_STAGE ? kStages * T::B_STAGE : G::B_STAGE;
+};
 
-// Kernel body. DMA selects the direct-to-LDS pipeline for the fast path
-// (aligned operands, k and n multiples of 4, 32-bit tile offsets); otherwise
-// the register-staged one. Other operands take the generic path.
-template <int WTM, int WTN, int BKT, bool PRIO, bool DMA>
-__device__ __forceinline__ void gemm_entry(const float *__restrict__ Ap, const float *__restrict__ Bp,
-                                           float *__restrict__ Cp, int64_t M, int64_t N, int64_t K, int64_t lda,
-                                           int64_t ldb, int64_t ldc) {
-  using T = Tile<WTM, WTN, BKT, DMA>;
-  using G = Tile<WTM, WTN, BKT, false>;  // the generic path's layout
-  constexpr int kA = kStages<DMA> * T::A_STAGE > G::A_STAGE ? kStages<DMA> * T::A_STAGE : G::A_STAGE;
-  constexpr int kB = kStages<DMA> * T::B_STAGE > G::B_STAGE ? kStages<DMA> * T::B_STAGE : G::B_STAGE;
-  __shared__ __attribute__((aligned(16))) float As[kA];
-  __shared__ __attribute__((aligned(16))) float Bs[kB];
+// Kernel body over LDS the caller provides (LdsNeed floats each): the fast
+// pipeline PIPE for aligned operands with k and n multiples of 4 and 32-bit
+// tile offsets, the generic path otherwise.
+template <int WTM, int WTN, int BKT, bool PRIO, int PIPE>
+__device__ __forceinline__ void gemm_body(const float *__restrict__ Ap, const float *__restrict__ Bp,
+                                          float *__restrict__ Cp, int64_t M, int64_t N, int64_t K, int64_t lda,
+                                          int64_t ldb, int64_t ldc, float *As, float *Bs) {
+  using T = Tile<WTM, WTN, BKT, PIPE == kPipeDma>;
   const bool a_vec = ((K & 3) == 0) && ((lda & 3) == 0) && kh::aligned16(Ap);
   const bool b_vec = ((N & 3) == 0) && ((ldb & 3) == 0) && kh::aligned16(Bp);
   // The fast loads address a tile's rows with 32-bit byte offsets.
   const bool fits32 = (int64_t)T::BM * lda * 4 < (1ll << 31) && (int64_t)T::BK * ldb * 4 < (1ll << 31);
   if (a_vec && b_vec && fits32)
-    gemm_tiles<WTM, WTN, BKT, DMA ? 2 : 1, PRIO>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, As, Bs);
+    gemm_tiles<WTM, WTN, BKT, PIPE, PRIO>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, As, Bs);
   else
     gemm_tiles<WTM, WTN, BKT, 0, PRIO>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, As, Bs);
+}
+
+// Kernel body with its own LDS and fast pipeline PIPE.
+template <int WTM, int WTN, int BKT, bool PRIO, int PIPE>
+__device__ __forceinline__ void gemm_entry_pipe(const float *__restrict__ Ap, const float *__restrict__ Bp,
+                                                float *__restrict__ Cp, int64_t M, int64_t N, int64_t K, int64_t lda,
+                                                int64_t ldb, int64_t ldc) {
+  using L = LdsNeed<WTM, WTN, BKT, PIPE>;
+  __shared__ __attribute__((aligned(16))) float As[L::A];
+  __shared__ __attribute__((aligned(16))) float Bs[L::B];
+  gemm_body<WTM, WTN, BKT, PRIO, PIPE>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, As, Bs);
+}
+
+// The same with DMA selecting the direct-to-LDS pipeline, else the
+// register-staged one.
+template <int WTM, int WTN, int BKT, bool PRIO, bool DMA>
+__device__ __forceinline__ void gemm_entry(const float *__restrict__ Ap, const float *__restrict__ Bp,
+                                           float *__restrict__ Cp, int64_t M, int64_t N, int64_t K, int64_t lda,
+                                           int64_t ldb, int64_t ldc) {
+  gemm_entry_pipe<WTM, WTN, BKT, PRIO, DMA ? kPipeDma : kPipeRegs>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc);
 }
 
 }  // namespace khg

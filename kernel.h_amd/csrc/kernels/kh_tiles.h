@@ -43,6 +43,10 @@
 #define KH_GEMM_RATE_BIG 142
 #define KH_GEMM_RATE_MID 135
 #define KH_GEMM_RATE_SMALL 125
+// Where the 64x64 tiles are chosen and number at least this many (four per
+// CU), the launcher takes `gemm_small_pf2` (two-ahead prefetch) instead of
+// `gemm_small`.
+#define KH_GEMM_SMALL_PF2_TILES 1024
 
 // Attention: query rows per workgroup (4 wavefronts x 32 rows).
 #define KH_ATTN_BLOCK_Q 128

@@ -161,7 +161,9 @@ const char *gemm_symbol(int64_t m, int64_t n) {
   const double small = gemm_score(ceil_div(m, KH_GEMM_SMALL_BM) * ceil_div(n, KH_GEMM_SMALL_BN),
                                   KH_GEMM_ROUND_SMALL, KH_GEMM_RATE_SMALL);
   if (big >= mid && big >= small) return "gemm";
-  return mid > small ? "gemm_mid" : "gemm_small";
+  if (mid > small) return "gemm_mid";
+  const int64_t tiles64 = ceil_div(m, KH_GEMM_SMALL_BM) * ceil_div(n, KH_GEMM_SMALL_BN);
+  return tiles64 >= KH_GEMM_SMALL_PF2_TILES ? "gemm_small_pf2" : "gemm_small";
 }
 
 int64_t gemm_grid(int64_t m, int64_t n) {

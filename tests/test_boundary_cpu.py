@@ -267,7 +267,7 @@ def test_kernarg_segment_is_2n_plus_3_slots(name, nslots):
     ("gemm", "m=4096,n=4096,k=64", (512, 1, 1), (256, 1, 1)),         # 128x256: exactly one round
     ("gemm", "m=8192,n=1024,k=8192", (512, 1, 1), (256, 1, 1)),       # 128x128 (gemm_mid): 512 tiles
     ("gemm", "m=6144,n=6144,k=1024", (9216, 1, 1), (256, 1, 1)),      # 64x64: 128x256 would fill 2.25 rounds
-    ("gemm", "m=3072,n=3072,k=3072", (2304, 1, 1), (256, 1, 1)),      # 64x64 (gemm_small)
+    ("gemm", "m=3072,n=3072,k=3072", (2304, 1, 1), (256, 1, 1)),      # 64x64 (gemm_small_pf2)
     ("gemm", "m=2048,n=2048,k=2048", (1024, 1, 1), (256, 1, 1)),      # 64x64: 128x128 would half-fill
     ("gemm", "m=1024,n=1024,k=1024", (256, 1, 1), (256, 1, 1)),       # 64x64
     ("gemm", "m=512,n=512,k=512", (64, 1, 1), (256, 1, 1)),

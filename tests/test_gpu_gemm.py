@@ -8,8 +8,8 @@
   reference (e2e_gemm_test.cpp:281); 8192^3 is checked on a row sample.
 * Ragged shapes, the reference launch geometry, and the A*B^T negative
   control (e2e_gemm_test.cpp:289-375).
-* Every tile symbol (`gemm` 128x256, `gemm_mid` 128x128, `gemm_small`
-  64x64) gives the same results at every shape, whichever the launcher
+* Every tile symbol (`gemm` 128x256, `gemm_mid` 128x128, `gemm_small` and
+  `gemm_small_pf2` 64x64) gives the same results at every shape, whichever the launcher
   would pick; and the launcher's own full-grid launch (one workgroup per
   tile, XCD-remapped) is checked at a large shape it sends to each symbol.
 """
@@ -88,9 +88,13 @@ def test_gemm_reference_geometry_and_negative_control(dev):
     assert O.rel_frobenius(C, wrong) > 1e-5
 
 
-@pytest.mark.parametrize("symbol", ["gemm", "gemm_mid", "gemm_small"])
+@pytest.mark.parametrize("symbol", ["gemm", "gemm_mid", "gemm_small", "gemm_small_pf2"])
 @pytest.mark.parametrize("m,n,k", [(256, 256, 256), (1000, 1000, 1000), (64, 192, 4097), (129, 65, 33),
-                                   (3, 5, 7), (512, 2048, 96)])
+                                   (3, 5, 7), (512, 2048, 96),
+                                   # the sizes the launcher gives gemm_small_pf2 (>= 1024 tiles of 64x64),
+                                   # with an odd slab count and a partial last slab, a short K, and an
+                                   # unaligned K (generic path at 16-deep slabs).
+                                   (2048, 2048, 260), (2112, 2048, 36), (2049, 2048, 33)])
 def test_every_gemm_symbol_at_every_shape(dev, symbol, m, n, k):
     # Integer fill: exact in fp32, so both tilings must agree bit for bit.
     A, B = O.gemm_int_inputs(m, n, k) if k <= 4096 else (None, None)
@@ -111,8 +115,8 @@ def test_every_gemm_symbol_at_every_shape(dev, symbol, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k,grid", [
-    (6144, 6144, 1024, 9216),   # gemm_small: 128x256 tiles would fill 2.25 rounds
-    (3072, 3072, 3072, 2304),   # gemm_small
+    (6144, 6144, 1024, 9216),   # gemm_small_pf2: 128x256 tiles would fill 2.25 rounds
+    (3072, 3072, 3072, 2304),   # gemm_small_pf2 (2304 tiles of 64x64)
     (8192, 1024, 8192, 512),    # gemm_mid: 512 tiles of 128x128
     (4096, 4096, 4096, 512),    # gemm: one full round of 128x256
 ])
