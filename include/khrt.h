@@ -220,6 +220,14 @@ KHRT_API int khrt_template_resources(const char *name, khrt_kernel_resources *ou
  * "k=v,k=v" text (the CLI's --shape syntax, main.cpp:242-266). */
 KHRT_API int khrt_template_geometry(const char *name, const char *shape, khrt_dim3 *grid,
                                     khrt_dim3 *block);
+/* The kernel symbol the launcher runs for a template at a shape ("k=v,k=v"):
+ * the template name itself or a variant in the same code object with the
+ * same arguments and results (gemm_mid, gemm_small, gemm_small_pf2,
+ * softmax_wide, layernorm_wide). Writes a NUL-terminated name of at most cap
+ * bytes. No reference counterpart: the reference compiles one symbol per
+ * template and shape (emitter.cpp:733-736); callers that report resources
+ * for a launch (kernelh compile --resources) need the symbol it runs. */
+KHRT_API int khrt_template_launch_symbol(const char *name, const char *shape, char *out, size_t cap);
 /* Loaded function handle of a template on the current device (module loaded
  * once per process from the embedded image). */
 KHRT_API int khrt_template_function(const char *name, void **function);

@@ -141,8 +141,12 @@ const char *code_object_of(const std::string &kernel) { return kernel == "scan_t
 
 // Occupancy of a template at its launcher block size (256; scan 1024).
 std::string resources_json(const std::string &kernel, const std::string &shape) {
+  // Resources of the symbol the launcher runs at this shape (a template may
+  // carry variants, e.g. gemm_small_pf2 or softmax_wide).
+  char sym[64] = {0};
+  if (khrt_template_launch_symbol(kernel.c_str(), shape.c_str(), sym, sizeof(sym)) != 0) return "";
   khrt_kernel_resources r{};
-  if (khrt_template_resources(kernel.c_str(), &r) != 0) return "";
+  if (khrt_template_resources(sym, &r) != 0) return "";
   khrt_dim3 grid{}, block{};
   khrt_template_geometry(kernel.c_str(), shape.c_str(), &grid, &block);
   khrt_device_limits lim{};
@@ -152,7 +156,8 @@ std::string resources_json(const std::string &kernel, const std::string &shape) 
   khrt_occupancy_report rep{};
   khrt_compute_occupancy(&in, &lim, nullptr, &rep);
   std::ostringstream os;
-  os << "{\n  \"kernel\": \"" << json_escape(kernel) << "\",\n  \"target\": \"amdgcn-gfx950\",\n"
+  os << "{\n  \"kernel\": \"" << json_escape(kernel) << "\",\n  \"symbol\": \"" << json_escape(sym)
+     << "\",\n  \"target\": \"amdgcn-gfx950\",\n"
      << "  \"shape\": \"" << json_escape(shape) << "\",\n"
      << "  \"vgpr_count\": " << r.vgpr_count << ",\n  \"agpr_count\": " << r.agpr_count << ",\n"
      << "  \"sgpr_count\": " << r.sgpr_count << ",\n  \"lds_bytes\": " << r.lds_bytes << ",\n"

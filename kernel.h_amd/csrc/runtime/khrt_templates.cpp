@@ -322,6 +322,20 @@ int khrt_template_geometry(const char *name, const char *shape, khrt_dim3 *grid,
   return geometry(name, s, *grid, *block);
 }
 
+int khrt_template_launch_symbol(const char *name, const char *shape, char *out, size_t cap) {
+  if (shape == nullptr || out == nullptr || cap == 0) return bad("khrt_template_launch_symbol: null argument");
+  const Template *t = find_template(name);
+  if (t == nullptr) return unknown_template(name);
+  Shape s;
+  if (!khrt::parse_shape(shape, s)) return khrt::fail(KHRT_E_INVALID, std::string("malformed shape '") + shape + "'");
+  khrt_dim3 grid, block;
+  if (int rc = geometry(name, s, grid, block)) return rc;  // the same shape checks as a launch
+  const std::string sym = launch_symbol(t, s);
+  if (sym.size() + 1 > cap) return bad("khrt_template_launch_symbol: output buffer too small");
+  std::memcpy(out, sym.c_str(), sym.size() + 1);
+  return 0;
+}
+
 int khrt_template_function(const char *name, void **function) {
   if (function == nullptr) return bad("khrt_template_function: null output");
   const Template *t = find_template(name);

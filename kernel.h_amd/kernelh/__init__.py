@@ -140,6 +140,7 @@ SIGNATURES = {
     "khrt_template_code_object": (_i, [ctypes.c_char_p, ctypes.POINTER(_vp), ctypes.POINTER(_sz)]),
     "khrt_template_resources": (_i, [ctypes.c_char_p, ctypes.POINTER(KernelResources)]),
     "khrt_template_geometry": (_i, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(Dim3), ctypes.POINTER(Dim3)]),
+    "khrt_template_launch_symbol": (_i, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
     "khrt_template_function": (_i, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "kh_vecadd": (_i, [_vp, _vp, _vp, _i64, _vp]),
     "kh_fused_gelu": (_i, [_vp, _vp, _vp, _i64, _vp]),
@@ -430,6 +431,13 @@ def geometry(name: str, shape: str):
     g, b = Dim3(), Dim3()
     check(lib.khrt_template_geometry(name.encode(), shape.encode(), ctypes.byref(g), ctypes.byref(b)))
     return g.tuple(), b.tuple()
+
+
+def launch_symbol(name: str, shape: str) -> str:
+    """Kernel symbol the launcher runs for template `name` at `shape`."""
+    buf = ctypes.create_string_buffer(64)
+    check(lib.khrt_template_launch_symbol(name.encode(), shape.encode(), buf, 64))
+    return buf.value.decode()
 
 
 def template_function(name: str) -> int:

@@ -277,6 +277,33 @@ def test_launcher_geometry(name, shape, grid, block):
     assert kh.geometry(name, shape) == (grid, block)
 
 
+@pytest.mark.parametrize("name,shape,symbol", [
+    ("gemm", "m=8192,n=8192,k=8192", "gemm"),
+    ("gemm", "m=8192,n=1024,k=8192", "gemm_mid"),
+    ("gemm", "m=1024,n=1024,k=1024", "gemm_small"),
+    ("gemm", "m=3072,n=3072,k=3072", "gemm_small_pf2"),   # >= 1024 tiles of 64x64
+    ("gemm", "m=2048,n=2048,k=2048", "gemm_small_pf2"),
+    ("softmax", "rows=4096,cols=1024", "softmax"),
+    ("softmax", "rows=16384,cols=4096", "softmax_wide"),
+    ("layernorm", "rows=16,cols=2048", "layernorm_wide"),
+    ("layernorm", "rows=16,cols=4100", "layernorm"),         # beyond the register paths: streaming
+    ("scan_totals", "n=1000000", "scan_totals"),
+])
+def test_launch_symbol(name, shape, symbol):
+    assert kh.launch_symbol(name, shape) == symbol
+    # Every launch symbol has resource notes (from the code object).
+    assert kh.resources(symbol)["wavefront_size"] == 64
+
+
+def test_launch_symbol_errors():
+    with pytest.raises(kh.KhrtError):
+        kh.launch_symbol("gemm", "m=1,n=1")          # k missing
+    with pytest.raises(kh.KhrtError):
+        kh.launch_symbol("matmul", "n=4")
+    buf = __import__("ctypes").create_string_buffer(4)
+    assert kh.lib.khrt_template_launch_symbol(b"gemm", b"m=3072,n=3072,k=3072", buf, 4) != 0  # too small
+
+
 @pytest.mark.parametrize("name,shape,msg", [
     ("softmax", "rows=4096", "'rows' and 'cols' are required"),
     ("attention", "batch=1,heads=1,seq=64,head_dim=32", "pinned to head_dim = 64"),
