@@ -166,9 +166,10 @@ const char *gemm_symbol(int64_t m, int64_t n) {
   return tiles64 >= KH_GEMM_SMALL_PF2_TILES ? "gemm_small_pf2" : "gemm_small";
 }
 
+// `gemm` is persistent: at most one workgroup per tile slot (two per CU).
 int64_t gemm_grid(int64_t m, int64_t n) {
   const std::string sym = gemm_symbol(m, n);
-  if (sym == "gemm") return ceil_div(m, KH_GEMM_BM) * ceil_div(n, KH_GEMM_BN);
+  if (sym == "gemm") return std::min<int64_t>(ceil_div(m, KH_GEMM_BM) * ceil_div(n, KH_GEMM_BN), KH_GEMM_ROUND_BIG);
   if (sym == "gemm_mid") return ceil_div(m, KH_GEMM_MID_BM) * ceil_div(n, KH_GEMM_MID_BN);
   return ceil_div(m, KH_GEMM_SMALL_BM) * ceil_div(n, KH_GEMM_SMALL_BN);
 }

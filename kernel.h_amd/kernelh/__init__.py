@@ -259,6 +259,18 @@ class Buffer:
             pass
 
 
+class Function(int):
+    """A kernel handle from GpuModule.get_function: the integer handle the C
+    ABI takes, holding a reference to its module so the module (and with it
+    the handle) cannot be unloaded while the handle is still reachable, e.g.
+    `GpuModule(image).get_function(name)` on a temporary module."""
+
+    def __new__(cls, handle: int, module: "GpuModule"):
+        obj = super().__new__(cls, handle)
+        obj.module = module
+        return obj
+
+
 class GpuModule:
     """Loaded code object (gpu_module.hpp): hipModuleLoadData / GetFunction.
     The runtime keeps its own copy of the image; the module is unloaded when
@@ -278,10 +290,10 @@ class GpuModule:
         except Exception:
             pass
 
-    def get_function(self, name: str) -> int:
+    def get_function(self, name: str) -> Function:
         f = ctypes.c_void_p()
         check(lib.khrt_module_get_function(ctypes.byref(f), self.handle, name.encode()))
-        return f.value
+        return Function(f.value, self)
 
     def unload(self) -> None:
         if self.handle:

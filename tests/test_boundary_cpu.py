@@ -262,9 +262,11 @@ def test_kernarg_segment_is_2n_plus_3_slots(name, nslots):
     ("scan", "n=1000000", (66, 1, 1), (1024, 1, 1)),
     ("scan", "n=67108864", (4370, 1, 1), (1024, 1, 1)),
     # gemm: the grid is the chosen symbol's tile count (rate x last-round fill).
-    ("gemm", "m=8192,n=8192,k=8192", (2048, 1, 1), (256, 1, 1)),     # 128x256 (gemm): 4 full rounds
-    ("gemm", "m=8192,n=8192,k=256", (2048, 1, 1), (256, 1, 1)),      # 128x256, skinny K
-    ("gemm", "m=4096,n=4096,k=64", (512, 1, 1), (256, 1, 1)),         # 128x256: exactly one round
+    # gemm (128x256) is persistent: two workgroups per CU loop over its tiles.
+    ("gemm", "m=8192,n=8192,k=8192", (512, 1, 1), (256, 1, 1)),      # 2048 tiles: 4 per workgroup
+    ("gemm", "m=8192,n=8192,k=256", (512, 1, 1), (256, 1, 1)),       # skinny K
+    ("gemm", "m=4096,n=4096,k=64", (512, 1, 1), (256, 1, 1)),         # exactly one round
+    ("gemm", "m=12288,n=12288,k=1024", (512, 1, 1), (256, 1, 1)),    # 4608 tiles: 9 per workgroup
     ("gemm", "m=8192,n=1024,k=8192", (512, 1, 1), (256, 1, 1)),       # 128x128 (gemm_mid): 512 tiles
     ("gemm", "m=6144,n=6144,k=1024", (9216, 1, 1), (256, 1, 1)),      # 64x64: 128x256 would fill 2.25 rounds
     ("gemm", "m=3072,n=3072,k=3072", (2304, 1, 1), (256, 1, 1)),      # 64x64 (gemm_small_pf2)
@@ -279,6 +281,7 @@ def test_launcher_geometry(name, shape, grid, block):
 
 @pytest.mark.parametrize("name,shape,symbol", [
     ("gemm", "m=8192,n=8192,k=8192", "gemm"),
+    ("gemm", "m=8192,n=8192,k=256", "gemm"),
     ("gemm", "m=8192,n=1024,k=8192", "gemm_mid"),
     ("gemm", "m=1024,n=1024,k=1024", "gemm_small"),
     ("gemm", "m=3072,n=3072,k=3072", "gemm_small_pf2"),   # >= 1024 tiles of 64x64

@@ -8,10 +8,11 @@
   reference (e2e_gemm_test.cpp:281); 8192^3 is checked on a row sample.
 * Ragged shapes, the reference launch geometry, and the A*B^T negative
   control (e2e_gemm_test.cpp:289-375).
-* Every tile symbol (`gemm` 128x256, `gemm_mid` 128x128, `gemm_small` and
-  `gemm_small_pf2` 64x64) gives the same results at every shape, whichever the launcher
-  would pick; and the launcher's own full-grid launch (one workgroup per
-  tile, XCD-remapped) is checked at a large shape it sends to each symbol.
+* Every tile symbol (`gemm` 128x256 persistent, `gemm_mid` 128x128,
+  `gemm_small` and `gemm_small_pf2` 64x64) gives the same results at every
+  shape and grid, whichever the launcher would pick; and the launcher's own
+  grid (one workgroup per tile, or at most two per CU for `gemm`;
+  XCD-remapped) is checked at a large shape it sends to each symbol.
 """
 import numpy as np
 import pytest
@@ -94,7 +95,10 @@ def test_gemm_reference_geometry_and_negative_control(dev):
                                    # the sizes the launcher gives gemm_small_pf2 (>= 1024 tiles of 64x64),
                                    # with an odd slab count and a partial last slab, a short K, and an
                                    # unaligned K (generic path at 16-deep slabs).
-                                   (2048, 2048, 260), (2112, 2048, 36), (2049, 2048, 33)])
+                                   (2048, 2048, 260), (2112, 2048, 36), (2049, 2048, 33),
+                                   # gemm's persistent cases: two slabs per tile (k = 20), one
+                                   # slab (k = 16, its per-tile fallback), edge tiles in m and n.
+                                   (300, 520, 20), (256, 512, 16), (1000, 1028, 100)])
 def test_every_gemm_symbol_at_every_shape(dev, symbol, m, n, k):
     # Integer fill: exact in fp32, so both tilings must agree bit for bit.
     A, B = O.gemm_int_inputs(m, n, k) if k <= 4096 else (None, None)
@@ -114,7 +118,31 @@ def test_every_gemm_symbol_at_every_shape(dev, symbol, m, n, k):
         assert O.rel_frobenius(C, O.ref_gemm(A, B, m, n, k)) <= 1e-5
 
 
+@pytest.mark.parametrize("extra", [4, 1])
+def test_gemm_padded_c_rows(dev, extra):
+    """C rows `n + extra` floats apart (slot 19 of the 21: C's row stride).
+    extra = 4 keeps C's rows 16-byte aligned (gemm's persistent path,
+    with its float4 stores); extra = 1 does not (its per-tile fallback). The
+    padding holds NaN and must stay NaN: no store lands past column n. m and
+    n leave edge tiles in both dimensions; 5 workgroups loop over 6 tiles."""
+    m, n, k = 300, 520, 200
+    pitch = n + extra
+    A, B = O.gemm_int_inputs(m, n, k)
+    dA, dB = up(A), up(B)
+    dC = up(np.full(m * pitch, np.nan, np.float32))
+    args = kh.LaunchArgs().add_memref(dA, [m, k]).add_memref(dB, [k, n]).add_memref(dC, [m, n])
+    args.slots[14 + 5] = pitch
+    mod = kh.GpuModule(kh.code_object("gemm"))
+    f = mod.get_function("gemm")
+    say(f"gemm m={m} n={n} k={k} C pitch={pitch}")
+    kh.kernel_launch(f, (5, 1, 1), (256, 1, 1), args)
+    C = down(dC, m * pitch).reshape(m, pitch)
+    assert np.array_equal(C[:, :n], (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
+    assert np.isnan(C[:, n:]).all()
+
+
 @pytest.mark.parametrize("m,n,k,grid", [
+    (8192, 8192, 256, 512),     # gemm: 2048 tiles of 128x256 over 512 persistent workgroups
     (6144, 6144, 1024, 9216),   # gemm_small_pf2: 128x256 tiles would fill 2.25 rounds
     (3072, 3072, 3072, 2304),   # gemm_small_pf2 (2304 tiles of 64x64)
     (8192, 1024, 8192, 512),    # gemm_mid: 512 tiles of 128x128
