@@ -75,13 +75,14 @@ static_assert(Tile<1, 1, 32, false>::BM == KH_GEMM_SMALL_BM && Tile<1, 1, 32, fa
 // The reference symbol: 128x256 tiles, persistent. Each workgroup loops
 // over tiles bid, bid + grid, ... (the launcher gives it min(tiles, two per
 // CU) workgroups; any grid is correct) and the three-stage slab ring runs on
-// across them. The MFMA operands are swapped so each lane holds four
-// consecutive columns of C: a tile goes out as 32 dwordx4 stores per wave,
-// issued after the next tile's first two slab fetches, and the next tile's
-// first barrier lets them stay in flight. Against one tile per workgroup
-// (same kernel, the previous form of this symbol): 8192^3 143.7 vs 142.3,
-// 4096^3 141.1 vs 140.5, 8192x8192x256 126.8 vs 122 TFLOP/s. K <= 16 and
-// unaligned operands take the per-tile pipeline (or the generic path).
+// across them, so a tile starts with its first two slabs already fetched.
+// Against one tile per workgroup (the previous form of this symbol, same
+// box): 8192^3 143.4 vs 142.0, 8192x8192x256 125.4 vs 123.0 TFLOP/s. Writing C
+// as float4s (MFMA operands swapped so a lane holds four consecutive
+// columns) let the stores overlap the next tile, but its 32-byte row pieces
+// doubled the kernel's L2 misses and measured 0.7% slower at 8192^3; C goes
+// out as whole 128-byte lines. K <= 16 and unaligned operands take the
+// per-tile pipeline (or the generic path).
 extern "C" __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 gemm(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
   khg::gemm_entry_flat<2, 4, 16, true>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);

@@ -410,6 +410,28 @@ __device__ __forceinline__ void k_loop_generic(v16f (&acc)[WTM][WTN], const floa
   }
 }
 
+// Writes a tile's accumulators to C. Accumulator layout: lane l, register
+// r -> row 8(r/4) + 4(l/32) + r%4, column l%32 of the 32x32 block, so each
+// store instruction writes two 128-byte row pieces (whole cache lines).
+template <int WTM, int WTN, class T>
+__device__ __forceinline__ void store_tile(const v16f (&acc)[WTM][WTN], float *__restrict__ Cp, int64_t M,
+                                           int64_t N, int64_t ldc, int64_t m0, int64_t n0, int wm, int wn,
+                                           int lane) {
+  const int col = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < WTM; ++i) {
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) {
+      const int64_t gc = n0 + wn * 32 * WTN + j * 32 + col;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t gr = m0 + wm * 32 * WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (gr < M && gc < N) Cp[gr * ldc + gc] = acc[i][j][r];
+      }
+    }
+  }
+}
+
 // Fast-path pipelines (gemm_body's PIPE).
 constexpr int kPipeRegs = 1;       // register-staged, one slab ahead
 constexpr int kPipeDma = 2;        // direct-to-LDS, three stages
@@ -458,108 +480,21 @@ __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const f
       k_loop_generic<WTM, WTN, T>(acc, Ap, Bp, M, N, K, lda, ldb, m0, n0, nslabs, a_vec, b_vec, As, Bs, tid, wm,
                                   wn, lane);
 
-    // Accumulator layout: lane l, register r -> row 8(r/4) + 4(l/32) + r%4,
-    // column l%32 of the 32x32 block.
-    const int col = lane & 31, h = lane >> 5;
-#pragma unroll
-    for (int i = 0; i < WTM; ++i) {
-#pragma unroll
-      for (int j = 0; j < WTN; ++j) {
-        const int64_t gc = n0 + wn * 32 * WTN + j * 32 + col;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t gr = m0 + wm * 32 * WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (gr < M && gc < N) Cp[gr * ldc + gc] = acc[i][j][r];
-        }
-      }
-    }
+    store_tile<WTM, WTN, T>(acc, Cp, M, N, ldc, m0, n0, wm, wn, lane);
   }
 }
 
 // ---------------------------------------------------------------------------
 // Persistent pipeline (the `gemm` symbol): the workgroup loops over its
 // tiles and the three-stage direct-to-LDS ring runs on across them, so the
-// next tile's first two slabs are fetched during this tile's last two and
-// its C stores overlap the next tile's MFMAs: no per-tile pipeline fill or
-// drain, which matters most for K of a few slabs per tile.
-
-// MFMA with the operands swapped, so each lane ends up holding four
-// consecutive columns of C: register r of lane l holds row l%32, column
-// 8(r/4) + 4(l/32) + r%4 of the 32x32 block. Same products in the same
-// order as mfma_frag, so the same bits.
-template <int WTM, int WTN>
-__device__ __forceinline__ void mfma_frag_t(v16f (&acc)[WTM][WTN], const Frag<WTM> &f) {
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-#pragma unroll
-    for (int i = 0; i < WTM; ++i) {
-      const float av = s == 0 ? f.a[i].x : s == 1 ? f.a[i].y : s == 2 ? f.a[i].z : f.a[i].w;
-#pragma unroll
-      for (int j = 0; j < WTN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.b[j][s], av, acc[i][j], 0, 0, 0);
-    }
-}
-
-// Writes a tile accumulated by mfma_frag_t: WTM x WTN x 4 dwordx4 buffer
-// stores per wave, always that many (the per-wave count the pipeline's
-// waits assume). Rows past M fall outside the buffer resource and columns
-// past N get an offset outside it, so the range check drops them. Needs C
-// 16-byte aligned with ldc and N multiples of 4 and BM ldc 4 < 2^31.
-template <int WTM, int WTN, class T>
-__device__ __forceinline__ void store_tile_t(const v16f (&acc)[WTM][WTN], float *__restrict__ Cp, int64_t M,
-                                             int64_t N, int64_t ldc, int64_t m0, int64_t n0, int wm, int wn,
-                                             int lane) {
-  const int64_t rows = (M - m0) < T::BM ? (M - m0) : T::BM;
-  const int r = lane & 31, h = lane >> 5;
-  auto pack = [&](int i, int j, int g) {
-    u32x4 v;
-    v.x = __float_as_uint(acc[i][j][4 * g + 0]);
-    v.y = __float_as_uint(acc[i][j][4 * g + 1]);
-    v.z = __float_as_uint(acc[i][j][4 * g + 2]);
-    v.w = __float_as_uint(acc[i][j][4 * g + 3]);
-    return v;
-  };
-  if (n0 + T::BN <= N) {
-    // Whole tile inside N: the resource starts at column n0 of row m0 and
-    // ends after row m0 + rows - 1; one offset register per row block, the
-    // column steps are immediate offsets.
-    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
-        Cp + m0 * ldc + n0, (short)0, (int)((rows * ldc - n0) * 4), kRsrcWord3);
-#pragma unroll
-    for (int i = 0; i < WTM; ++i) {
-      const int lr = wm * 32 * WTM + i * 32 + r;
-      const int base = (lr * (int)ldc + wn * 32 * WTN + 4 * h) * 4;
-#pragma unroll
-      for (int j = 0; j < WTN; ++j)
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-          __builtin_amdgcn_raw_buffer_store_b128(pack(i, j, g), rc, base + (j * 32 + 8 * g) * 4, 0, 0);
-    }
-    return;
-  }
-  const __amdgpu_buffer_rsrc_t rc =
-      __builtin_amdgcn_make_buffer_rsrc(Cp + m0 * ldc, (short)0, (int)(rows * ldc * 4), kRsrcWord3);
-#pragma unroll
-  for (int i = 0; i < WTM; ++i) {
-    const int lr = wm * 32 * WTM + i * 32 + r;
-#pragma unroll
-    for (int j = 0; j < WTN; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int64_t gc = n0 + wn * 32 * WTN + j * 32 + 8 * g + 4 * h;
-        const uint32_t off = (gc < N) ? (uint32_t)((lr * ldc + gc) * 4) : kOutside;
-        __builtin_amdgcn_raw_buffer_store_b128(pack(i, j, g), rc, (int)off, 0, 0);
-      }
-  }
-}
+// next tile's first two slabs are fetched during this tile's last two: no
+// per-tile pipeline fill (the fill and drain are a large share of the time
+// for K of a few slabs per tile).
 
 // One slab of the persistent ring: chunk 0's MFMAs, the barrier (slab q+1
 // has landed and stage fut is free), the fetch of a later slab into stage
 // fut, slab q+1's first fragments, then this slab's remaining chunks.
-// WAITN: vector-memory operations that may stay in flight at the barrier,
-// i.e. those issued after slab q+1's loads (the previous tile's C stores
-// when q starts a tile).
-template <int WTM, int WTN, class T, bool PRIO, int WAITN>
+template <int WTM, int WTN, class T, bool PRIO>
 __device__ __forceinline__ void flat_step(v16f (&acc)[WTM][WTN], Frag<WTM> &f0, Frag<WTM> &f1, int &cur,
                                           const float *__restrict__ Ap, const float *__restrict__ Bp, int64_t M,
                                           int64_t N, int64_t K, int64_t lda, int64_t ldb, bool dma, int64_t dm0,
@@ -571,18 +506,18 @@ __device__ __forceinline__ void flat_step(v16f (&acc)[WTM][WTN], Frag<WTM> &f0, 
   const float *sA = As + cur * T::A_STAGE, *sB = Bs + cur * T::B_STAGE;
   if constexpr (C > 1) read_frag<WTM, WTN, T>(f1, sA, sB, 1, wm, wn, lane);
   if (PRIO) __builtin_amdgcn_s_setprio(1);
-  mfma_frag_t<WTM, WTN>(acc, f0);
+  mfma_frag<WTM, WTN>(acc, f0);
   if (PRIO) __builtin_amdgcn_s_setprio(0);
-  vm_barrier<WAITN>();
+  vm_barrier<0>();
   if (dma)
     dma_slab<T>(Ap, Bp, M, N, K, lda, ldb, dm0, dn0, dk0, As + fut * T::A_STAGE, Bs + fut * T::B_STAGE, wv, lane);
   if (read_next) read_frag<WTM, WTN, T>(f0, As + nxt * T::A_STAGE, Bs + nxt * T::B_STAGE, 0, wm, wn, lane);
   if (PRIO) __builtin_amdgcn_s_setprio(1);
-  if constexpr (C > 1) mfma_frag_t<WTM, WTN>(acc, f1);
+  if constexpr (C > 1) mfma_frag<WTM, WTN>(acc, f1);
 #pragma unroll
   for (int c = 2; c < C; ++c) {
     read_frag<WTM, WTN, T>(f1, sA, sB, c, wm, wn, lane);
-    mfma_frag_t<WTM, WTN>(acc, f1);
+    mfma_frag<WTM, WTN>(acc, f1);
   }
   if (PRIO) __builtin_amdgcn_s_setprio(0);
   cur = nxt;
@@ -591,17 +526,14 @@ __device__ __forceinline__ void flat_step(v16f (&acc)[WTM][WTN], Frag<WTM> &f0, 
 // The persistent tile loop. Slab j of the workgroup's stream sits in stage
 // j % 3; slab ks of a tile fetches slab ks+2 of the same tile or, in the
 // tile's last two slabs, slab 0 or 1 of the next. The tile's C stores go
-// out after those fetches, so the next tile's first barrier lets them stay
-// in flight (vector-memory operations complete in issue order). Needs at
-// least two slabs per tile (K > BK) and fewer than 2^31 tiles.
+// out after those fetches. Needs at least two slabs per tile (K > BK) and
+// fewer than 2^31 tiles.
 template <int WTM, int WTN, int BKT, bool PRIO>
 __device__ __forceinline__ void gemm_tiles_flat(const float *__restrict__ Ap, const float *__restrict__ Bp,
                                                 float *__restrict__ Cp, int64_t M, int64_t N, int64_t K,
                                                 int64_t lda, int64_t ldb, int64_t ldc, float *As, float *Bs) {
   using T = Tile<WTM, WTN, BKT, true>;
   constexpr int BK = T::BK;
-  constexpr int S = WTM * WTN * 4;  // C stores per wave per tile
-  static_assert(T::NA + T::NB + S < 64, "in-flight operations must fit the vmcnt field");
   const int tid = threadIdx.x;
   const int lane = kh::lane_id();
   const int wave = tid >> 6;
@@ -653,22 +585,18 @@ __device__ __forceinline__ void gemm_tiles_flat(const float *__restrict__ Ap, co
       const bool same = ns > 2;
       const bool dma = same || has_next;
       const int64_t dm0 = same ? cm0 : nm0, dn0 = same ? cn0 : nn0, dk0 = same ? 2 * BK : 0;
-      if (t > 0)
-        flat_step<WTM, WTN, T, PRIO, S>(acc, f0, f1, cur, Ap, Bp, M, N, K, lda, ldb, dma, dm0, dn0, dk0, true, As,
-                                        Bs, wv, wm, wn, lane);
-      else
-        flat_step<WTM, WTN, T, PRIO, 0>(acc, f0, f1, cur, Ap, Bp, M, N, K, lda, ldb, dma, dm0, dn0, dk0, true, As,
-                                        Bs, wv, wm, wn, lane);
+      flat_step<WTM, WTN, T, PRIO>(acc, f0, f1, cur, Ap, Bp, M, N, K, lda, ldb, dma, dm0, dn0, dk0, true, As, Bs,
+                                   wv, wm, wn, lane);
     }
     for (int64_t ks = 1; ks < ns - 2; ++ks)
-      flat_step<WTM, WTN, T, PRIO, 0>(acc, f0, f1, cur, Ap, Bp, M, N, K, lda, ldb, true, cm0, cn0, (ks + 2) * BK,
+      flat_step<WTM, WTN, T, PRIO>(acc, f0, f1, cur, Ap, Bp, M, N, K, lda, ldb, true, cm0, cn0, (ks + 2) * BK,
                                       true, As, Bs, wv, wm, wn, lane);
     // The last two slabs (the last one only, when ns = 2) fetch the next
     // tile's slabs 0 and 1.
     for (int64_t ks = ns > 2 ? ns - 2 : 1; ks < ns; ++ks)
-      flat_step<WTM, WTN, T, PRIO, 0>(acc, f0, f1, cur, Ap, Bp, M, N, K, lda, ldb, has_next, nm0, nn0,
+      flat_step<WTM, WTN, T, PRIO>(acc, f0, f1, cur, Ap, Bp, M, N, K, lda, ldb, has_next, nm0, nn0,
                                       (ks + 2 - ns) * BK, ks + 1 < ns || has_next, As, Bs, wv, wm, wn, lane);
-    store_tile_t<WTM, WTN, T>(acc, Cp, M, N, ldc, cm0, cn0, wm, wn, lane);
+    store_tile<WTM, WTN, T>(acc, Cp, M, N, ldc, cm0, cn0, wm, wn, lane);
     cm0 = nm0;
     cn0 = nn0;
   }
@@ -714,10 +642,10 @@ __device__ __forceinline__ void gemm_entry_pipe(const float *__restrict__ Ap, co
   gemm_body<WTM, WTN, BKT, PRIO, PIPE>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, As, Bs);
 }
 
-// Kernel body of the persistent variant: gemm_tiles_flat when A, B and C
-// are 16-byte aligned with k, n and ldc multiples of 4, K > BK and the tile
-// offsets fit 32 bits; the direct-to-LDS per-tile pipeline (or the generic
-// path) otherwise. Same LDS as gemm_entry_pipe's direct-to-LDS form.
+// Kernel body of the persistent variant: gemm_tiles_flat when A and B are
+// 16-byte aligned with k and n multiples of 4, K > BK and the tile offsets
+// fit 32 bits; the direct-to-LDS per-tile pipeline (or the generic path)
+// otherwise. Same LDS as gemm_entry_pipe's direct-to-LDS form.
 template <int WTM, int WTN, int BKT, bool PRIO>
 __device__ __forceinline__ void gemm_entry_flat(const float *__restrict__ Ap, const float *__restrict__ Bp,
                                                 float *__restrict__ Cp, int64_t M, int64_t N, int64_t K, int64_t lda,
@@ -727,9 +655,8 @@ __device__ __forceinline__ void gemm_entry_flat(const float *__restrict__ Ap, co
   __shared__ __attribute__((aligned(16))) float As[L::A];
   __shared__ __attribute__((aligned(16))) float Bs[L::B];
   const bool vec = ((K & 3) == 0) && ((lda & 3) == 0) && kh::aligned16(Ap) && ((N & 3) == 0) &&
-                   ((ldb & 3) == 0) && kh::aligned16(Bp) && ((ldc & 3) == 0) && kh::aligned16(Cp);
-  const bool fits32 = (int64_t)T::BM * lda * 4 < (1ll << 31) && (int64_t)T::BK * ldb * 4 < (1ll << 31) &&
-                      (int64_t)T::BM * ldc * 4 < (1ll << 31);
+                   ((ldb & 3) == 0) && kh::aligned16(Bp);
+  const bool fits32 = (int64_t)T::BM * lda * 4 < (1ll << 31) && (int64_t)T::BK * ldb * 4 < (1ll << 31);
   const int64_t tiles = ((M + T::BM - 1) / T::BM) * ((N + T::BN - 1) / T::BN);
   if (vec && fits32 && K > T::BK && tiles < (1ll << 31))
     gemm_tiles_flat<WTM, WTN, BKT, PRIO>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, As, Bs);

@@ -120,11 +120,11 @@ def test_every_gemm_symbol_at_every_shape(dev, symbol, m, n, k):
 
 @pytest.mark.parametrize("extra", [4, 1])
 def test_gemm_padded_c_rows(dev, extra):
-    """C rows `n + extra` floats apart (slot 19 of the 21: C's row stride).
-    extra = 4 keeps C's rows 16-byte aligned (gemm's persistent path,
-    with its float4 stores); extra = 1 does not (its per-tile fallback). The
-    padding holds NaN and must stay NaN: no store lands past column n. m and
-    n leave edge tiles in both dimensions; 5 workgroups loop over 6 tiles."""
+    """C rows `n + extra` floats apart (slot 19 of the 21: C's row stride;
+    16-byte aligned rows for extra = 4, not for extra = 1), through gemm's
+    persistent path. The padding holds NaN and must stay NaN: no store
+    lands past column n. m and n leave edge tiles in both dimensions; 5
+    workgroups loop over 6 tiles."""
     m, n, k = 300, 520, 200
     pitch = n + extra
     A, B = O.gemm_int_inputs(m, n, k)
