@@ -235,9 +235,10 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
       load_k(kr, rk, ks, TK, tid);
       store_k(kr, Ks + TK * LDK, tid);
       __syncthreads();
-      v16f sc[2], sn[2];
-      qk_tile(sc, q, Ks, lane);
-      for (int64_t t = 0; t + 1 < ntiles; ++t) {
+      // One pipeline step: S^T of tile t+1 into sn while tile t's softmax
+      // and PV consume sc. The loop is unrolled by two so sc and sn swap
+      // roles instead of being copied.
+      auto step = [&](int64_t t, v16f (&sc)[2], v16f (&sn)[2]) __attribute__((always_inline)) {
         const int cur = t & 1;
         load_k(kr, rk, ks, (t + 2) * TK, tid);
         load_v(vr, rv, ks, (t + 1) * TK, tid);
@@ -246,10 +247,21 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
         store_k(kr, Ks + cur * TK * LDK, tid);
         store_v(vr, Vt + (cur ^ 1) * D * LDV, tid);
         __syncthreads();
-        sc[0] = sn[0];
-        sc[1] = sn[1];
+      };
+      v16f sa[2], sb[2];
+      qk_tile(sa, q, Ks, lane);
+      int64_t t = 0;
+      for (; t + 2 < ntiles; t += 2) {
+        step(t, sa, sb);
+        step(t + 1, sb, sa);
       }
-      softmax_pv<true>(o, m, l, sc, Vt + ((ntiles - 1) & 1) * D * LDV, (ntiles - 1) * TK, seq, lane);
+      if (t + 1 < ntiles) {
+        step(t, sa, sb);
+        ++t;
+        sa[0] = sb[0];
+        sa[1] = sb[1];
+      }
+      softmax_pv<true>(o, m, l, sa, Vt + (t & 1) * D * LDV, t * TK, seq, lane);
     } else {
       for (int64_t t = 0; t < ntiles; ++t) {
         stage_kv_generic(Ks, Vt, Kg, Vg, ks, t * TK, seq);
