@@ -100,6 +100,23 @@ def test_module_outlives_caller_image_buffer(dev):
     kh.check(kh.lib.khrt_module_unload(h))
 
 
+def test_function_handle_keeps_its_module_loaded(dev):
+    # A handle taken from a temporary GpuModule holds the module: the module
+    # is unloaded only once no handle of it is reachable (regression test
+    # for a launch through the handle of a module already unloaded).
+    import gc
+    f = kh.GpuModule(kh.code_object("vecadd")).get_function("vecadd")
+    gc.collect()
+    n = 4096
+    a, b = O.vecadd_inputs(n)
+    da, db, dc = up(a), up(b), empty(n)
+    args = kh.LaunchArgs().add_memref(da, [n]).add_memref(db, [n]).add_memref(dc, [n])
+    say("vecadd through the handle of a temporary module")
+    kh.kernel_launch(f, (16, 1, 1), (256, 1, 1), args)
+    assert np.array_equal(down(dc, n), O.ref_vecadd(a, b))
+    assert int(f) == f and f.module.handle
+
+
 def test_events_time_a_launch(dev):
     n = 1 << 20
     a = up(np.ones(n, np.float32))
