@@ -118,6 +118,31 @@ def test_every_gemm_symbol_at_every_shape(dev, symbol, m, n, k):
         assert O.rel_frobenius(C, O.ref_gemm(A, B, m, n, k)) <= 1e-5
 
 
+def test_gemm_symbols_random_shapes_exact(dev):
+    """Seeded random shapes (ragged m, n, k; 60% with n, k multiples of 4 so
+    the fast paths run) through every tile symbol at a random grid, with
+    small-integer inputs: every sum is exact in fp32, so each result must
+    equal the fp64 product bit for bit whatever the tiling and grid."""
+    rng = np.random.default_rng(20261201)
+    mod = kh.GpuModule(kh.code_object("gemm"))
+    fns = {sym: mod.get_function(sym) for sym in ("gemm", "gemm_mid", "gemm_small", "gemm_small_pf2")}
+    for _ in range(30):
+        m, n = int(rng.integers(1, 700)), int(rng.integers(1, 700))
+        k = int(rng.choice([int(rng.integers(1, 60)), int(rng.integers(1, 500))]))
+        if rng.random() < 0.6:
+            n, k = max(4, n // 4 * 4), max(4, k // 4 * 4)
+        A = rng.integers(-3, 4, (m, k)).astype(np.float32)
+        B = rng.integers(-3, 4, (k, n)).astype(np.float32)
+        want = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+        dA, dB, dC = up(A), up(B), empty(m * n)
+        args = kh.LaunchArgs().add_memref(dA, [m, k]).add_memref(dB, [k, n]).add_memref(dC, [m, n])
+        for sym, f in fns.items():
+            grid = int(rng.choice([1, 3, 8, 37, 512]))
+            say(f"{sym} m={m} n={n} k={k} grid={grid}")
+            kh.kernel_launch(f, (grid, 1, 1), (256, 1, 1), args)
+            assert np.array_equal(down(dC, m * n).reshape(m, n), want), (sym, m, n, k, grid)
+
+
 @pytest.mark.parametrize("extra", [4, 1])
 def test_gemm_padded_c_rows(dev, extra):
     """C rows `n + extra` floats apart (slot 19 of the 21: C's row stride;
