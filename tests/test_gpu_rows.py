@@ -73,7 +73,7 @@ def test_softmax_reference_geometry(dev):
 
 
 @pytest.mark.parametrize("symbol", ["softmax", "softmax_wide", "layernorm", "layernorm_wide"])
-@pytest.mark.parametrize("cols", [256, 1000, 1024, 2048, 4096, 5000])
+@pytest.mark.parametrize("cols", [64, 256, 512, 1000, 1024, 2048, 4096, 5000])
 def test_every_row_symbol_at_every_width(dev, symbol, cols):
     # Each symbol of a template computes the same result at every width (the
     # launcher picks one by width; raw callers may launch either).
@@ -97,6 +97,26 @@ def test_every_row_symbol_at_every_width(dev, symbol, cols):
     got = down(dy, rows * cols).reshape(rows, cols)
     assert np.max(np.abs(got - ref)) <= 1e-4
 
+
+
+@pytest.mark.parametrize("block", [64, 128, 192])
+@pytest.mark.parametrize("cols", [128, 1024])
+def test_layernorm_narrow_block_sizes(dev, block, cols):
+    # The narrow symbol copies gamma and beta into LDS with the block's
+    # threads before its rows: any multiple of 64 threads per block, with
+    # grid-strided rows, gives the same result.
+    rows = 45
+    x, seed = O.lcg_fill(rows * cols, 0x51ED27)
+    g, seed = O.lcg_fill(cols, seed)
+    b, seed = O.lcg_fill(cols, seed)
+    f = kh.GpuModule(kh.code_object("layernorm")).get_function("layernorm")
+    dx, dg, db, dy = up(x), up(g), up(b), empty(rows * cols)
+    args = kh.LaunchArgs().add_memref(dx, [rows, cols]).add_memref(dg, [cols]).add_memref(db, [cols])
+    args.add_memref(dy, [rows, cols])
+    say(f"layernorm block={block} rows={rows} cols={cols}")
+    kh.kernel_launch(f, (4, 1, 1), (block, 1, 1), args)
+    got = down(dy, rows * cols).reshape(rows, cols)
+    assert np.max(np.abs(got - O.ref_layernorm(x, g, b, rows, cols))) <= 1e-4
 
 def _layernorm(x, g, b, rows, cols):
     dx, dg, db, dy = up(x), up(g), up(b), empty(rows * cols)
