@@ -112,3 +112,143 @@ gemm_small_pf2(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF
                                                              B_s0, C_s0);
 }
 
+
+// 32x32 tiles with K split over the workgroup's waves (8 at the launcher's
+// 512 threads; any 64..512 threads, a multiple of 64, are correct), for
+// launches whose larger tiles leave most CUs idle: 512^3 has 64 tiles of
+// 64x64 for 256 CUs, and 256 tiles of 32x32. Wave w of nw accumulates the
+// products of its K range (contiguous chunks of kc = 8 * ceil(K / (8 nw)))
+// straight from global memory into one v_mfma_f32_32x32x2f32 accumulator,
+// without LDS: lane l (r = l % 32, h = l / 32) loads the float4
+// A[m0 + r][k + 4h .. k + 4h + 3] and the four B[k + 4h + i][n0 + r], so MFMA
+// i of a group of 8 k sums k + i (lanes 0-31) and k + 4 + i (lanes 32-63):
+// every k of the group exactly once. Rows, columns and k past the matrix or
+// chunk edge load a clamped in-range address and are replaced by 0, so the
+// loads carry no branch. The partial tiles meet in LDS, and output register
+// i is summed by wave i % nw in the fixed order w0 + w1 + ... : the result
+// does not depend on timing. Measured against `gemm_small` (64x64 tiles):
+// 512^3 28-30 vs 18.0 TFLOP/s, 512x512x2048 37-41 vs 22, 256^3 6.3-6.5 vs
+// 3.8. Four waves per workgroup reached 22 at 512^3; sixteen spilled, and
+// so did loading 8 groups per batch (6 groups: slower at every shape).
+namespace {
+
+using khg::v16f;
+constexpr int kKsTile = KH_GEMM_KSPLIT_BM;
+constexpr int kKsMaxWaves = KH_GEMM_KSPLIT_THREADS / 64;
+constexpr int kKsBatch = 4;  // groups of 8 k loaded ahead per batch
+static_assert(KH_GEMM_KSPLIT_BM == 32 && KH_GEMM_KSPLIT_BN == 32, "one 32x32 MFMA accumulator per wave");
+
+// Loads one group of 8 k for this lane: k is the lane's first k of the
+// group (a multiple of 4 when VEC), K the end of the wave's chunk.
+template <bool VEC>
+__device__ __forceinline__ void ks_load(const float *__restrict__ A, const float *__restrict__ B, int64_t K,
+                                        int64_t lda, int64_t ldb, int64_t arow, int64_t bcol, bool arow_ok,
+                                        bool bcol_ok, int64_t k, float4 &a, float (&b)[4]) {
+  if constexpr (VEC) {
+    const bool ok = arow_ok && k < K;
+    const float4 t = *reinterpret_cast<const float4 *>(A + arow * lda + (k < K ? k : K - 4));
+    a = ok ? t : make_float4(0.f, 0.f, 0.f, 0.f);
+  } else {
+    float t[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t kk = k + i;
+      const float v = A[arow * lda + (kk < K ? kk : K - 1)];
+      t[i] = (arow_ok && kk < K) ? v : 0.0f;
+    }
+    a = make_float4(t[0], t[1], t[2], t[3]);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t kk = k + i;
+    const float v = B[(kk < K ? kk : K - 1) * ldb + bcol];
+    b[i] = (bcol_ok && kk < K) ? v : 0.0f;
+  }
+}
+
+__device__ __forceinline__ void ks_mfma(v16f &acc, const float4 &a, const float (&b)[4]) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b[3], acc, 0, 0, 0);
+}
+
+// NWC: the wave count when known at compile time (the launcher's 512
+// threads), else 0 and the count comes from blockDim.
+template <bool VEC, int NWC>
+__device__ __forceinline__ void gemm_ksplit_body(const float *__restrict__ A, const float *__restrict__ B,
+                                                 float *__restrict__ C, int64_t M, int64_t N, int64_t K,
+                                                 int64_t lda, int64_t ldb, int64_t ldc, float *red) {
+  const int lane = kh::lane_id(), wave = threadIdx.x / kh::kWave;
+  const int nw = NWC > 0 ? NWC : blockDim.x / kh::kWave;  // whole waves; a partial last wave takes no k, no output
+  const int r = lane & 31, h = lane >> 5;
+  const int64_t tiles_m = (M + kKsTile - 1) / kKsTile, tiles_n = (N + kKsTile - 1) / kKsTile;
+  const int64_t total = tiles_m * tiles_n;
+  const int64_t kc = 8 * ((K + 8 * nw - 1) / (8 * nw));
+  const int64_t kb = wave * kc, ke = kb + kc < K ? kb + kc : K;
+  const int64_t groups = ke > kb ? (ke - kb + 7) / 8 : 0;
+  for (int64_t t = blockIdx.x; t < total; t += gridDim.x) {
+    const int64_t m0 = (t / tiles_n) * kKsTile, n0 = (t % tiles_n) * kKsTile;
+    const bool arow_ok = m0 + r < M, bcol_ok = n0 + r < N;
+    const int64_t arow = arow_ok ? m0 + r : M - 1, bcol = bcol_ok ? n0 + r : N - 1;
+    v16f acc = {};
+    float4 a0[kKsBatch], a1[kKsBatch];
+    float b0[kKsBatch][4], b1[kKsBatch][4];
+    auto load = [&](float4 (&a)[kKsBatch], float (&b)[kKsBatch][4], int64_t g) {
+#pragma unroll
+      for (int i = 0; i < kKsBatch; ++i) {
+        ks_load<VEC>(A, B, ke, lda, ldb, arow, bcol, arow_ok, bcol_ok, kb + 8 * (g + i) + 4 * h, a[i], b[i]);
+      }
+    };
+    auto math = [&](const float4 (&a)[kKsBatch], const float (&b)[kKsBatch][4]) {
+#pragma unroll
+      for (int i = 0; i < kKsBatch; ++i) ks_mfma(acc, a[i], b[i]);
+    };
+    // Batches of kKsBatch groups, double-buffered: the next batch's loads
+    // are issued before this batch's MFMAs. Groups past `groups` load
+    // clamped addresses and contribute 0.
+    if (groups > 0) load(a0, b0, 0);
+    int64_t g = 0;
+    for (; g + kKsBatch < groups; g += 2 * kKsBatch) {
+      load(a1, b1, g + kKsBatch);
+      math(a0, b0);
+      if (g + 2 * kKsBatch < groups) load(a0, b0, g + 2 * kKsBatch);
+      math(a1, b1);
+    }
+    if (g < groups) math(a0, b0);
+    // Partial tiles into LDS: red[wave][register][lane].
+#pragma unroll
+    for (int i = 0; i < 16; ++i) red[(wave * 16 + i) * kh::kWave + lane] = acc[i];
+    kh::lds_barrier();
+    if (wave < nw) {
+      for (int i = wave; i < 16; i += nw) {
+        float s = red[i * kh::kWave + lane];
+        for (int w = 1; w < nw; ++w) s += red[(16 * w + i) * kh::kWave + lane];
+        const int64_t gr = m0 + 8 * (i >> 2) + 4 * h + (i & 3), gc = n0 + r;
+        if (gr < M && gc < N) C[gr * ldc + gc] = s;
+      }
+    }
+    kh::lds_barrier();
+  }
+}
+
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(KH_GEMM_KSPLIT_THREADS)
+gemm_ksplit(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
+  __shared__ float red[kKsMaxWaves * 16 * 64];
+  const float *Ap = KH_PTR(A);
+  const int64_t K = A_n1, lda = A_s0;
+  const bool vec = ((K & 3) == 0) && ((lda & 3) == 0) && kh::aligned16(Ap);
+  if (blockDim.x == KH_GEMM_KSPLIT_THREADS) {
+    if (vec) {
+      gemm_ksplit_body<true, kKsMaxWaves>(Ap, KH_PTR(B), KH_PTR(C), A_n0, B_n1, K, lda, B_s0, C_s0, red);
+    } else {
+      gemm_ksplit_body<false, kKsMaxWaves>(Ap, KH_PTR(B), KH_PTR(C), A_n0, B_n1, K, lda, B_s0, C_s0, red);
+    }
+  } else if (vec) {
+    gemm_ksplit_body<true, 0>(Ap, KH_PTR(B), KH_PTR(C), A_n0, B_n1, K, lda, B_s0, C_s0, red);
+  } else {
+    gemm_ksplit_body<false, 0>(Ap, KH_PTR(B), KH_PTR(C), A_n0, B_n1, K, lda, B_s0, C_s0, red);
+  }
+}

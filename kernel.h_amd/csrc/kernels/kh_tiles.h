@@ -47,6 +47,12 @@
 // CU), the launcher takes `gemm_small_pf2` (two-ahead prefetch) instead of
 // `gemm_small`.
 #define KH_GEMM_SMALL_PF2_TILES 1024
+// `gemm_ksplit`: 32x32 tiles, K split over the 8 waves of a 512-thread
+// workgroup. The launcher takes it when its tiles fit one round (at most
+// one workgroup per CU): there the larger tiles leave three CUs in four idle.
+#define KH_GEMM_KSPLIT_BM 32
+#define KH_GEMM_KSPLIT_BN 32
+#define KH_GEMM_KSPLIT_THREADS 512
 
 // Attention: query rows per workgroup (4 wavefronts x 32 rows).
 #define KH_ATTN_BLOCK_Q 128

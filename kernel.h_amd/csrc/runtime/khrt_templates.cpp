@@ -154,6 +154,7 @@ double gemm_score(int64_t tiles, int64_t round, double rate) {
 }
 
 const char *gemm_symbol(int64_t m, int64_t n) {
+  if (ceil_div(m, KH_GEMM_KSPLIT_BM) * ceil_div(n, KH_GEMM_KSPLIT_BN) <= KH_GEMM_CUS) return "gemm_ksplit";
   const double big = gemm_score(ceil_div(m, KH_GEMM_BM) * ceil_div(n, KH_GEMM_BN), KH_GEMM_ROUND_BIG,
                                 KH_GEMM_RATE_BIG);
   const double mid = gemm_score(ceil_div(m, KH_GEMM_MID_BM) * ceil_div(n, KH_GEMM_MID_BN), KH_GEMM_ROUND_MID,
@@ -171,6 +172,7 @@ int64_t gemm_grid(int64_t m, int64_t n) {
   const std::string sym = gemm_symbol(m, n);
   if (sym == "gemm") return std::min<int64_t>(ceil_div(m, KH_GEMM_BM) * ceil_div(n, KH_GEMM_BN), KH_GEMM_ROUND_BIG);
   if (sym == "gemm_mid") return ceil_div(m, KH_GEMM_MID_BM) * ceil_div(n, KH_GEMM_MID_BN);
+  if (sym == "gemm_ksplit") return ceil_div(m, KH_GEMM_KSPLIT_BM) * ceil_div(n, KH_GEMM_KSPLIT_BN);
   return ceil_div(m, KH_GEMM_SMALL_BM) * ceil_div(n, KH_GEMM_SMALL_BN);
 }
 
@@ -218,6 +220,7 @@ int geometry(const char *name, const Shape &s, khrt_dim3 &grid, khrt_dim3 &block
       return khrt::fail(KHRT_E_INVALID, "gemm: shape attributes 'm', 'n' and 'k' are required and must be positive");
     }
     grid.x = clamp_grid(gemm_grid(m, n));
+    if (std::string(gemm_symbol(m, n)) == "gemm_ksplit") block.x = KH_GEMM_KSPLIT_THREADS;
   } else if (t == "attention") {
     if (!need(s, "batch", b) || !need(s, "heads", h) || !need(s, "seq", seq) || !need(s, "head_dim", d)) {
       return khrt::fail(KHRT_E_INVALID,

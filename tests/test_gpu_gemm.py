@@ -9,10 +9,11 @@
 * Ragged shapes, the reference launch geometry, and the A*B^T negative
   control (e2e_gemm_test.cpp:289-375).
 * Every tile symbol (`gemm` 128x256 persistent, `gemm_mid` 128x128,
-  `gemm_small` and `gemm_small_pf2` 64x64) gives the same results at every
-  shape and grid, whichever the launcher would pick; and the launcher's own
-  grid (one workgroup per tile, or at most two per CU for `gemm`;
-  XCD-remapped) is checked at a large shape it sends to each symbol.
+  `gemm_small` and `gemm_small_pf2` 64x64, `gemm_ksplit` 32x32 with K split
+  over the workgroup's waves, at any 64..512 threads) gives the same results
+  at every shape and grid, whichever the launcher would pick; and the
+  launcher's own grid (one workgroup per tile, or at most two per CU for
+  `gemm`; XCD-remapped) is checked at a shape it sends to each symbol.
 """
 import numpy as np
 import pytest
@@ -89,7 +90,7 @@ def test_gemm_reference_geometry_and_negative_control(dev):
     assert O.rel_frobenius(C, wrong) > 1e-5
 
 
-@pytest.mark.parametrize("symbol", ["gemm", "gemm_mid", "gemm_small", "gemm_small_pf2"])
+@pytest.mark.parametrize("symbol", ["gemm", "gemm_mid", "gemm_small", "gemm_small_pf2", "gemm_ksplit"])
 @pytest.mark.parametrize("m,n,k", [(256, 256, 256), (1000, 1000, 1000), (64, 192, 4097), (129, 65, 33),
                                    (3, 5, 7), (512, 2048, 96),
                                    # the sizes the launcher gives gemm_small_pf2 (>= 1024 tiles of 64x64),
@@ -125,7 +126,7 @@ def test_gemm_symbols_random_shapes_exact(dev):
     equal the fp64 product bit for bit whatever the tiling and grid."""
     rng = np.random.default_rng(20261201)
     mod = kh.GpuModule(kh.code_object("gemm"))
-    fns = {sym: mod.get_function(sym) for sym in ("gemm", "gemm_mid", "gemm_small", "gemm_small_pf2")}
+    fns = {sym: mod.get_function(sym) for sym in ("gemm", "gemm_mid", "gemm_small", "gemm_small_pf2", "gemm_ksplit")}
     for _ in range(30):
         m, n = int(rng.integers(1, 700)), int(rng.integers(1, 700))
         k = int(rng.choice([int(rng.integers(1, 60)), int(rng.integers(1, 500))]))
@@ -138,8 +139,9 @@ def test_gemm_symbols_random_shapes_exact(dev):
         args = kh.LaunchArgs().add_memref(dA, [m, k]).add_memref(dB, [k, n]).add_memref(dC, [m, n])
         for sym, f in fns.items():
             grid = int(rng.choice([1, 3, 8, 37, 512]))
-            say(f"{sym} m={m} n={n} k={k} grid={grid}")
-            kh.kernel_launch(f, (grid, 1, 1), (256, 1, 1), args)
+            block = int(rng.choice([64, 192, 512])) if sym == "gemm_ksplit" else 256  # 1, 3 or 8 waves
+            say(f"{sym} m={m} n={n} k={k} grid={grid} block={block}")
+            kh.kernel_launch(f, (grid, 1, 1), (block, 1, 1), args)
             assert np.array_equal(down(dC, m * n).reshape(m, n), want), (sym, m, n, k, grid)
 
 
@@ -172,6 +174,7 @@ def test_gemm_padded_c_rows(dev, extra):
     (3072, 3072, 3072, 2304),   # gemm_small_pf2 (2304 tiles of 64x64)
     (8192, 1024, 8192, 512),    # gemm_mid: 512 tiles of 128x128
     (4096, 4096, 4096, 512),    # gemm: one full round of 128x256
+    (512, 512, 2048, 256),      # gemm_ksplit: 256 tiles of 32x32 at 512 threads
 ])
 def test_gemm_launcher_choice_at_scale(dev, m, n, k, grid):
     assert kh.geometry("gemm", f"m={m},n={n},k={k}")[0] == (grid, 1, 1)
