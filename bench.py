@@ -43,7 +43,7 @@ METRIC = "GEMM-8192 fp32 TFLOPS + softmax/scan HBM GB/s, % of MI355X roofline"
 # 2.000 and WRITE_SIZE by 1.000, the factors a copy kernel of known size
 # reads), recorded in profiles/templates_baseline_sizes_hbm_traffic.md.
 PMC_TRAFFIC_BYTES = {
-    "vecadd": 201374080, "softmax": 33634176, "layernorm": 33726694, "scan": 539377210,
+    "vecadd": 201374080, "softmax": 33634176, "layernorm": 33737882, "scan": 539377210,
     "fused_gelu": 537017626, "gemm": 4281652941, "attention": 1208230925,
 }
 
