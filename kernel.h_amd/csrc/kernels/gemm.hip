@@ -174,8 +174,10 @@ __device__ __forceinline__ void ks_mfma(v16f &acc, const float4 &a, const float 
 }
 
 // NWC: the wave count when known at compile time (the launcher's 512
-// threads), else 0 and the count comes from blockDim.
-template <bool VEC, int NWC>
+// threads), else 0 and the count comes from blockDim. DEEP compiles in the
+// interior-tile path with three batches of loads in flight, for K chunks of
+// at least three batches.
+template <bool VEC, int NWC, bool DEEP>
 __device__ __forceinline__ void gemm_ksplit_body(const float *__restrict__ A, const float *__restrict__ B,
                                                  float *__restrict__ C, int64_t M, int64_t N, int64_t K,
                                                  int64_t lda, int64_t ldb, int64_t ldc, float *red) {
@@ -184,7 +186,8 @@ __device__ __forceinline__ void gemm_ksplit_body(const float *__restrict__ A, co
   const int r = lane & 31, h = lane >> 5;
   const int64_t tiles_m = (M + kKsTile - 1) / kKsTile, tiles_n = (N + kKsTile - 1) / kKsTile;
   const int64_t total = tiles_m * tiles_n;
-  const int64_t kc = 8 * ((K + 8 * nw - 1) / (8 * nw));
+  // DEEP chunks are whole batches of 4 groups (32 k).
+  const int64_t kc = DEEP ? 32 * ((K + 32 * nw - 1) / (32 * nw)) : 8 * ((K + 8 * nw - 1) / (8 * nw));
   const int64_t kb = wave * kc, ke = kb + kc < K ? kb + kc : K;
   const int64_t groups = ke > kb ? (ke - kb + 7) / 8 : 0;
   for (int64_t t = blockIdx.x; t < total; t += gridDim.x) {
@@ -192,6 +195,42 @@ __device__ __forceinline__ void gemm_ksplit_body(const float *__restrict__ A, co
     const bool arow_ok = m0 + r < M, bcol_ok = n0 + r < N;
     const int64_t arow = arow_ok ? m0 + r : M - 1, bcol = bcol_ok ? n0 + r : N - 1;
     v16f acc = {};
+    if (DEEP && VEC && m0 + kKsTile <= M && n0 + kKsTile <= N && ke - kb == kc && kc >= 3 * 32 &&
+        31 * lda + 8 <= (1 << 30) && (kc + 8) * ldb + 32 <= (1 << 30)) {
+      // Interior tile, a whole chunk of at least three batches: no clamps,
+      // and three batches of loads in flight (a ring of three register
+      // sets; the tail reloads the last batch and skips its math).
+      const uint32_t aoff = (uint32_t)(r * lda + 4 * h), boff = (uint32_t)(4 * h * ldb + r);
+      const float *abase = A + m0 * lda + kb, *bbase = B + kb * ldb + n0;
+      const int64_t nb = kc / 32;
+      struct Set {
+        float4 a[kKsBatch];
+        float b[kKsBatch][4];
+      };
+      Set f0, f1, f2;
+      auto fload = [&](Set &f, int64_t j) {
+#pragma unroll
+        for (int i = 0; i < kKsBatch; ++i) {
+          f.a[i] = *reinterpret_cast<const float4 *>(abase + (32 * j + 8 * i) + aoff);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) f.b[i][q] = (bbase + (32 * j + 8 * i + q) * ldb)[boff];
+        }
+      };
+      auto fmath = [&](const Set &f) {
+#pragma unroll
+        for (int i = 0; i < kKsBatch; ++i) ks_mfma(acc, f.a[i], f.b[i]);
+      };
+      fload(f0, 0);
+      fload(f1, 1);
+      for (int64_t j = 0; j < nb; j += 3) {
+        fload(f2, j + 2 < nb ? j + 2 : nb - 1);
+        fmath(f0);
+        fload(f0, j + 3 < nb ? j + 3 : nb - 1);
+        if (j + 1 < nb) fmath(f1);
+        fload(f1, j + 4 < nb ? j + 4 : nb - 1);
+        if (j + 2 < nb) fmath(f2);
+      }
+    } else {
     float4 a0[kKsBatch], a1[kKsBatch];
     float b0[kKsBatch][4], b1[kKsBatch][4];
     auto load = [&](float4 (&a)[kKsBatch], float (&b)[kKsBatch][4], int64_t g) {
@@ -216,6 +255,7 @@ __device__ __forceinline__ void gemm_ksplit_body(const float *__restrict__ A, co
       math(a1, b1);
     }
     if (g < groups) math(a0, b0);
+    }
     // Partial tiles into LDS: red[wave][register][lane].
 #pragma unroll
     for (int i = 0; i < 16; ++i) red[(wave * 16 + i) * kh::kWave + lane] = acc[i];
@@ -234,21 +274,37 @@ __device__ __forceinline__ void gemm_ksplit_body(const float *__restrict__ A, co
 
 }  // namespace
 
-extern "C" __global__ void __launch_bounds__(KH_GEMM_KSPLIT_THREADS)
-gemm_ksplit(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
-  __shared__ float red[kKsMaxWaves * 16 * 64];
-  const float *Ap = KH_PTR(A);
-  const int64_t K = A_n1, lda = A_s0;
+template <bool DEEP>
+__device__ __forceinline__ void gemm_ksplit_entry(const float *Ap, const float *Bp, float *Cp, int64_t M, int64_t N,
+                                                  int64_t K, int64_t lda, int64_t ldb, int64_t ldc, float *red) {
   const bool vec = ((K & 3) == 0) && ((lda & 3) == 0) && kh::aligned16(Ap);
   if (blockDim.x == KH_GEMM_KSPLIT_THREADS) {
     if (vec) {
-      gemm_ksplit_body<true, kKsMaxWaves>(Ap, KH_PTR(B), KH_PTR(C), A_n0, B_n1, K, lda, B_s0, C_s0, red);
+      gemm_ksplit_body<true, kKsMaxWaves, DEEP>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, red);
     } else {
-      gemm_ksplit_body<false, kKsMaxWaves>(Ap, KH_PTR(B), KH_PTR(C), A_n0, B_n1, K, lda, B_s0, C_s0, red);
+      gemm_ksplit_body<false, kKsMaxWaves, DEEP>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, red);
     }
   } else if (vec) {
-    gemm_ksplit_body<true, 0>(Ap, KH_PTR(B), KH_PTR(C), A_n0, B_n1, K, lda, B_s0, C_s0, red);
+    gemm_ksplit_body<true, 0, DEEP>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, red);
   } else {
-    gemm_ksplit_body<false, 0>(Ap, KH_PTR(B), KH_PTR(C), A_n0, B_n1, K, lda, B_s0, C_s0, red);
+    gemm_ksplit_body<false, 0, DEEP>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, red);
   }
+}
+
+extern "C" __global__ void __launch_bounds__(KH_GEMM_KSPLIT_THREADS)
+gemm_ksplit(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
+  __shared__ float red[kKsMaxWaves * 16 * 64];
+  gemm_ksplit_entry<false>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0, red);
+}
+
+// Same tiles and split with the deep-chunk path compiled in: the launcher
+// takes it over `gemm_ksplit` for K >= KH_GEMM_KSPLIT_DEEP_K. A kernel of
+// its own: compiled into `gemm_ksplit`, the extra registers slowed the
+// short-chunk path (512^3: 28 -> 18 TFLOP/s). Measured against it:
+// 512x512x2048 42 vs 37 TFLOP/s, 512x512x8192 54 vs 40; at K = 1024 the two
+// were level.
+extern "C" __global__ void __launch_bounds__(KH_GEMM_KSPLIT_THREADS)
+gemm_ksplit_deep(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
+  __shared__ float red[kKsMaxWaves * 16 * 64];
+  gemm_ksplit_entry<true>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0, red);
 }

@@ -53,6 +53,9 @@
 #define KH_GEMM_KSPLIT_BM 32
 #define KH_GEMM_KSPLIT_BN 32
 #define KH_GEMM_KSPLIT_THREADS 512
+// From this K on, the launcher takes `gemm_ksplit_deep` (three batches of
+// loads in flight per wave) for the same launches.
+#define KH_GEMM_KSPLIT_DEEP_K 2048
 
 // Attention: query rows per workgroup (4 wavefronts x 32 rows).
 #define KH_ATTN_BLOCK_Q 128

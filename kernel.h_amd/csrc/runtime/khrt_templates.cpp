@@ -153,8 +153,10 @@ double gemm_score(int64_t tiles, int64_t round, double rate) {
   return rate * static_cast<double>(tiles) / static_cast<double>(ceil_div(tiles, round) * round);
 }
 
-const char *gemm_symbol(int64_t m, int64_t n) {
-  if (ceil_div(m, KH_GEMM_KSPLIT_BM) * ceil_div(n, KH_GEMM_KSPLIT_BN) <= KH_GEMM_CUS) return "gemm_ksplit";
+const char *gemm_symbol(int64_t m, int64_t n, int64_t k) {
+  if (ceil_div(m, KH_GEMM_KSPLIT_BM) * ceil_div(n, KH_GEMM_KSPLIT_BN) <= KH_GEMM_CUS) {
+    return k >= KH_GEMM_KSPLIT_DEEP_K ? "gemm_ksplit_deep" : "gemm_ksplit";
+  }
   const double big = gemm_score(ceil_div(m, KH_GEMM_BM) * ceil_div(n, KH_GEMM_BN), KH_GEMM_ROUND_BIG,
                                 KH_GEMM_RATE_BIG);
   const double mid = gemm_score(ceil_div(m, KH_GEMM_MID_BM) * ceil_div(n, KH_GEMM_MID_BN), KH_GEMM_ROUND_MID,
@@ -169,10 +171,10 @@ const char *gemm_symbol(int64_t m, int64_t n) {
 
 // `gemm` is persistent: at most one workgroup per tile slot (two per CU).
 int64_t gemm_grid(int64_t m, int64_t n) {
-  const std::string sym = gemm_symbol(m, n);
+  const std::string sym = gemm_symbol(m, n, 0);
   if (sym == "gemm") return std::min<int64_t>(ceil_div(m, KH_GEMM_BM) * ceil_div(n, KH_GEMM_BN), KH_GEMM_ROUND_BIG);
   if (sym == "gemm_mid") return ceil_div(m, KH_GEMM_MID_BM) * ceil_div(n, KH_GEMM_MID_BN);
-  if (sym == "gemm_ksplit") return ceil_div(m, KH_GEMM_KSPLIT_BM) * ceil_div(n, KH_GEMM_KSPLIT_BN);
+  if (sym == "gemm_ksplit") return ceil_div(m, KH_GEMM_KSPLIT_BM) * ceil_div(n, KH_GEMM_KSPLIT_BN);  // and _deep
   return ceil_div(m, KH_GEMM_SMALL_BM) * ceil_div(n, KH_GEMM_SMALL_BN);
 }
 
@@ -220,7 +222,7 @@ int geometry(const char *name, const Shape &s, khrt_dim3 &grid, khrt_dim3 &block
       return khrt::fail(KHRT_E_INVALID, "gemm: shape attributes 'm', 'n' and 'k' are required and must be positive");
     }
     grid.x = clamp_grid(gemm_grid(m, n));
-    if (std::string(gemm_symbol(m, n)) == "gemm_ksplit") block.x = KH_GEMM_KSPLIT_THREADS;
+    if (std::string(gemm_symbol(m, n, k)).rfind("gemm_ksplit", 0) == 0) block.x = KH_GEMM_KSPLIT_THREADS;
   } else if (t == "attention") {
     if (!need(s, "batch", b) || !need(s, "heads", h) || !need(s, "seq", seq) || !need(s, "head_dim", d)) {
       return khrt::fail(KHRT_E_INVALID,
@@ -252,8 +254,8 @@ const char *launch_symbol(const Template *t, const Shape &s) {
     }
   }
   if (n == "gemm") {
-    auto m = s.find("m"), nn = s.find("n");
-    if (m != s.end() && nn != s.end()) return gemm_symbol(m->second, nn->second);
+    auto m = s.find("m"), nn = s.find("n"), k = s.find("k");
+    if (m != s.end() && nn != s.end()) return gemm_symbol(m->second, nn->second, k != s.end() ? k->second : 0);
   }
   return t->name;
 }

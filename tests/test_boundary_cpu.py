@@ -274,6 +274,7 @@ def test_kernarg_segment_is_2n_plus_3_slots(name, nslots):
     ("gemm", "m=1024,n=1024,k=1024", (256, 1, 1), (256, 1, 1)),       # 64x64
     ("gemm", "m=512,n=512,k=512", (256, 1, 1), (512, 1, 1)),        # gemm_ksplit: 256 tiles of 32x32, 8 waves
     ("gemm", "m=768,n=768,k=768", (144, 1, 1), (256, 1, 1)),        # 576 tiles of 32x32: 64x64 instead
+    ("gemm", "m=512,n=512,k=8192", (256, 1, 1), (512, 1, 1)),       # gemm_ksplit_deep
     ("attention", "batch=4,heads=16,seq=4096,head_dim=64", (32, 16, 4), (256, 1, 1)),
 ])
 def test_launcher_geometry(name, shape, grid, block):
@@ -287,7 +288,8 @@ def test_launcher_geometry(name, shape, grid, block):
     ("gemm", "m=1024,n=1024,k=1024", "gemm_small"),
     ("gemm", "m=3072,n=3072,k=3072", "gemm_small_pf2"),   # >= 1024 tiles of 64x64
     ("gemm", "m=2048,n=2048,k=2048", "gemm_small_pf2"),
-    ("gemm", "m=512,n=512,k=2048", "gemm_ksplit"),        # 256 tiles of 32x32: one round
+    ("gemm", "m=512,n=512,k=2048", "gemm_ksplit_deep"),   # 256 tiles of 32x32, deep K
+    ("gemm", "m=512,n=512,k=1024", "gemm_ksplit"),
     ("gemm", "m=300,n=520,k=100", "gemm_ksplit"),
     ("gemm", "m=768,n=768,k=768", "gemm_small"),
     ("softmax", "rows=4096,cols=1024", "softmax"),

@@ -9,8 +9,9 @@
 * Ragged shapes, the reference launch geometry, and the A*B^T negative
   control (e2e_gemm_test.cpp:289-375).
 * Every tile symbol (`gemm` 128x256 persistent, `gemm_mid` 128x128,
-  `gemm_small` and `gemm_small_pf2` 64x64, `gemm_ksplit` 32x32 with K split
-  over the workgroup's waves, at any 64..512 threads) gives the same results
+  `gemm_small` and `gemm_small_pf2` 64x64, `gemm_ksplit` and
+  `gemm_ksplit_deep` 32x32 with K split over the workgroup's waves, at any
+  64..512 threads) gives the same results
   at every shape and grid, whichever the launcher would pick; and the
   launcher's own grid (one workgroup per tile, or at most two per CU for
   `gemm`; XCD-remapped) is checked at a shape it sends to each symbol.
@@ -90,7 +91,8 @@ def test_gemm_reference_geometry_and_negative_control(dev):
     assert O.rel_frobenius(C, wrong) > 1e-5
 
 
-@pytest.mark.parametrize("symbol", ["gemm", "gemm_mid", "gemm_small", "gemm_small_pf2", "gemm_ksplit"])
+@pytest.mark.parametrize("symbol", ["gemm", "gemm_mid", "gemm_small", "gemm_small_pf2", "gemm_ksplit",
+                                    "gemm_ksplit_deep"])
 @pytest.mark.parametrize("m,n,k", [(256, 256, 256), (1000, 1000, 1000), (64, 192, 4097), (129, 65, 33),
                                    (3, 5, 7), (512, 2048, 96),
                                    # the sizes the launcher gives gemm_small_pf2 (>= 1024 tiles of 64x64),
@@ -126,7 +128,8 @@ def test_gemm_symbols_random_shapes_exact(dev):
     equal the fp64 product bit for bit whatever the tiling and grid."""
     rng = np.random.default_rng(20261201)
     mod = kh.GpuModule(kh.code_object("gemm"))
-    fns = {sym: mod.get_function(sym) for sym in ("gemm", "gemm_mid", "gemm_small", "gemm_small_pf2", "gemm_ksplit")}
+    fns = {sym: mod.get_function(sym) for sym in ("gemm", "gemm_mid", "gemm_small", "gemm_small_pf2", "gemm_ksplit",
+                                                       "gemm_ksplit_deep")}
     for _ in range(30):
         m, n = int(rng.integers(1, 700)), int(rng.integers(1, 700))
         k = int(rng.choice([int(rng.integers(1, 60)), int(rng.integers(1, 500))]))
@@ -139,7 +142,7 @@ def test_gemm_symbols_random_shapes_exact(dev):
         args = kh.LaunchArgs().add_memref(dA, [m, k]).add_memref(dB, [k, n]).add_memref(dC, [m, n])
         for sym, f in fns.items():
             grid = int(rng.choice([1, 3, 8, 37, 512]))
-            block = int(rng.choice([64, 192, 512])) if sym == "gemm_ksplit" else 256  # 1, 3 or 8 waves
+            block = int(rng.choice([64, 192, 512])) if sym.startswith("gemm_ksplit") else 256  # 1, 3 or 8 waves
             say(f"{sym} m={m} n={n} k={k} grid={grid} block={block}")
             kh.kernel_launch(f, (grid, 1, 1), (block, 1, 1), args)
             assert np.array_equal(down(dC, m * n).reshape(m, n), want), (sym, m, n, k, grid)
@@ -174,7 +177,8 @@ def test_gemm_padded_c_rows(dev, extra):
     (3072, 3072, 3072, 2304),   # gemm_small_pf2 (2304 tiles of 64x64)
     (8192, 1024, 8192, 512),    # gemm_mid: 512 tiles of 128x128
     (4096, 4096, 4096, 512),    # gemm: one full round of 128x256
-    (512, 512, 2048, 256),      # gemm_ksplit: 256 tiles of 32x32 at 512 threads
+    (512, 512, 1024, 256),      # gemm_ksplit: 256 tiles of 32x32 at 512 threads
+    (512, 470, 4100, 240),      # gemm_ksplit_deep: edge tiles in n, a partial last K chunk
 ])
 def test_gemm_launcher_choice_at_scale(dev, m, n, k, grid):
     assert kh.geometry("gemm", f"m={m},n={n},k={k}")[0] == (grid, 1, 1)
