@@ -8,9 +8,11 @@
 //
 //   * Workgroup = 256 threads (4 wave64s, 2x2) computing a BM x BN tile of C;
 //     each wave owns a quarter as WTM x WTN MFMA 32x32 accumulators. Four
-//     symbols, all correct for every shape; the launcher scores each by its
-//     full-occupancy rate times how busy its last round of workgroups would
-//     be (kh_tiles.h) and takes the best:
+//     such symbols, all correct for every shape; the launcher scores each by
+//     its full-occupancy rate times how busy its last round of workgroups
+//     would be (kh_tiles.h) and takes the best, unless the launch has at most
+//     256 tiles of 32x32 (then `gemm_ksplit` / `gemm_ksplit_deep`, at the
+//     end of this file, split K over 8 waves instead):
 //       `gemm`        128x256 tiles (64x128 per wave, 128 accumulator registers
 //                     per lane), 16-deep K slabs: the least LDS and L2 traffic
 //                     per MFMA (8192^3, 4096^3, 8192x8192x256); persistent
@@ -18,7 +20,7 @@
 //       `gemm_mid`    128x128 tiles (64x64 per wave), 32-deep slabs (e.g.
 //                     8192x1024x8192);
 //       `gemm_small`  64x64 tiles, for grids the larger tiles would fill
-//                     unevenly (512^3, 1024^3);
+//                     unevenly (768^3, 1024^3);
 //       `gemm_small_pf2` the same tiles with two-ahead prefetch, when they
 //                     number at least KH_GEMM_SMALL_PF2_TILES (2048^3 to
 //                     3584^3, 6144x6144x1024).
