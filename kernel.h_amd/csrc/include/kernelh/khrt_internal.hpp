@@ -50,12 +50,7 @@ class LaunchArgs {
 // tables and sections all lie inside it; otherwise the reason.
 std::string check_elf_image(const unsigned char *b, size_t size);
 
-// Prelude registry: functions that need another kernel of their module
-// launched first with the same parameters (scan -> scan_reset).
-void register_prelude(void *function, void *prelude, void *module);
-
 // Drops cached occupancy answers (called when a module is unloaded).
 void clear_occupancy_cache();
-void *prelude_for(void *function);
 
 }  // namespace khrt

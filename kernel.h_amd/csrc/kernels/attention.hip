@@ -42,7 +42,9 @@
 // geometry (kernelh_backend.cpp:420-422). Workgroups of exactly 256 threads
 // over 16-byte aligned rows of at least 64 floats take the pipelined path;
 // other launches stage each tile synchronously, and rows that are not
-// 16-byte aligned are read and written a float at a time.
+// 16-byte aligned are read and written a float at a time. Q, K, V and O each
+// use their own descriptor's strides. Descriptors that are not four
+// [batch, heads, seq, 64] tensors with contiguous rows are refused: O := NaN.
 #include "kh_device.h"
 #include "kh_tiles.h"
 
@@ -62,12 +64,12 @@ constexpr float kNegBig = -1e30f;  // finite "minus infinity" seed for m
 // Any workgroup size: synchronous strided staging of one tile.
 __device__ __forceinline__ void stage_kv_generic(float *__restrict__ Ks, float *__restrict__ Vt,
                                                  const float *__restrict__ Kg, const float *__restrict__ Vg,
-                                                 int64_t ks, int64_t key0, int64_t seq) {
+                                                 int64_t ks, int64_t vs, int64_t key0, int64_t seq) {
   for (int e = threadIdx.x; e < TK * D; e += blockDim.x) {
     const int key = e / D, d = e % D;
     const int64_t kk = key0 + key;
     Ks[key * LDK + d] = kk < seq ? Kg[kk * ks + d] : 0.0f;
-    Vt[d * LDV + key] = kk < seq ? Vg[kk * ks + d] : 0.0f;
+    Vt[d * LDV + key] = kk < seq ? Vg[kk * vs + d] : 0.0f;
   }
 }
 
@@ -158,10 +160,10 @@ __device__ __forceinline__ void load_k(float4 (&k)[4], __amdgpu_buffer_rsrc_t rk
     k[i] = as_f4(__builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
   }
 }
-__device__ __forceinline__ void load_v(float4 (&v)[4], __amdgpu_buffer_rsrc_t rv, int64_t ks, int64_t key0, int tid) {
+__device__ __forceinline__ void load_v(float4 (&v)[4], __amdgpu_buffer_rsrc_t rv, int64_t vs, int64_t key0, int tid) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t off = (uint32_t)(((key0 + (tid & 63)) * ks + 4 * ((tid >> 6) + 4 * i)) * 4);
+    const uint32_t off = (uint32_t)(((key0 + (tid & 63)) * vs + 4 * ((tid >> 6) + 4 * i)) * 4);
     v[i] = as_f4(__builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
   }
 }
@@ -183,11 +185,13 @@ __device__ __forceinline__ void store_v(const float4 (&v)[4], float *__restrict_
 // One workgroup's query tiles of one (b, h) slice. VEC4: rows of Q, K, V and
 // O are 16-byte aligned (float4 access, and the pipelined path for 256-thread
 // workgroups); otherwise Q and O move a float at a time and tiles are staged
-// synchronously. Ks, Vt: two LDS tile buffers each, one tile apart.
+// synchronously. qs, ks, vs, os: row strides (floats) of Q, K, V and O.
+// Ks, Vt: two LDS tile buffers each, one tile apart.
 template <bool VEC4>
 __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, const float *__restrict__ Kg,
                                                 const float *__restrict__ Vg, float *__restrict__ Og, int64_t qs,
-                                                int64_t ks, int64_t os, int64_t seq, float *Ks, float *Vt) {
+                                                int64_t ks, int64_t vs, int64_t os, int64_t seq, float *Ks,
+                                                float *Vt) {
   const int tid = threadIdx.x;
   const int lane = kh::lane_id();
   const int wave = tid / kh::kWave;
@@ -196,9 +200,11 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
   const int64_t rows_per_block = (int64_t)QW * nwaves;
   const int64_t nqt = (seq + rows_per_block - 1) / rows_per_block;
   const int64_t ntiles = (seq + TK - 1) / TK;
-  // The fast path's buffer loads address the slice with 32-bit offsets and
-  // bound it by seq rows of ks floats, so every row must hold its D floats.
-  const bool fast = VEC4 && blockDim.x == kFastThreads && ks >= D && (seq + 2 * TK) * ks * 4 < (1ll << 31);
+  // The fast path's buffer loads address the slices with 32-bit offsets and
+  // bound K by seq rows of ks floats and V by seq rows of vs floats, so every
+  // row must hold its D floats.
+  const bool fast = VEC4 && blockDim.x == kFastThreads && ks >= D && vs >= D &&
+                    (seq + 2 * TK) * (ks > vs ? ks : vs) * 4 < (1ll << 31);
   // log2(e)/sqrt(d): S^T comes out in log2 units, so exp(S - m) = 2^(S' - m').
   const float qscale = kh::kLog2e * 0.125f;
 
@@ -226,10 +232,10 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
       const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(Kg), (short)0,
                                                                           (int)(seq * ks * 4), 0x00020000);
       const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(Vg), (short)0,
-                                                                          (int)(seq * ks * 4), 0x00020000);
+                                                                          (int)(seq * vs * 4), 0x00020000);
       float4 kr[4], vr[4];
       load_k(kr, rk, ks, 0, tid);
-      load_v(vr, rv, ks, 0, tid);
+      load_v(vr, rv, vs, 0, tid);
       store_k(kr, Ks, tid);
       store_v(vr, Vt, tid);
       load_k(kr, rk, ks, TK, tid);
@@ -241,7 +247,7 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
       auto step = [&](int64_t t, v16f (&sc)[2], v16f (&sn)[2]) __attribute__((always_inline)) {
         const int cur = t & 1;
         load_k(kr, rk, ks, (t + 2) * TK, tid);
-        load_v(vr, rv, ks, (t + 1) * TK, tid);
+        load_v(vr, rv, vs, (t + 1) * TK, tid);
         qk_tile(sn, q, Ks + (cur ^ 1) * TK * LDK, lane);
         softmax_pv<false>(o, m, l, sc, Vt + cur * D * LDV, t * TK, seq, lane);
         store_k(kr, Ks + cur * TK * LDK, tid);
@@ -264,7 +270,7 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
       softmax_pv<true>(o, m, l, sa, Vt + (t & 1) * D * LDV, t * TK, seq, lane);
     } else {
       for (int64_t t = 0; t < ntiles; ++t) {
-        stage_kv_generic(Ks, Vt, Kg, Vg, ks, t * TK, seq);
+        stage_kv_generic(Ks, Vt, Kg, Vg, ks, vs, t * TK, seq);
         __syncthreads();
         v16f sg[2];
         qk_tile(sg, q, Ks, lane);
@@ -310,6 +316,33 @@ attention(KH_MEMREF4(const float, Q), KH_MEMREF4(const float, K), KH_MEMREF4(con
   const float *__restrict__ Vp = KH_PTR(V);
   float *__restrict__ Op = KH_PTR(O);
   const int64_t heads = Q_n1, seq = Q_n2;
+  // The template's contract (attention.cpp:109-120 refuses other shapes):
+  // four [batch, heads, seq, 64] tensors with contiguous head_dim rows.
+  // Anything else is refused by filling O (as its descriptor describes it)
+  // with NaN, never by computing from memory the descriptors do not cover.
+  const bool same = K_n0 == Q_n0 && V_n0 == Q_n0 && O_n0 == Q_n0 && K_n1 == heads && V_n1 == heads &&
+                    O_n1 == heads && K_n2 == seq && V_n2 == seq && O_n2 == seq;
+  const bool d64 = Q_n3 == D && K_n3 == D && V_n3 == D && O_n3 == D;
+  const bool rows = (Q_s3 == 1 || Q_n3 <= 1) && (K_s3 == 1 || K_n3 <= 1) && (V_s3 == 1 || V_n3 <= 1) &&
+                    (O_s3 == 1 || O_n3 <= 1);
+  if (!(same && d64 && rows)) {
+    const int64_t total = O_n0 * O_n1 * O_n2 * O_n3;
+    const int64_t threads = (int64_t)blockDim.x * blockDim.y * blockDim.z;
+    const int64_t flat = ((int64_t)threadIdx.z * blockDim.y + threadIdx.y) * blockDim.x + threadIdx.x;
+    const int64_t block = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    const int64_t step = threads * gridDim.x * gridDim.y * gridDim.z;
+    for (int64_t e = block * threads + flat; e < total; e += step) {
+      int64_t r = e;
+      const int64_t i3 = r % O_n3;
+      r /= O_n3;
+      const int64_t i2 = r % O_n2;
+      r /= O_n2;
+      const int64_t i1 = r % O_n1;
+      const int64_t i0 = r / O_n1;
+      Op[i0 * O_s0 + i1 * O_s1 + i2 * O_s2 + i3 * O_s3] = __builtin_nanf("");
+    }
+    return;
+  }
   const int64_t hb = blockIdx.y, bb = blockIdx.z;
   if (hb >= heads || bb >= Q_n0) return;
   // Row stride of the [s, d] slice is s2 (d contiguous, s3 == 1).
@@ -325,7 +358,7 @@ attention(KH_MEMREF4(const float, Q), KH_MEMREF4(const float, K), KH_MEMREF4(con
   const bool vec4 = kh::aligned16(Qp) && kh::aligned16(Kp) && kh::aligned16(Vp) && kh::aligned16(Op) &&
                     ((Q_s0 | Q_s1 | Q_s2 | K_s0 | K_s1 | K_s2 | V_s0 | V_s1 | V_s2 | O_s0 | O_s1 | O_s2) & 3) == 0;
   if (vec4)
-    attention_slice<true>(Qg, Kg, Vg, Og, Q_s2, K_s2, O_s2, seq, Ks, Vt);
+    attention_slice<true>(Qg, Kg, Vg, Og, Q_s2, K_s2, V_s2, O_s2, seq, Ks, Vt);
   else
-    attention_slice<false>(Qg, Kg, Vg, Og, Q_s2, K_s2, O_s2, seq, Ks, Vt);
+    attention_slice<false>(Qg, Kg, Vg, Og, Q_s2, K_s2, V_s2, O_s2, seq, Ks, Vt);
 }

@@ -16,8 +16,6 @@
 #endif
 #define KH_SCAN_THREADS 1024
 #define KH_SCAN_TILE (KH_SCAN_PER_THREAD * (KH_SCAN_THREADS - 64))
-// Smallest tile any accepted launch uses (256 threads); sizes the state.
-#define KH_SCAN_MIN_TILE (KH_SCAN_PER_THREAD * (256 - 64))
 
 // GEMM block tiles (rows of C x columns of C per workgroup of 256 threads).
 #define KH_GEMM_BM 128

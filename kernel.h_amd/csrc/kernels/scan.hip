@@ -7,7 +7,8 @@
 // reference needs both launches: a per-256 double-float Blelloch pass, then
 // ONE workgroup that serially builds the exact prefix of all T totals
 // (scan.cpp:400-452). Here `scan` alone produces the final y in one pass over
-// HBM (read x once, write y once: 8 B/element):
+// HBM (read x once, write y once: 8 B/element), launched by itself on
+// whatever the totals buffers hold:
 //
 //   * A workgroup of W threads (256..1024, a multiple of 64) has W/64 - 1
 //     data waves and one control wave. The data waves own a tile of
@@ -32,25 +33,53 @@
 //     issued together) and stops at the nearest inclusive prefix.
 //
 // Look-back state lives in the caller's totals buffers (the reference ABI
-// has no separate workspace):
-//   totals_lo as uint32: [0] = tile ticket
-//   totals_hi as 64-bit slots: [2t] = aggregate of tile t, [2t+1] = its
-//       inclusive prefix, each an fp64 bit pattern, all-ones = not published
-// All-ones cannot be a published value: an fp32 input widened to fp64 has
-// its low 29 mantissa bits clear and fp64 addition only yields canonical or
-// propagated NaN payloads, so a slot's single 64-bit load tells both whether
-// and what was published. Slots are written and polled with relaxed
+// has no separate workspace) and needs no clearing between calls:
+//
+//   totals_lo, from its first 8-byte boundary: a 40-byte Header
+//       counter  64-bit ticket counter; it only ever grows, across calls
+//       base     the counter value at the start of the current call: the
+//                ticket `base + i` is tile i
+//       nonce    device real-time clock when these buffers were first seen
+//       done     workgroups of the current call that have finished
+//       failed   bounded waits that ran out (diagnostic; y is NaN there)
+//       check    mix(base, nonce, header address): the header is recognised
+//                only when it matches
+//   totals_hi, from its first 8-byte boundary: one 24-byte Record per tile
+//       0 .. ntiles-2 (the last tile has no successor): {aggregate,
+//       inclusive prefix, check}, the values as fp64 bit patterns. Once the
+//       aggregate is out, check = aggregate ^ tag_agg(t); once the inclusive
+//       prefix is out, check = aggregate ^ inclusive ^ tag_inc(t), where t is
+//       the tile's absolute ticket and the tags derive from a session key.
+//
+// A value counts as published only when the record's words satisfy one of
+// those equations for this call's ticket of that tile. Tickets are never
+// reused on one header and the session key differs per header address and
+// per nonce, so stale records of earlier calls, zero-filled or NaN-filled
+// memory and leftovers of other kernels all read as "not yet published" (a
+// random 64-bit match is the only way through). The words are separate
+// relaxed atomics; a reader that sees some new and some old words sees a
+// mismatch and polls again. They are written and polled with relaxed
 // agent-scope atomics (coherent across the 8 XCD L2s without the L2
 // write-back/invalidate an acquire/release pair would cost on every poll).
-// Capacity: tiles of >= 192 P elements need 16 B each in totals_hi
-// (T = ceil(n/256) floats); the kernel refuses (y := NaN) anything else.
-// `scan_reset` (same code object) clears the ticket and marks every slot
-// empty; the runtime launches it first, in stream order, before every
-// `scan`, and `scan_totals` does the same afterwards.
+//
+// Calls that run one after another on the same buffers (stream order) need
+// nothing from the host: the last workgroup of a call to finish sets
+// base := counter and re-signs the header for the next call. A header that
+// is not recognised (fresh, zeroed, garbage) is claimed by one workgroup with
+// a compare-and-swap; it starts a new session (base := counter, nonce := the
+// real-time clock) while the others wait for the signature. Tickets taken
+// before that point are told apart by base and taken again. Two calls that
+// overlap in time on the same totals buffers race (as with any shared
+// output buffer); calls on different buffers are independent.
+//
+// Capacity: 40 B (+4 for alignment) of totals_lo and 24 B per tile but one
+// (+4) of totals_hi, both with unit stride; the reference's T = ceil(n/256)
+// floats always suffice (a tile is at least 3072 elements, 48 B of T).
+// Anything else is refused by writing NaN to y without touching the totals.
 //
 // Every wait is bounded: after kSpinLimit polls a tile gives up, poisons its
-// result with NaN and records the failure in the ticket word's top bit, so a
-// corrupted state can never hang the device.
+// result with NaN and counts the failure in the header, so a corrupted
+// state can never hang the device.
 #include "kh_device.h"
 #include "kh_tiles.h"
 
@@ -59,21 +88,181 @@ namespace {
 constexpr int kMaxThreads = KH_SCAN_THREADS;
 constexpr int kMinThreads = 256;
 constexpr int kPerThread = KH_SCAN_PER_THREAD;
-constexpr int kMinTile = KH_SCAN_MIN_TILE;  // 256 threads: sizes the look-back state
 #ifndef KH_SCAN_WINDOW
 #define KH_SCAN_WINDOW 2
 #endif
 constexpr int kWindow = KH_SCAN_WINDOW;  // predecessors polled per lane per look-back step
 constexpr uint32_t kSpinLimit = 1u << 22;
-constexpr uint32_t kFailBit = 0x80000000u;
 constexpr uint64_t kEmpty = ~0ull;
 
-__device__ __forceinline__ uint64_t slot_load(const uint64_t *p) {
+struct Header {
+  uint64_t counter, base, nonce;
+  uint32_t done, failed;
+  uint64_t check;
+};
+static_assert(sizeof(Header) == 40, "header layout");
+
+struct Record {
+  uint64_t agg, inc, check;
+};
+static_assert(sizeof(Record) == 24, "record layout");
+
+// Stafford's mix13 finaliser of SplitMix64: a bijection of 64-bit words.
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ uint64_t nonzero(uint64_t v) { return v == 0 ? 1 : v; }
+
+__device__ __forceinline__ uint64_t session_key(const Header *h, uint64_t nonce) {
+  return mix64(reinterpret_cast<uintptr_t>(h) ^ mix64(nonce ^ 0x5ca11ab1e5ca4a11ull));
+}
+
+__device__ __forceinline__ uint64_t header_check(const Header *h, uint64_t base, uint64_t nonce) {
+  return nonzero(mix64(session_key(h, nonce) ^ mix64(base ^ 0x0c0ffee0ddba11ull)));
+}
+
+// Never a header's check word (only by a random 64-bit coincidence): marks a
+// header being claimed.
+__device__ __forceinline__ uint64_t claim_mark(const Header *h) {
+  return nonzero(mix64(reinterpret_cast<uintptr_t>(h) ^ 0xc1a1bedc1a1bedull));
+}
+
+// Record tags of the tile with absolute ticket t: a session key XOR t. An
+// aggregate-only record has check = agg ^ agg_tag, a complete one
+// check = agg ^ inc ^ inc_tag. Within a session, distinct t give distinct
+// tags; the two kinds use unrelated keys, and a record written under
+// another session (or never written) passes only if its words happen to XOR
+// to a value fixed by unrelated mix64 outputs.
+struct Keys {
+  uint64_t agg, inc;
+};
+
+__device__ __forceinline__ Keys record_keys(uint64_t key) { return Keys{key, mix64(key ^ 0x1dc0ffee5eedull)}; }
+
+__device__ __forceinline__ uint64_t tag(uint64_t key, uint64_t t) { return key ^ t; }
+
+template <typename T>
+__device__ __forceinline__ T ld(const T *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void slot_store(uint64_t *p, double v) {
-  __hip_atomic_store(p, (uint64_t)__double_as_longlong(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+template <typename T>
+__device__ __forceinline__ void st(T *p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename T>
+__device__ __forceinline__ T fetch_add(T *p, T v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t bits(double v) { return (uint64_t)__double_as_longlong(v); }
+
+// Publishes the aggregate of tile t (absolute ticket).
+__device__ __forceinline__ void publish_aggregate(Record *r, const Keys &k, uint64_t t, double agg) {
+  st(&r->agg, bits(agg));
+  st(&r->check, bits(agg) ^ tag(k.agg, t));
+}
+
+// Publishes the inclusive prefix of tile t, whose aggregate is agg (written
+// again here: tile 0 publishes both at once).
+__device__ __forceinline__ void publish_inclusive(Record *r, const Keys &k, uint64_t t, double agg, double inc) {
+  st(&r->agg, bits(agg));
+  st(&r->inc, bits(inc));
+  st(&r->check, bits(agg) ^ bits(inc) ^ tag(k.inc, t));
+}
+
+// The call's view of the state: where it is, the ticket of tile 0 and the
+// session key the record tags derive from.
+struct Session {
+  Header *h;
+  Record *rec;
+  uint64_t base;
+  Keys keys;
+};
+
+// Run by one thread per workgroup at the start of a multi-tile call. Takes
+// the workgroup's first two tickets (t0 < t1, both >= base) and the
+// session; false if the header could not be established within the bounded
+// wait. The header loads and the ticket atomics go out together, so a
+// recognised header costs one round trip.
+struct Opened {
+  uint64_t base, nonce, t0, t1;
+  bool ok;
+};
+
+__device__ __forceinline__ Opened open_session(Header *h) {
+  Opened o;
+  o.ok = true;
+  o.base = ld(&h->base);
+  o.nonce = ld(&h->nonce);
+  uint64_t seen = ld(&h->check);
+  o.t0 = fetch_add(&h->counter, uint64_t(1));
+  o.t1 = fetch_add(&h->counter, uint64_t(1));
+  // Valid: the header is stable for the whole call (only the last workgroup
+  // to finish changes it), so the three words belong together.
+  if (seen == header_check(h, o.base, o.nonce)) return o;
+  // Not recognised (or read while a claimant was writing it). `check` is
+  // read with acquire ordering before base and nonce: when it is a
+  // claimant's signature, the base and nonce read after it are the ones it
+  // signs. A workgroup claims the header only from an unsigned check value,
+  // with a compare-and-swap, so exactly one claims it; the others wait for
+  // the signature.
+  const uint64_t mark = claim_mark(h);
+  for (uint32_t spins = 0;; ++spins) {
+    seen = __hip_atomic_load(&h->check, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+    o.base = ld(&h->base);
+    o.nonce = ld(&h->nonce);
+    if (seen == header_check(h, o.base, o.nonce)) break;
+    uint64_t expect = seen;
+    if (seen != mark && __hip_atomic_compare_exchange_strong(&h->check, &expect, mark, __ATOMIC_RELAXED,
+                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+      // A read-modify-write, so every ticket before it is < base and every
+      // ticket after it >= base.
+      o.base = fetch_add(&h->counter, uint64_t(0));
+      o.nonce = __builtin_amdgcn_s_memrealtime();
+      st(&h->base, o.base);
+      st(&h->nonce, o.nonce);
+      st(&h->done, 0u);
+      st(&h->failed, 0u);
+      __hip_atomic_store(&h->check, header_check(h, o.base, o.nonce), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    if (spins > kSpinLimit) {
+      // The claimant never signed (or the header held the claim mark by
+      // chance): drop the mark so that the next call claims it afresh.
+      uint64_t m = mark;
+      __hip_atomic_compare_exchange_strong(&h->check, &m, uint64_t(0), __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+      o.ok = false;
+      return o;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+  // Tickets taken before the session began are not tiles of this call.
+  if ((int64_t)(o.t1 - o.base) < 0) {
+    o.t0 = fetch_add(&h->counter, uint64_t(1));
+    o.t1 = fetch_add(&h->counter, uint64_t(1));
+  } else if ((int64_t)(o.t0 - o.base) < 0) {
+    o.t0 = o.t1;
+    o.t1 = fetch_add(&h->counter, uint64_t(1));
+  }
+  return o;
+}
+
+// Run by one thread per workgroup after its last ticket has returned. The
+// last workgroup of the call re-signs the header with base := counter, which
+// is the first ticket the next call will see.
+__device__ __forceinline__ void close_session(Header *h, uint64_t nonce) {
+  const uint32_t blocks = gridDim.x * gridDim.y * gridDim.z;
+  if (fetch_add(&h->done, 1u) != blocks - 1) return;
+  const uint64_t next = fetch_add(&h->counter, uint64_t(0));
+  st(&h->base, next);
+  st(&h->done, 0u);
+  st(&h->check, header_check(h, next, nonce));
 }
 
 __device__ __forceinline__ double wave_sum_f64(double v) {
@@ -170,27 +359,46 @@ __device__ __forceinline__ void store_seg(const float (&o)[kPerThread], __amdgpu
 }
 
 // One look-back window: predecessors end, end-1, ..., end - 64 kWindow + 1;
-// lane l, slot j holds distance d = l + 64 j behind `end`. Slots before tile
-// 0 act as an inclusive prefix of value 0.
+// lane l, slot j holds distance d = l + 64 j behind `end`. Unpublished
+// values read as kEmpty (never an fp64 sum of fp32 inputs: those keep the
+// low 29 mantissa bits of every operand clear, and fp64 addition yields only
+// canonical or propagated NaNs). Slots before tile 0 act as an inclusive
+// prefix of value 0.
 struct Window {
   uint64_t inc[kWindow], ag[kWindow];
 };
 
-__device__ __forceinline__ void poll_window(Window &w, uint64_t *slots, int64_t end, int lane) {
+__device__ __forceinline__ void poll_window(Window &w, const Session &s, int64_t end, int lane) {
+  // Byte offsets of the records from the (wave-uniform) record base: 32-bit,
+  // as no device holds 2^32 B of records (that would be 2^27 tiles).
+  uint64_t ag[kWindow], inc[kWindow], chk[kWindow];
 #pragma unroll
   for (int j = 0; j < kWindow; ++j) {
     const int64_t idx = end - lane - kh::kWave * j;
-    w.inc[j] = (idx >= 0) ? slot_load(&slots[2 * idx + 1]) : 0ull;
-    w.ag[j] = (idx >= 0) ? slot_load(&slots[2 * idx]) : kEmpty;
+    const Record *r = reinterpret_cast<const Record *>(reinterpret_cast<const char *>(s.rec) +
+                                                       (uint32_t)(idx >= 0 ? idx : 0) * (uint32_t)sizeof(Record));
+    ag[j] = ld(&r->agg);
+    inc[j] = ld(&r->inc);
+    chk[j] = ld(&r->check);
+  }
+#pragma unroll
+  for (int j = 0; j < kWindow; ++j) {
+    const int64_t idx = end - lane - kh::kWave * j;
+    const uint64_t t = s.base + (uint64_t)idx;
+    const bool before = idx < 0;
+    const bool has_inc = (chk[j] ^ ag[j] ^ inc[j]) == tag(s.keys.inc, t);
+    const bool has_ag = has_inc || (chk[j] ^ ag[j]) == tag(s.keys.agg, t);
+    w.inc[j] = before ? 0ull : (has_inc ? inc[j] : kEmpty);
+    w.ag[j] = before ? kEmpty : (has_ag ? ag[j] : kEmpty);
   }
 }
 
-// Exclusive prefix of `tile` from its predecessors' published slots (run by
-// one whole wave; the result is wave-uniform), starting from window `w`,
-// already polled for end = tile - 1. Slots only ever go from unpublished to
-// their final value, so an early poll is a valid (if possibly incomplete)
-// observation. NaN if the bounded wait ran out.
-__device__ __forceinline__ double look_back(uint64_t *slots, uint32_t *state, int64_t tile, int lane, Window w) {
+// Exclusive prefix of `tile` from its predecessors' published records (run
+// by one whole wave; the result is wave-uniform), starting from window `w`,
+// already polled for end = tile - 1. Records only ever go from unpublished to
+// their final value within a call, so an early poll is a valid (if possibly
+// incomplete) observation. NaN if the bounded wait ran out.
+__device__ __forceinline__ double look_back(const Session &s, int64_t tile, int lane, Window w) {
   double excl = 0.0;
   int64_t end = tile - 1;  // newest predecessor still to account for
   uint32_t spins = 0;
@@ -211,11 +419,11 @@ __device__ __forceinline__ double look_back(uint64_t *slots, uint32_t *state, in
     }
     if (__ballot(pending) != 0) {
       if (++spins > kSpinLimit) {
-        if (lane == 0) atomicOr(state, kFailBit);
+        if (lane == 0) fetch_add(&s.h->failed, 1u);
         return __builtin_nan("");
       }
       __builtin_amdgcn_s_sleep(1);
-      poll_window(w, slots, end, lane);
+      poll_window(w, s, end, lane);
       continue;
     }
     double contrib = 0.0;
@@ -231,8 +439,15 @@ __device__ __forceinline__ double look_back(uint64_t *slots, uint32_t *state, in
     excl += wave_sum_f64(contrib);
     if (first < kWindow * kh::kWave) return excl;
     end -= kWindow * kh::kWave;
-    poll_window(w, slots, end, lane);
+    poll_window(w, s, end, lane);
   }
+}
+
+// Tile index of an absolute ticket; tickets past the call's tiles map to
+// ntiles (the loop's end marker).
+__device__ __forceinline__ int64_t tile_of(uint64_t ticket, uint64_t base, int64_t ntiles) {
+  const uint64_t i = ticket - base;
+  return i < (uint64_t)ntiles ? (int64_t)i : ntiles;
 }
 
 // The tile loop of one persistent workgroup, a three-stage pipeline. In
@@ -253,10 +468,9 @@ __device__ __forceinline__ double look_back(uint64_t *slots, uint32_t *state, in
 // tiles, and each of those is either finished or in the reduce stage of a
 // workgroup that publishes it without waiting on anything.
 template <bool VEC>
-__device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *__restrict__ Y, uint32_t *state,
-                                           uint64_t *slots, int64_t n, int64_t tr, int64_t tn, bool single,
-                                           uint32_t *s_raw, double *s_wave_total, double *s_prefix,
-                                           double *s_off) {
+__device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *__restrict__ Y, const Session &ses,
+                                           int64_t n, int64_t tr, int64_t tn, bool single, uint64_t *s_raw,
+                                           double *s_wave_total, double *s_prefix, double *s_off) {
   const int tid = threadIdx.x;
   const int lane = kh::lane_id();
   const int wave = tid / kh::kWave;
@@ -283,15 +497,15 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
     // Defined only where it is used (control wave, lane 0): a default value
     // on the data path would be a register write that must wait for the
     // pending atomic, i.e. for all of that wave's outstanding memory ops.
-    uint32_t raw;
+    uint64_t raw;
     // The first look-back poll for tile tc goes out now, before the barrier:
     // tc was reduced (and its predecessors' aggregates published) in earlier
     // iterations, so its round trip overlaps the data waves' reduction.
     // Defined on the control wave only, like `raw`.
     Window w;
     if (ctrl) {
-      if (lane == 0 && !single) raw = atomicAdd(state, 1u);
-      if (tc > 0) poll_window(w, slots, tc - 1, lane);
+      if (lane == 0 && !single) raw = fetch_add(&ses.h->counter, uint64_t(1));
+      if (tc > 0) poll_window(w, ses, tc - 1, lane);
     } else if (tr < ntiles) {
       // ---- reduce tile tr: per-row lane sums (fp64), wave scans, wave total ---
       // off[k] = (rows before k) + (lanes before this one in row k); exact,
@@ -315,18 +529,26 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
       double agg_r = 0.0;
       if (tr < ntiles) {
         agg_r = wave_sum_f64(lane < ndata ? s_wave_total[lane] : 0.0);
-        if (!single && lane == 0) slot_store(&slots[2 * tr + (tr == 0 ? 1 : 0)], agg_r);
+        if (!single && lane == 0 && tr < ntiles - 1) {
+          Record *r = ses.rec + tr;
+          if (tr == 0)
+            publish_inclusive(r, ses.keys, ses.base, agg_r, agg_r);
+          else
+            publish_aggregate(r, ses.keys, ses.base + tr, agg_r);
+        }
       }
       // ---- decoupled look-back for tile tc -------------------------------------
       double excl = 0.0;
       if (tc > 0) {
-        excl = look_back(slots, state, tc, lane, w);
-        if (lane == 0) slot_store(&slots[2 * tc + 1], excl + agg_c);
+        excl = look_back(ses, tc, lane, w);
+        if (lane == 0 && tc < ntiles - 1) {
+          publish_inclusive(ses.rec + tc, ses.keys, ses.base + tc, agg_c, excl + agg_c);
+        }
       }
       agg_c = agg_r;
       if (lane == 0) {
         *s_prefix = excl;
-        s_raw[slot] = single ? 0u : raw;  // the raw ticket word; masked by its readers
+        s_raw[slot] = single ? 0ull : raw;
       }
     } else {
       // ---- tile tn's loads go out now and land during the look-back ----------
@@ -336,7 +558,7 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
         for (int w = 0; w < wave; ++w) wexcl_r += s_wave_total[w];
     }
     kh::lds_barrier();  // barrier B
-    const int64_t after = single ? ntiles : (int64_t)(s_raw[slot] & ~kFailBit);
+    const int64_t after = single ? ntiles : tile_of(s_raw[slot], ses.base, ntiles);
 
     if (!ctrl && tc >= 0) {
       // ---- y = fl32(prefix + row offset + running sum within the float4) -----
@@ -377,6 +599,19 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
   }
 }
 
+// First 8-byte boundary of a float buffer (0 or 1 floats in), by pointer
+// arithmetic so that the compiler keeps the global address space.
+template <typename T>
+__device__ __forceinline__ T *align8(float *p) {
+  return reinterpret_cast<T *>(p + ((reinterpret_cast<uintptr_t>(p) >> 2) & 1));
+}
+
+// Bytes of a unit-stride float buffer from its first 8-byte boundary.
+__device__ __forceinline__ int64_t bytes_from_align8(const float *p, int64_t n0, int64_t s0) {
+  if (n0 > 1 && s0 != 1) return 0;
+  return 4 * (n0 - (int64_t)((reinterpret_cast<uintptr_t>(p) >> 2) & 1));
+}
+
 }  // namespace
 
 extern "C" __global__ void __launch_bounds__(kMaxThreads)
@@ -386,89 +621,97 @@ scan(KH_MEMREF1(const float, x), KH_MEMREF1(float, y), KH_MEMREF1(float, y_lo),
   (void)y_lo_base;
   const float *__restrict__ X = KH_PTR(x);
   float *__restrict__ Y = KH_PTR(y);
-  uint32_t *state = reinterpret_cast<uint32_t *>(KH_PTR(totals_lo));
-  uint64_t *slots = reinterpret_cast<uint64_t *>(KH_PTR(totals_hi));
   const int64_t n = x_n0;
-  const int64_t tile_elems = (int64_t)(blockDim.x - kh::kWave) * kPerThread;
-  const int64_t ntiles = (n + tile_elems - 1) / tile_elems;
   const int tid = threadIdx.x;
 
   __shared__ int64_t s_ticket[2];
-  __shared__ uint32_t s_raw[2];
+  __shared__ uint64_t s_raw[2];
+  __shared__ uint64_t s_session[2];
   __shared__ double s_wave_total[kMaxThreads / kh::kWave];
   __shared__ double s_off[2 * kRows * kMaxThreads];
   __shared__ double s_prefix;
 
-  // The look-back state needs 16 B per tile in totals_hi; workgroups of at
-  // least 256 threads always fit the reference's T = ceil(n/256) floats.
-  // Anything smaller is refused here by poisoning y, never by a hang.
-  if (ntiles > 1 && (blockDim.x < kMinThreads || 4 * ntiles > totals_hi_n0)) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + tid; i < n; i += (int64_t)blockDim.x * gridDim.x)
-      Y[i] = __builtin_nanf("");
+  if (n <= 0) return;
+  // Refusals, decided identically by every workgroup before any state is
+  // touched: the launch shape the tile loop assumes (one-dimensional
+  // workgroups of whole waves, at least three data waves) and room for the
+  // header and the records. y := NaN, never a hang or a stray write.
+  const bool shape_ok = blockDim.x >= kMinThreads && blockDim.x % kh::kWave == 0 && blockDim.y == 1 &&
+                        blockDim.z == 1;
+  const int64_t tile_elems = (int64_t)((int)blockDim.x - kh::kWave) * kPerThread;
+  const int64_t ntiles = shape_ok ? (n + tile_elems - 1) / tile_elems : 0;
+  const bool room = ntiles == 1 ||
+                    (bytes_from_align8(KH_PTR(totals_lo), totals_lo_n0, totals_lo_s0) >= (int64_t)sizeof(Header) &&
+                     bytes_from_align8(KH_PTR(totals_hi), totals_hi_n0, totals_hi_s0) >=
+                         (int64_t)sizeof(Record) * (ntiles - 1));
+  __shared__ bool s_refuse;
+  bool refuse = !shape_ok || !room;
+  Session ses{align8<Header>(KH_PTR(totals_lo)), align8<Record>(KH_PTR(totals_hi)), 0, Keys{0, 0}};
+  const bool single = ntiles == 1;  // one tile: one workgroup, no look-back state
+  Opened o{0, 0, 0, 0, true};
+  if (!refuse && !single) {
+    if (tid == 0) {
+      o = open_session(ses.h);
+      s_session[0] = o.base;
+      s_session[1] = session_key(ses.h, o.nonce);
+      s_ticket[0] = tile_of(o.t0, o.base, ntiles);
+      s_ticket[1] = tile_of(o.t1, o.base, ntiles);
+      s_refuse = !o.ok;
+    }
+    kh::lds_barrier();
+    refuse = s_refuse;
+  }
+  if (refuse) {
+    const int64_t threads = (int64_t)blockDim.x * blockDim.y * blockDim.z;
+    const int64_t flat = ((int64_t)threadIdx.z * blockDim.y + threadIdx.y) * blockDim.x + tid;
+    const int64_t block = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    const int64_t blocks = (int64_t)gridDim.x * gridDim.y * gridDim.z;
+    for (int64_t i = block * threads + flat; i < n; i += blocks * threads) Y[i] = __builtin_nanf("");
     return;
   }
-  const bool single = ntiles == 1;  // one tile: block 0, no look-back state
   if (single) {
-    if (blockIdx.x != 0) return;
+    if (blockIdx.x != 0 || blockIdx.y != 0 || blockIdx.z != 0) return;
     s_ticket[0] = 0;
     s_ticket[1] = ntiles;
-  } else if (tid == 0) {
-    s_ticket[0] = (int64_t)(atomicAdd(state, 1u) & ~kFailBit);
-    s_ticket[1] = (int64_t)(atomicAdd(state, 1u) & ~kFailBit);
+    s_session[0] = 0;
+    s_session[1] = 0;
+    kh::lds_barrier();
   }
-  kh::lds_barrier();
   const int64_t first = s_ticket[0];
   const int64_t second = s_ticket[1];
-  if (first >= ntiles) return;
-  if (kh::aligned16(X) && kh::aligned16(Y) && (n & 3) == 0)
-    scan_tiles<true>(X, Y, state, slots, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off);
-  else
-    scan_tiles<false>(X, Y, state, slots, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off);
-}
-
-// Clears the ticket (totals_lo[0]) and marks every tile slot in totals_hi
-// empty. Sized for the smallest tile any scan launch uses (256 threads).
-__device__ __forceinline__ void reset_state(uint32_t *state, uint64_t *slots, int64_t ntiles) {
-  const int64_t stride = (int64_t)blockDim.x * gridDim.x;
-  const int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i0 == 0) state[0] = 0u;
-  for (int64_t i = i0; i < 2 * ntiles; i += stride) slots[i] = kEmpty;
-}
-
-// Launched by the runtime before every `scan` on the same stream.
-extern "C" __global__ void __launch_bounds__(256)
-scan_reset(KH_MEMREF1(const float, x), KH_MEMREF1(float, y), KH_MEMREF1(float, y_lo),
-           KH_MEMREF1(float, totals_hi), KH_MEMREF1(float, totals_lo)) {
-  const int64_t ntiles = (x_n0 + kMinTile - 1) / kMinTile;
-  if (ntiles <= 1) return;
-  reset_state(reinterpret_cast<uint32_t *>(KH_PTR(totals_lo)), reinterpret_cast<uint64_t *>(KH_PTR(totals_hi)),
-              ntiles);
+  ses.base = s_session[0];
+  ses.keys = record_keys(s_session[1]);
+  if (first < ntiles) {
+    if (kh::aligned16(X) && kh::aligned16(Y) && (n & 3) == 0)
+      scan_tiles<true>(X, Y, ses, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off);
+    else
+      scan_tiles<false>(X, Y, ses, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off);
+  }
+  // Every ticket this workgroup took has returned by now (the last one was
+  // read through LDS before the final barrier).
+  if (!single && tid == 0) close_session(ses.h, o.nonce);
 }
 
 // The reference's second pass (scan.cpp:350-453). With the single-pass
-// `scan`, y is already final: this kernel leaves y unchanged, writes each
-// 256-element block's exclusive offset (off_hi = y[256 b - 1], the fp32
-// rounding of the exact exclusive prefix; off_lo = off_lo2 = 0) and clears
-// the look-back state for the next call.
+// `scan`, y is already final: this kernel leaves y and the totals unchanged
+// and writes each 256-element block's exclusive offset (off_hi = y[256 b - 1],
+// the fp32 rounding of the exact exclusive prefix; off_lo = off_lo2 = 0).
 extern "C" __global__ void __launch_bounds__(256)
 scan_totals(KH_MEMREF1(float, totals_hi), KH_MEMREF1(float, totals_lo), KH_MEMREF1(float, off_hi),
             KH_MEMREF1(float, off_lo), KH_MEMREF1(float, off_lo2), KH_MEMREF1(float, y),
             KH_MEMREF1(float, y_lo)) {
+  (void)totals_hi_alloc;
+  (void)totals_lo_alloc;
   const int64_t n = y_n0;
   const int64_t T = off_hi_n0;
-  const int64_t ntiles = (n + kMinTile - 1) / kMinTile;
   const float *__restrict__ Y = KH_PTR(y);
   float *__restrict__ oh = KH_PTR(off_hi);
   float *__restrict__ ol = KH_PTR(off_lo);
   float *__restrict__ ol2 = KH_PTR(off_lo2);
   const int64_t stride = (int64_t)blockDim.x * gridDim.x;
   for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < T; b += stride) {
-    oh[b] = (b == 0) ? 0.0f : Y[b * 256 - 1];
+    oh[b] = (b == 0 || b * 256 > n) ? 0.0f : Y[b * 256 - 1];
     ol[b] = 0.0f;
     ol2[b] = 0.0f;
-  }
-  if (ntiles > 1) {
-    reset_state(reinterpret_cast<uint32_t *>(KH_PTR(totals_lo)), reinterpret_cast<uint64_t *>(KH_PTR(totals_hi)),
-                ntiles);
   }
 }

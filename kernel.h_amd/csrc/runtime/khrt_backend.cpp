@@ -21,11 +21,6 @@ namespace {
 thread_local std::string g_error;
 int g_device = -1;
 std::mutex g_mu;
-struct Prelude {
-  void *function;  // kernel launched first with the same parameters
-  void *module;    // module both kernels live in
-};
-std::unordered_map<void *, Prelude> g_prelude;
 // Private copy of each loaded module's code object, keyed by module.
 std::unordered_map<void *, std::unique_ptr<unsigned char[], void (*)(void *)>> g_images;
 }  // namespace
@@ -136,17 +131,6 @@ std::string check_elf_image(const unsigned char *b, size_t size) {
     }
   }
   return "";
-}
-
-void register_prelude(void *function, void *prelude, void *module) {
-  std::lock_guard<std::mutex> lock(g_mu);
-  g_prelude[function] = Prelude{prelude, module};
-}
-
-void *prelude_for(void *function) {
-  std::lock_guard<std::mutex> lock(g_mu);
-  auto it = g_prelude.find(function);
-  return it == g_prelude.end() ? nullptr : it->second.function;
 }
 
 }  // namespace khrt
@@ -307,15 +291,6 @@ int khrt_module_get_function(void **function, void *module, const char *name) {
     return fail(static_cast<int>(e), std::string("hipModuleGetFunction(\"") + name + "\"): " + hipGetErrorString(e));
   }
   *function = f;
-  // The look-back scan carries its state-reset prelude in the same module.
-  if (std::strcmp(name, "scan") == 0) {
-    hipFunction_t reset = nullptr;
-    if (hipModuleGetFunction(&reset, static_cast<hipModule_t>(module), "scan_reset") == hipSuccess) {
-      register_prelude(f, reset, module);
-    } else {
-      (void)hipGetLastError();
-    }
-  }
   return 0;
 }
 
@@ -325,9 +300,6 @@ int khrt_module_unload(void *module) {
   if (e != hipSuccess) return fail_hip(e, "hipModuleUnload");
   std::lock_guard<std::mutex> lock(g_mu);
   g_images.erase(module);  // the private image copy goes with the module
-  for (auto it = g_prelude.begin(); it != g_prelude.end();) {
-    it = (it->second.module == module) ? g_prelude.erase(it) : std::next(it);
-  }
   clear_occupancy_cache();
   return 0;
 }

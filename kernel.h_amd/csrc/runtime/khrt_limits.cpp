@@ -222,9 +222,6 @@ int verified_launch(void *function, khrt_dim3 grid, khrt_dim3 block, size_t shar
   c.static_shared_bytes = shared;
   const std::string diag = verify(c, limits, function);
   if (!diag.empty()) return fail(KHRT_E_REFUSED, "KernelLaunch::launch refused: " + diag);
-  if (void *pre = prelude_for(function)) {
-    if (int rc = khrt_launch_raw(pre, khrt_dim3{64, 1, 1}, khrt_dim3{256, 1, 1}, 0, stream, params)) return rc;
-  }
   return khrt_launch_raw(function, grid, block, shared, stream, params);
 }
 

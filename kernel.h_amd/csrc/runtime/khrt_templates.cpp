@@ -260,6 +260,37 @@ const char *launch_symbol(const Template *t, const Shape &s) {
   return t->name;
 }
 
+// Workgroups of `block` threads of `fn` resident on the whole device at
+// once (occupancy per CU x CUs), asked once per function; 0 if unknown.
+int64_t resident_workgroups(void *fn, unsigned block) {
+  struct Entry {
+    void *fn;
+    unsigned block;
+    int64_t resident;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> cache;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (const auto &e : cache) {
+      if (e.fn == fn && e.block == block) return e.resident;
+    }
+  }
+  int per_cu = 0;
+  khrt_device_limits live;
+  int64_t resident = 0;
+  if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, static_cast<hipFunction_t>(fn),
+                                                         static_cast<int>(block), 0) == hipSuccess &&
+      per_cu > 0 && khrt_live_limits(&live) == 0 && live.cu_count > 0) {
+    resident = int64_t(per_cu) * live.cu_count;
+  } else {
+    (void)hipGetLastError();
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  cache.push_back({fn, block, resident});
+  return resident;
+}
+
 // Packs, verifies and launches template `name`.
 int launch_template(const char *name, khrt::LaunchArgs &args, const Shape &shape, void *stream) {
   const Template *t = find_template(name);
@@ -271,14 +302,8 @@ int launch_template(const char *name, khrt::LaunchArgs &args, const Shape &shape
   if (std::strcmp(name, "scan") == 0) {
     // The look-back scan is persistent: one resident wave of workgroups
     // loops over tiles, so launch no more workgroups than fit at once.
-    int per_cu = 0;
-    khrt_device_limits live;
-    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, static_cast<hipFunction_t>(fn),
-                                                           static_cast<int>(block.x), 0) == hipSuccess &&
-        per_cu > 0 && khrt_live_limits(&live) == 0 && live.cu_count > 0) {
-      grid.x = static_cast<unsigned>(std::min<int64_t>(grid.x, int64_t(per_cu) * live.cu_count));
-    } else {
-      (void)hipGetLastError();
+    if (const int64_t resident = resident_workgroups(fn, block.x); resident > 0) {
+      grid.x = static_cast<unsigned>(std::min<int64_t>(grid.x, resident));
     }
   }
   return khrt::verified_launch(fn, grid, block, 0, stream, args.params(), args.count());
@@ -405,14 +430,10 @@ int kh_layernorm(const float *x, const float *gamma, const float *beta, float *y
 int kh_scan(const float *x, float *y, float *y_lo, float *totals_hi, float *totals_lo, int64_t n, void *stream) {
   if (n <= 0) return bad("scan: n must be positive");
   if (!x || !y || !totals_hi || !totals_lo) return bad("scan: null buffer");
+  // The look-back state (a 40-byte header in totals_lo, 24 B per tile in
+  // totals_hi) always fits the reference's T = ceil(n/256) floats of each;
+  // the kernel establishes it on first use and keeps it valid across calls.
   const int64_t T = ceil_div(n, 256);
-  const int64_t tiles = ceil_div(n, KH_SCAN_MIN_TILE);  // smallest tile the kernel accepts
-  if (tiles > 1 && (reinterpret_cast<uintptr_t>(totals_hi) & 7u) != 0) {
-    return bad("scan: totals_hi must be 8-byte aligned (it holds the fp64 look-back values)");
-  }
-  // Look-back state: 16 B per tile in totals_hi, the ticket in totals_lo[0].
-  // T = ceil(n/256) floats always suffices once there is more than one tile.
-  if (tiles > 1 && T < 4 * tiles) return bad("scan: totals buffers too small for the look-back state");
   khrt::LaunchArgs args;
   args.add_memref(x, {n});
   args.add_memref(y, {n});

@@ -333,8 +333,8 @@ def test_entry_points_validate_before_touching_a_device():
         kh.vecadd(None, 0x10, 0x20, 16)
     assert "null buffer" in e.value.message
     with pytest.raises(kh.KhrtError) as e:
-        kh.scan(0x1000, 0x2000, 0x3000, 0x4004, 0x5000, 1 << 20)
-    assert "8-byte aligned" in e.value.message
+        kh.scan(0x1000, 0x2000, 0x3000, None, 0x5000, 1 << 20)
+    assert "null buffer" in e.value.message
 
 
 def test_corrupt_image_is_a_typed_error():

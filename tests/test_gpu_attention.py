@@ -111,6 +111,69 @@ def test_attention_padded_row_stride(dev, pitch):
     _check(Q, K, V, np.ascontiguousarray(got), b, h, s)
 
 
+@pytest.mark.parametrize("threads", [256, 64])
+def test_attention_distinct_pitches(dev, threads):
+    """Q, K, V and O each with a row pitch of their own (64 / 68 / 80 / 72
+    floats; 256-thread workgroups take the pipelined path, 64-thread ones
+    the synchronous one). Padding is NaN in the inputs, so reading V (or K)
+    with another tensor's stride shows up as a wrong or non-finite row; O's
+    padding must keep its sentinel."""
+    b, h, s = 2, 2, 200
+    pitches = {"Q": 64, "K": 68, "V": 80, "O": 72}
+    n = b * h * s * D
+    Q = O.normal(n, 21, 0.0, 1.0)
+    K = O.normal(n, 22, 0.0, 1.0)
+    V = O.normal(n, 23, 0.0, 1.0)
+
+    def padded(x, pitch, fill):
+        p = np.full((b * h * s, pitch), fill, np.float32)
+        if x is not None:
+            p[:, :D] = x.reshape(b * h * s, D)
+        return p
+
+    host = {"Q": padded(Q, 64, np.nan), "K": padded(K, 68, np.nan), "V": padded(V, 80, np.nan),
+            "O": padded(None, 72, -7.0)}
+    bufs = {k: up(v.ravel()) for k, v in host.items()}
+    args = kh.LaunchArgs()
+    for i, name in enumerate(("Q", "K", "V", "O")):
+        p = pitches[name]
+        args.add_memref(bufs[name], [b, h, s, D])
+        # Rank-4 descriptor: ptr, ptr, offset, 4 sizes, 4 strides (slots 7..10).
+        args.slots[11 * i + 7:11 * i + 11] = [h * s * p, s * p, p, 1]
+    say(f"attention distinct pitches {pitches} threads={threads}")
+    grid = ((s + 127) // 128, h, b) if threads == 256 else (s, h, b)
+    kh.kernel_launch(kh.template_function("attention"), grid, (threads, 1, 1), args)
+    out = down(bufs["O"], b * h * s * 72).reshape(b * h * s, 72)
+    assert np.all(out[:, D:] == -7.0), "O's row padding was written"
+    _check(Q, K, V, np.ascontiguousarray(out[:, :D]).reshape(b * h, s, D), b, h, s)
+
+
+@pytest.mark.parametrize("bad", ["head_dim32", "kv_seq", "v_heads"])
+def test_attention_refuses_other_shapes(dev, bad):
+    """head_dim != 64 (attention.cpp:115-120) or K/V extents that differ from
+    Q's: O is filled with NaN (by its own descriptor) and nothing past it is
+    touched."""
+    b, h, s, d = 1, 2, 128, 64
+    shapes = {k: [b, h, s, d] for k in "QKVO"}
+    if bad == "head_dim32":
+        shapes = {k: [b, h, s, 32] for k in "QKVO"}
+    elif bad == "kv_seq":
+        shapes["K"] = [b, h, s // 2, d]
+        shapes["V"] = [b, h, s // 2, d]
+    else:
+        shapes["V"] = [b, 1, s, d]
+    guard = 1024
+    bufs = {k: empty(int(np.prod(v)) + guard, 1.0) for k, v in shapes.items()}
+    args = kh.LaunchArgs()
+    for k in "QKVO":
+        args.add_memref(bufs[k], shapes[k])
+    say(f"attention refusal {bad}")
+    kh.launch_raw(kh.template_function("attention"), ((s + 127) // 128, h, b), (256, 1, 1), args)
+    no = int(np.prod(shapes["O"]))
+    out = down(bufs["O"], no + guard)
+    assert np.all(np.isnan(out[:no])) and np.all(out[no:] == 1.0)
+
+
 def test_attention_reference_geometry_and_negative_control(dev):
     b, h, s = 1, 2, 256
     n = b * h * s * D

@@ -1,9 +1,15 @@
 """Single-pass look-back scan on the GPU: bit-exact against the fp64 prefix
 rounded to fp32 (the reference pins max abs 0.0 at these sizes and seed,
 e2e_scan_test.cpp:17-20, 225-256), the BASELINE sizes 10^6 and 2^26, ragged
-tails, repeated calls on the same (dirty) buffers, the reference's raw
-two-launch protocol (scan then scan_totals on uninitialised buffers,
-kernelh_backend.cpp:334-357) and the exclusive-reference negative control.
+tails, repeated calls on the same (dirty) buffers, and the exclusive-reference
+negative control.
+
+The reference launches `scan` and `scan_totals` itself, with plain
+hipModuleLaunchKernel on uninitialised buffers and its own geometry
+(kernelh_backend.cpp:334-357, e2e_scan_test.cpp:150-175). Those tests here go
+through `khrt_launch_raw`: no verification, nothing launched before the
+kernel, totals buffers as the caller left them (never written, zero-filled,
+NaN-filled, or left by an earlier call or by the reference's own protocol).
 """
 import numpy as np
 import pytest
@@ -52,9 +58,75 @@ def test_scan_repeated_calls_reuse_state(dev):
         assert np.array_equal(got, ref)
 
 
+def _scan_args(dx, dy, dylo, dth, dtl, n, T, T_hi=None, T_lo=None):
+    a = kh.LaunchArgs().add_memref(dx, [n]).add_memref(dy, [n]).add_memref(dylo, [n]) \
+        .add_memref(dth, [T if T_hi is None else T_hi]).add_memref(dtl, [T if T_lo is None else T_lo])
+    assert a.param_count() == 25
+    return a
+
+
+def _raw_scan(f, x_buf, y_buf, ylo, th, tl, n, geometry):
+    """One raw `scan` launch: the reference's geometry, ceil(n/256) x 256
+    (kernelh_backend.cpp:335), or the launcher's (1024 threads, one resident
+    round of workgroups)."""
+    T = kh.scan_workspace_floats(n)
+    if geometry == "reference":
+        grid, block = (T, 1, 1), (256, 1, 1)
+    else:
+        grid, block = kh.geometry("scan", f"n={n}")
+        grid = (min(grid[0], 256), 1, 1)
+    kh.launch_raw(f, grid, block, _scan_args(x_buf, y_buf, ylo, th, tl, n, T))
+
+
+# What the caller's totals buffers hold before the first launch.
+_TOTALS = {"uninitialised": None, "zero": 0.0, "nan": float("nan"), "ones": 1.0}
+
+
+@pytest.mark.parametrize("n", [1000000, 1 << 26])
+@pytest.mark.parametrize("geometry", ["reference", "launcher"])
+def test_scan_raw_launch_any_totals(dev, n, geometry):
+    """`scan` alone through plain hipModuleLaunchKernel on totals in every
+    starting state, then again on the same buffers (state left by the
+    previous call), bit-exact each time."""
+    x = O.uniform(n, 0x5CA4 + n, 0.0, 1.0)  # 2^-24 grid: the fp64 prefix is exact
+    ref = np.cumsum(x.astype(np.float64)).astype(np.float32)
+    T = kh.scan_workspace_floats(n)
+    m = kh.GpuModule(kh.code_object("scan"))
+    f = m.get_function("scan")
+    dx = up(x)
+    for state, fill in _TOTALS.items():
+        th, tl = empty(T, fill), empty(T, fill)
+        for call in range(2):
+            dy = empty(n)
+            say(f"scan raw n={n} geometry={geometry} totals={state} call={call}")
+            _raw_scan(f, dx, dy, empty(1, None), th, tl, n, geometry)
+            got = down(dy, n)
+            bad = np.flatnonzero(got != ref)
+            assert bad.size == 0, f"{state} call {call}: {bad.size} differ, first at {bad[:5]}"
+
+
+def test_scan_raw_launch_misaligned_totals(dev):
+    """Totals descriptors that start 4 bytes past an 8-byte boundary (the
+    header and records move to the next boundary inside the buffer)."""
+    n = 500000
+    T = kh.scan_workspace_floats(n)
+    x = O.mt19937_fill(n, 0x29C0FFEE)
+    ref = O.ref_scan(x)
+    f = kh.GpuModule(kh.code_object("scan")).get_function("scan")
+    th_big, tl_big = empty(T + 2, 3.0), empty(T + 2, -2.0)
+    dx = up(x)
+    for call in range(2):
+        dy = empty(n)
+        say(f"scan raw misaligned totals call={call}")
+        kh.launch_raw(f, (T, 1, 1), (256, 1, 1),
+                      _scan_args(dx, dy, empty(1, None), th_big.ptr + 4, tl_big.ptr + 4, n, T))
+        assert np.array_equal(down(dy, n), ref)
+
+
 def test_scan_reference_two_launch_protocol(dev):
     # Raw protocol: caller geometry ceil(n/256) x 256 for `scan`, 1 x 256 for
-    # `scan_totals`, uninitialised device buffers, verified KernelLaunch path.
+    # `scan_totals`, uninitialised device buffers, plain launches; then a
+    # second scan on the same buffers after scan_totals has run.
     n = 65536 + 17
     T = (n + 255) // 256
     x = O.mt19937_fill(n, 0x29C0FFEE)
@@ -63,21 +135,81 @@ def test_scan_reference_two_launch_protocol(dev):
     dth, dtl, oh, ol, ol2 = (empty(T, None) for _ in range(5))
     m = kh.GpuModule(kh.code_object("scan"))
     f1, f2 = m.get_function("scan"), m.get_function("scan_totals")
-    a1 = kh.LaunchArgs().add_memref(dx, [n]).add_memref(dy, [n]).add_memref(dylo, [n]) \
-        .add_memref(dth, [T]).add_memref(dtl, [T])
-    assert a1.param_count() == 25
     a2 = kh.LaunchArgs()
     for b, s in ((dth, T), (dtl, T), (oh, T), (ol, T), (ol2, T), (dy, n), (dylo, n)):
         a2.add_memref(b, [s])
     assert a2.param_count() == 35
-    say("scan raw two-launch protocol")
-    kh.kernel_launch(f1, (T, 1, 1), (256, 1, 1), a1)
-    kh.kernel_launch(f2, (1, 1, 1), (256, 1, 1), a2)
-    got = down(dy, n)
     ref = O.ref_scan(x)
-    assert np.array_equal(got, ref)
-    offs = down(oh, T)
-    assert offs[0] == 0.0 and np.array_equal(offs[1:], ref[255:-1:256][: T - 1])
+    for call in range(2):
+        dy.fill(float("nan"))
+        say(f"scan raw two-launch protocol call={call}")
+        kh.launch_raw(f1, (T, 1, 1), (256, 1, 1), _scan_args(dx, dy, dylo, dth, dtl, n, T))
+        kh.launch_raw(f2, (1, 1, 1), (256, 1, 1), a2)
+        got = down(dy, n)
+        assert np.array_equal(got, ref)
+        offs = down(oh, T)
+        assert offs[0] == 0.0 and np.array_equal(offs[1:], ref[255:-1:256][: T - 1])
+
+
+def test_scan_verified_kernel_launch(dev):
+    # The reference's KernelLaunch path (verified, then launched) on the
+    # same code object, reference geometry.
+    n = 123457
+    T = kh.scan_workspace_floats(n)
+    x = O.mt19937_fill(n, 0x51AC0D3E)
+    f = kh.GpuModule(kh.code_object("scan")).get_function("scan")
+    dy = empty(n)
+    say("scan verified kernel_launch")
+    kh.kernel_launch(f, (T, 1, 1), (256, 1, 1), _scan_args(up(x), dy, empty(1, None), empty(T, None),
+                                                           empty(T, None), n, T))
+    assert np.array_equal(down(dy, n), O.ref_scan(x))
+
+
+@pytest.mark.parametrize("short", ["totals_hi", "totals_lo", "block"])
+def test_scan_refuses_without_touching_totals(dev, short):
+    """Too little room for the look-back state, or a workgroup shape the tile
+    loop does not take: y becomes NaN and the totals (and the memory past
+    them) keep their contents."""
+    n = 200000  # 66 tiles of 3072 at 256 threads: 65 records of 24 B = 390 floats
+    T = kh.scan_workspace_floats(n)
+    x = O.uniform(n, 5, 0.0, 1.0)
+    guard = 4096
+    th, tl = empty(T + guard, 5.0), empty(T + guard, 6.0)
+    t_hi, t_lo, block = T, T, 256
+    if short == "totals_hi":
+        t_hi = 300
+    elif short == "totals_lo":
+        t_lo = 9  # 36 B: the 40-byte header does not fit
+    else:
+        block = 128
+    f = kh.GpuModule(kh.code_object("scan")).get_function("scan")
+    dy = empty(n, 0.25)
+    say(f"scan refusal short={short}")
+    kh.launch_raw(f, ((n + block - 1) // block, 1, 1), (block, 1, 1),
+                  _scan_args(up(x), dy, empty(1, None), th, tl, n, T, t_hi, t_lo))
+    assert np.all(np.isnan(down(dy, n)))
+    assert np.all(down(th, T + guard) == 5.0) and np.all(down(tl, T + guard) == 6.0)
+
+
+def test_scan_two_streams_distinct_buffers(dev):
+    """Calls on different totals buffers are independent, also when they run
+    at the same time on two streams."""
+    n = 1 << 22
+    xs = [O.uniform(n, 900 + i, 0.0, 1.0) for i in range(2)]
+    refs = [np.cumsum(x.astype(np.float64)).astype(np.float32) for x in xs]
+    T = kh.scan_workspace_floats(n)
+    streams = [kh.Stream(), kh.Stream()]
+    bufs = [(up(x), empty(n), empty(1, None), empty(T, None), empty(T, None)) for x in xs]
+    for rep in range(3):
+        say(f"scan two streams rep={rep}")
+        for (dx, dy, dylo, th, tl), s in zip(bufs, streams):
+            kh.scan(dx, dy, dylo, th, tl, n, s)
+        for s in streams:
+            s.synchronize()
+        for (dx, dy, *_), ref in zip(bufs, refs):
+            assert np.array_equal(down(dy, n), ref)
+    for s in streams:
+        s.destroy()
 
 
 def test_scan_negative_control_exclusive(dev):
