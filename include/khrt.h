@@ -186,10 +186,8 @@ KHRT_API int khrt_compute_occupancy(const khrt_occupancy_input *input,
 /* ---- 4. Verified launch (kernel_launch.cpp:100-132) --------------------- */
 /* Refuses (KHRT_E_REFUSED, message "KernelLaunch::launch refused: ...") when
  * the verifier finds any violation against the live device limits; null
- * function or empty params -> KHRT_E_INVALID. Kernels whose code object
- * carries a look-back state prelude (scan) get it launched first, in stream
- * order, so a caller replaying the reference's raw two-launch protocol on
- * uninitialised buffers stays correct. */
+ * function or empty params -> KHRT_E_INVALID. Launches exactly the given
+ * kernel, nothing before or after it. */
 KHRT_API int khrt_kernel_launch(void *function, khrt_dim3 grid, khrt_dim3 block,
                                 size_t shared_bytes, void *stream, void **params,
                                 size_t param_count);
@@ -253,14 +251,19 @@ KHRT_API int kh_layernorm(const float *x, const float *gamma, const float *beta,
 /* scan: inclusive prefix sum of x[n] into y[n] (scan.cpp:163-341 argument
  * list: x, y, y_lo[n], totals_hi[T], totals_lo[T], T = ceil(n/256)) ->
  * 25 slots. y holds the finished result when the launch completes;
- * y_lo is not written; totals_hi/lo hold the look-back state. */
+ * y_lo is not written. totals_hi/lo hold the look-back state: whatever they
+ * contain before the first call (never written, zeroed, another kernel's
+ * data), the kernel recognises it as not its own and starts afresh, and it
+ * leaves them valid for the next call; the same holds for a raw
+ * hipModuleLaunchKernel of the `scan` symbol. Calls that overlap in time on
+ * the same totals buffers race. */
 KHRT_API int kh_scan(const float *x, float *y, float *y_lo, float *totals_hi, float *totals_lo,
                      int64_t n, void *stream);
 /* scan_totals: the reference's second pass (scan.cpp:350-453 argument list:
  * totals_hi, totals_lo, off_hi, off_lo, off_lo2 [T]; y, y_lo [n]) -> 35
- * slots. With the single-pass scan it leaves y unchanged, clears the
- * look-back state and writes each 256-block's exclusive offset
- * (off_hi = fp32 rounding, off_lo = off_lo2 = 0). */
+ * slots. With the single-pass scan it leaves y and the totals unchanged and
+ * writes each 256-block's exclusive offset (off_hi = fp32 rounding,
+ * off_lo = off_lo2 = 0). */
 KHRT_API int kh_scan_totals(const float *totals_hi, const float *totals_lo, float *off_hi,
                             float *off_lo, float *off_lo2, float *y, float *y_lo, int64_t n,
                             void *stream);
