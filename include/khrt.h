@@ -275,6 +275,16 @@ KHRT_API int kh_gemm(const float *A, const float *B, float *C, int64_t m, int64_
  * head_dim must be 64 (attention.cpp:115-120). */
 KHRT_API int kh_attention(const float *Q, const float *K, const float *V, float *O, int64_t batch,
                           int64_t heads, int64_t seq, int64_t head_dim, void *stream);
+/* scan without allocating: y[n] = inclusive prefix sum of x[n], the result
+ * of kh_scan, with the look-back state in a 4 MiB device array per GPU that
+ * the library holds until the process ends, instead of caller totals. No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory at call time (HIP graph capture, serving loops, harnesses
+ * that forbid hipMalloc). khrt_init_device sets it up on a device (array
+ * address, scan module, verified launch shape); the call itself allocates
+ * nothing and refuses a device not set up that way. n <= 2^31. Calls on one
+ * GPU share its array: calls that overlap in time on one GPU race. */
+KHRT_API int kh_scan_noalloc(const float *x, float *y, int64_t n, void *stream);
 
 /* ---- 6. Roofline microbenchmarks (bench/refs/roofline.hip:22-53,
  *         bench/harness/roofline.cpp:60-130) ------------------------------ */

@@ -183,11 +183,18 @@ def build(jobs: int = 8, verbose: bool = False) -> None:
     embed = write_embed(present)
     write_resources(present)
 
-    rt_srcs = sorted(os.path.join(RDIR, f) for f in os.listdir(RDIR) if f.endswith(".cpp"))
+    # Runtime sources: plain C++ (host compiler) and HIP (hipcc, host code
+    # plus the device variables they register with the HIP runtime).
+    rt_srcs = sorted(os.path.join(RDIR, f) for f in os.listdir(RDIR) if f.endswith((".cpp", ".hip")))
 
     def cxx(src):
         obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-        run([CXX, *HOST_FLAGS, "-c", src, "-o", obj], verbose)
+        if src.endswith(".hip"):
+            run([HIPCC, "-x", "hip", f"--offload-arch={ARCH}", "-O2", "-fPIC", "-std=c++17",
+                 "-fvisibility=hidden", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                 f"-I{REPO}/include", f"-I{HERE}/csrc/include", f"-I{KDIR}", "-c", src, "-o", obj], verbose)
+        else:
+            run([CXX, *HOST_FLAGS, "-c", src, "-o", obj], verbose)
         return obj
 
     with ThreadPoolExecutor(max_workers=jobs) as ex:

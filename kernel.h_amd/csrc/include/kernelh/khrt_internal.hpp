@@ -50,6 +50,11 @@ class LaunchArgs {
 // tables and sections all lie inside it; otherwise the reason.
 std::string check_elf_image(const unsigned char *b, size_t size);
 
+// Per-device set-up of the allocation-free scan entry point (its state
+// array's address, the scan function, a verified launch shape); run by
+// khrt_init_device with the device current.
+int noalloc_setup(int device);
+
 // Drops cached occupancy answers (called when a module is unloaded).
 void clear_occupancy_cache();
 

@@ -180,7 +180,7 @@ int khrt_init_device(int ordinal) {
   e = hipSetDevice(ordinal);
   if (e != hipSuccess) return fail_hip(e, "hipSetDevice");
   g_device = ordinal;
-  return 0;
+  return noalloc_setup(ordinal);
 }
 
 int khrt_get_device_info(khrt_device_info *out) {

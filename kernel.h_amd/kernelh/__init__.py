@@ -147,6 +147,7 @@ SIGNATURES = {
     "kh_softmax": (_i, [_vp, _vp, _i64, _i64, _vp]),
     "kh_layernorm": (_i, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "kh_scan": (_i, [_vp, _vp, _vp, _vp, _vp, _i64, _vp]),
+    "kh_scan_noalloc": (_i, [_vp, _vp, _i64, _vp]),
     "kh_scan_totals": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
     "kh_gemm": (_i, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "kh_attention": (_i, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
@@ -476,6 +477,11 @@ def layernorm(x, gamma, beta, y, rows: int, cols: int, stream=None) -> None:
 
 def scan(x, y, y_lo, totals_hi, totals_lo, n: int, stream=None) -> None:
     check(lib.kh_scan(_ptr(x), _ptr(y), _ptr(y_lo), _ptr(totals_hi), _ptr(totals_lo), n, _ptr(stream)))
+
+
+def scan_noalloc(x, y, n: int, stream=None) -> None:
+    """kh_scan without caller totals and without allocating (khrt.h)."""
+    check(lib.kh_scan_noalloc(_ptr(x), _ptr(y), n, _ptr(stream)))
 
 
 def scan_totals(totals_hi, totals_lo, off_hi, off_lo, off_lo2, y, y_lo, n: int, stream=None) -> None:
