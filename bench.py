@@ -1,12 +1,14 @@
 #!/usr/bin/env python3
 """Benchmark of the kernel.h seven-template hot path on one MI355X.
 
-One step = one pass of the suite the BASELINE metric is quoted on, at the
-BASELINE sizes: gemm 8192^3 (the headline `value`, fp32 TFLOP/s), softmax
-4096x1024 and scan 2^26 (HBM GB/s), plus vecadd 2^24, layernorm 4096x1024,
-fused_gelu 2^26 and attention b4 h16 s4096 d64, each reported under
-"kernels". Inputs are synthetic (numpy generators), resident in HBM before
-the timed region; every launch goes through the khrt C-ABI
+One step = one pass of the suite the BASELINE metric is quoted on: the seven
+templates at all thirteen BASELINE configurations. gemm 8192^3 is the
+headline `value` (fp32 TFLOP/s); softmax 4096x1024 and scan 2^26 are the
+metric's HBM rows; vecadd 2^24, layernorm 4096x1024, fused_gelu 2^22 and
+2^26, scan 10^6, gemm 512^3 / 2048^3 / 8192x8192x256 and attention b4 h16 d64
+at seq 1024 and 4096 complete it, each reported under "kernels". Inputs are
+synthetic (seeded numpy generators of the BASELINE distributions), resident
+in HBM before the timed region; every launch goes through the khrt C-ABI
 (hipModuleLaunchKernel on the embedded gfx950 code objects).
 
 Timing: W untimed warmup steps, then K timed steps bracketed by device
@@ -17,8 +19,11 @@ from HBM rather than the 256 MB Infinity Cache.
 
 Roofline: `achieved` = algorithmic bytes (or FLOPs) per launch / average
 launch duration; `peak` = MI355X published peak (HBM 8 TB/s; fp32 MFMA
-157.3 TFLOP/s). The CPU baseline times the oracle's fp64 reference on a
-bounded sample on this host.
+157.3 TFLOP/s). The measured HBM ceiling of a kernel is the best of copy and
+triad streams at 3 GiB and at that kernel's own bytes per launch (rotated
+the same way), each with the product's streaming geometry and with a
+32-workgroups-per-CU grid. The CPU baseline times the oracle's fp64
+references on a bounded sample on this host.
 """
 from __future__ import annotations
 
@@ -39,13 +44,16 @@ ROTATE_BYTES = 1 << 30  # rotate buffer sets until the working set exceeds 1 GiB
 
 METRIC = "GEMM-8192 fp32 TFLOPS + softmax/scan HBM GB/s, % of MI355X roofline"
 
-# HBM bytes per launch from two rocprofv3 --pmc passes (FETCH_SIZE scaled by
-# 2.000 and WRITE_SIZE by 1.000, the factors a copy kernel of known size
-# reads), recorded in profiles/templates_baseline_sizes_hbm_traffic.md.
+# HBM bytes per launch of the headline kernels, taken from two rocprofv3
+# --pmc passes (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000: the factors a copy
+# kernel of known size reads) over `bench.py --kernels <name>` with its
+# buffer rotation, recorded in profiles/templates_baseline_sizes_hbm_traffic.md.
+# Constants of that profile, not measured by the run that reports them.
 PMC_TRAFFIC_BYTES = {
     "vecadd": 201374080, "softmax": 33634176, "layernorm": 33737882, "scan": 539377210,
     "fused_gelu": 537017626, "gemm": 4281652941, "attention": 1208230925,
 }
+PMC_TRAFFIC_SOURCE = "profiles/templates_baseline_sizes_hbm_traffic.md (constant, not measured by this run)"
 
 
 def log(msg: str) -> None:
@@ -63,17 +71,20 @@ def normal(rng, n, sd):
 
 
 class Case:
-    """One template at one BASELINE configuration."""
+    """One template at one BASELINE configuration. `host` makes the seeded
+    input arrays once; every buffer set gets its own device copies of them
+    (plus its own outputs), so rotated launches read distinct memory."""
 
-    def __init__(self, name, config, work, unit, bound, setup, launch, traffic_note=""):
+    def __init__(self, name, config, work, unit, bound, host, device, launch, note=""):
         self.name, self.config, self.work, self.unit, self.bound = name, config, work, unit, bound
-        self.setup, self.launch, self.traffic_note = setup, launch, traffic_note
+        self.host, self.device, self.launch, self.note = host, device, launch, note
         self.sets = []
         self.ms = []
 
 
 def make_cases(kh, rng, only):
     up = lambda a: kh.Buffer.from_array(a)
+    out = lambda count: kh.Buffer(4 * count)
     cases = []
 
     def add(c):
@@ -82,87 +93,71 @@ def make_cases(kh, rng, only):
 
     n = 1 << 24
     add(Case("vecadd", "n=2^24 fp32, a,b ~ U[-1,1]", 12.0 * n, "GB/s", "hbm",
-             lambda: (up(u24(rng, n, -1, 1)), up(u24(rng, n, -1, 1)), kh.Buffer(4 * n)),
+             lambda: (u24(rng, n, -1, 1), u24(rng, n, -1, 1)),
+             lambda h: (up(h[0]), up(h[1]), out(n)),
              lambda s, st: kh.vecadd(s[0], s[1], s[2], n, st)))
 
     R, C = 4096, 1024
     add(Case("softmax", "4096x1024 fp32, x ~ N(0, 4^2)", 8.0 * R * C, "GB/s", "hbm",
-             lambda: (up(normal(rng, R * C, 4.0)), kh.Buffer(4 * R * C)),
+             lambda: (normal(rng, R * C, 4.0),),
+             lambda h: (up(h[0]), out(R * C)),
              lambda s, st: kh.softmax(s[0], s[1], R, C, st)))
 
     add(Case("layernorm", "4096x1024 fp32, eps 1e-5, x ~ N(0, 4^2), gamma U[0.5,1.5], beta U[-0.1,0.1]",
              8.0 * R * C + 8.0 * C, "GB/s", "hbm",
-             lambda: (up(normal(rng, R * C, 4.0)), up(u24(rng, C, 0.5, 1.5)), up(u24(rng, C, -0.1, 0.1)),
-                      kh.Buffer(4 * R * C)),
+             lambda: (normal(rng, R * C, 4.0), u24(rng, C, 0.5, 1.5), u24(rng, C, -0.1, 0.1)),
+             lambda h: (up(h[0]), up(h[1]), up(h[2]), out(R * C)),
              lambda s, st: kh.layernorm(s[0], s[1], s[2], s[3], R, C, st)))
 
-    ns = 1 << 26
-    T = kh.scan_workspace_floats(ns)
-    add(Case("scan", "inclusive n=2^26 fp32, x ~ U[0,1) on the 2^-24 grid", 8.0 * ns, "GB/s", "hbm",
-             lambda: (up(u24(rng, ns, 0, 1)), kh.Buffer(4 * ns), kh.Buffer(4 * T), kh.Buffer(4 * T)),
-             lambda s, st: kh.scan(s[0], s[1], None, s[2], s[3], ns, st)))
+    def scan_case(name, ns, label):
+        T = kh.scan_workspace_floats(ns)
+        return Case(name, f"inclusive n={label} fp32, x ~ U[0,1) on the 2^-24 grid", 8.0 * ns, "GB/s", "hbm",
+                    lambda: (u24(rng, ns, 0, 1),),
+                    lambda h: (up(h[0]), out(ns), out(T), out(T)),
+                    lambda s, st: kh.scan(s[0], s[1], None, s[2], s[3], ns, st))
 
-    ng = 1 << 26
-    add(Case("fused_gelu", "n=2^26 fp32, x ~ N(0,1); out = gelu_tanh(1.5x+0.5)", 8.0 * ng, "GB/s", "hbm",
-             lambda: (up(normal(rng, ng, 1.0)), kh.Buffer(4 * ng)),
-             lambda s, st: kh.fused_gelu(s[0], None, s[1], ng, st),
-             "reference formula counts 12 B/elem (metrics.cpp:36-38); 8 B/elem are moved"))
+    add(scan_case("scan", 1 << 26, "2^26"))
+    add(scan_case("scan_1e6", 1000000, "10^6"))
 
-    M = 8192
-    add(Case("gemm", "C=A*B fp32 row-major, m=n=k=8192, A,B ~ U[-1,1]", 2.0 * M * M * M, "TFLOP/s", "mfma",
-             lambda: (up(u24(rng, M * M, -1, 1)), up(u24(rng, M * M, -1, 1)), kh.Buffer(4 * M * M)),
-             lambda s, st: kh.gemm(s[0], s[1], s[2], M, M, M, st)))
+    def gelu_case(name, ng, label):
+        return Case(name, f"n={label} fp32, x ~ N(0,1); out = gelu_tanh(1.5x+0.5)", 8.0 * ng, "GB/s", "hbm",
+                    lambda: (normal(rng, ng, 1.0),),
+                    lambda h: (up(h[0]), out(ng)),
+                    lambda s, st: kh.fused_gelu(s[0], None, s[1], ng, st),
+                    "reference formula counts 12 B/elem (metrics.cpp:36-38); 8 B/elem are moved")
 
-    b, h, s_, d = 4, 16, 4096, 64
-    add(Case("attention", "non-causal b=4 h=16 s=4096 d=64 fp32, Q,K,V ~ N(0,1)", 4.0 * b * h * s_ * s_ * d,
-             "TFLOP/s", "mfma",
-             lambda: tuple(up(normal(rng, b * h * s_ * d, 1.0)) for _ in range(3)) + (kh.Buffer(4 * b * h * s_ * d),),
-             lambda s, st: kh.attention(s[0], s[1], s[2], s[3], b, h, s_, d, st)))
+    add(gelu_case("fused_gelu", 1 << 26, "2^26"))
+    add(gelu_case("fused_gelu_2^22", 1 << 22, "2^22"))
+
+    def gemm_case(name, m, nn, k):
+        return Case(name, f"C=A*B fp32 row-major, m={m} n={nn} k={k}, A,B ~ U[-1,1]", 2.0 * m * nn * k,
+                    "TFLOP/s", "mfma",
+                    lambda: (u24(rng, m * k, -1, 1), u24(rng, k * nn, -1, 1)),
+                    lambda h: (up(h[0]), up(h[1]), out(m * nn)),
+                    lambda s, st: kh.gemm(s[0], s[1], s[2], m, nn, k, st))
+
+    add(gemm_case("gemm", 8192, 8192, 8192))
+    add(gemm_case("gemm_512", 512, 512, 512))
+    add(gemm_case("gemm_2048", 2048, 2048, 2048))
+    add(gemm_case("gemm_8192x8192x256", 8192, 8192, 256))
+
+    def attention_case(name, b, h, s_, d=64):
+        e = b * h * s_ * d
+        return Case(name, f"non-causal b={b} h={h} s={s_} d={d} fp32, Q,K,V ~ N(0,1)", 4.0 * b * h * s_ * s_ * d,
+                    "TFLOP/s", "mfma",
+                    lambda: tuple(normal(rng, e, 1.0) for _ in range(3)),
+                    lambda hh: (up(hh[0]), up(hh[1]), up(hh[2]), out(e)),
+                    lambda s, st: kh.attention(s[0], s[1], s[2], s[3], b, h, s_, d, st))
+
+    add(attention_case("attention", 4, 16, 4096))
+    add(attention_case("attention_s1024", 4, 16, 1024))
     return cases
-
-
-def measure_ceilings(kh, stream, reps=5):
-    """Measured roofline denominators: triad and copy over 2^28 floats per
-    buffer (3 GiB / 2 GiB moved per launch, beyond the 256 MB MALL, as the
-    reference's roofline_triad, bench/harness/roofline.cpp:60-84) and the
-    fp32 MFMA microbenchmark (8 independent chains per wave, two waves per
-    SIMD, ~2 ms per launch: shorter launches under-measure it, as the clock
-    has not settled and launch gaps count)."""
-    n = 1 << 28
-    a, b, c = kh.Buffer(4 * n), kh.Buffer(4 * n), kh.Buffer(4 * n)
-    a.fill(1.0, stream)
-    b.fill(2.0, stream)
-    e0, e1 = kh.Event(), kh.Event()
-
-    def timed(fn):
-        fn()
-        stream.synchronize()
-        e0.record(stream)
-        for _ in range(reps):
-            fn()
-        e1.record(stream)
-        e1.synchronize()
-        return e0.elapsed_ms(e1) / reps
-
-    t_triad = timed(lambda: kh.roofline_triad(a, b, c, n, stream))
-    t_copy = timed(lambda: kh.roofline_copy(a, c, n, stream))
-    cu = kh.device_info()["cu_count"]
-    blocks, iters = cu * 2, 4096
-    out = kh.Buffer(4 * blocks * 256)
-    flops = float(blocks) * 4 * iters * 8 * 4096
-    t_mfma = timed(lambda: kh.roofline_mfma(out, blocks, iters, stream))
-    for buf in (a, b, c, out):
-        buf.free()
-    return {"hbm_triad_gbps": 12.0 * n / (t_triad * 1e-3) / 1e9,
-            "hbm_copy_gbps": 8.0 * n / (t_copy * 1e-3) / 1e9,
-            "fp32_mfma_tflops": flops / (t_mfma * 1e-3) / 1e12,
-            "triad_bytes_per_launch": 12 * n, "copy_bytes_per_launch": 8 * n,
-            "mfma_config": f"{blocks} workgroups x 4 waves x {iters} x 8 v_mfma_f32_32x32x2f32"}
 
 
 def available(kh, name):
     try:
-        kh.code_object(name)
+        kh.code_object(name.split("_")[0] if name.startswith(("gemm", "scan", "attention")) else
+                       "fused_gelu" if name.startswith("fused_gelu") else name)
         return True
     except kh.KhrtError:
         return False
@@ -172,53 +167,172 @@ def set_bytes(sets):
     return sum(b.nbytes for b in sets)
 
 
-def _gemm_rows_rate(O, A, B, M, threads, budget_s):
-    """Grows a row sample of the 8192^3 fp64 GEMM reference until it has run
-    for about budget_s seconds; returns (TFLOP/s, rows, seconds)."""
-    O.set_threads(threads)
-    done, dt, rows = 0, 0.0, max(threads, 2)
-    while dt < budget_s and done < M:
-        rows = min(rows, M - done)
+def rotation_count(bytes_per_set, cap=1024):
+    """Buffer sets it takes to exceed ROTATE_BYTES (at most cap)."""
+    return max(1, min(cap, -(-ROTATE_BYTES // max(1, int(bytes_per_set)))))
+
+
+def time_queued(kh, stream, launches, prime):
+    """Average GPU duration of `launches` (callables, issued back to back)
+    queued behind a ~0.35 ms copy, so the host has enqueued them all before
+    the first starts: microsecond kernels are timed at the GPU's rate, not
+    the host's submission rate."""
+    e0, e1 = kh.Event(), kh.Event()
+    kh.roofline_copy(prime[0], prime[1], prime[2], stream)
+    e0.record(stream)
+    for f in launches:
+        f()
+    e1.record(stream)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / len(launches)
+    e0.destroy()
+    e1.destroy()
+    return ms
+
+
+def measure_ceilings(kh, stream, hbm_cases, prime, steps):
+    """Measured roofline denominators.
+
+    HBM: plain copy (8 B/float) and triad (12 B/float) streams, the
+    reference's roofline_triad pattern (bench/refs/roofline.hip:22-30, 2^28
+    floats: 3 GiB per launch, beyond the 256 MB MALL) plus copies and triads
+    of exactly each HBM kernel's bytes per launch, rotated like that
+    kernel's buffers. Each runs under two geometries: the product streaming
+    kernels' (one unrolled step per thread, ceil(n/4/1024) workgroups of
+    256) and 32 grid-strided workgroups per CU. A kernel's ceiling is the
+    best of the 3 GiB streams and its own-size streams.
+
+    fp32 MFMA: 8 independent v_mfma_f32_32x32x2f32 chains per wave, two waves
+    per SIMD, ~2 ms per launch (shorter launches under-measure it, as the
+    clock has not settled and launch gaps count)."""
+    co = os.path.join(REPO, "kernel.h_amd", "build", "co", "roofline.hsaco")
+    with open(co, "rb") as f:
+        mod = kh.GpuModule(f.read())
+    fn = {"copy": mod.get_function("roofline_copy"), "triad": mod.get_function("roofline_triad")}
+    cu = kh.device_info()["cu_count"]
+
+    def grids(n):
+        return {"product": max(1, -(-(n // 4) // 1024)), "32/CU": 32 * cu}
+
+    def stream_rate(kind, n, sets, grid, reps):
+        def launch(bufs):
+            args = kh.LaunchArgs()
+            for b in bufs:
+                args.add_memref(b, [n])
+            return lambda: kh.launch_raw(fn[kind], (grid, 1, 1), (256, 1, 1), args, stream)
+        calls = [launch(sets[i % len(sets)]) for i in range(reps)]
+        calls[0]()
+        ms = time_queued(kh, stream, calls, prime)
+        return (12.0 if kind == "triad" else 8.0) * n / (ms * 1e-3) / 1e9
+
+    def streams(n, reps, rotate):
+        per = {"copy": 2, "triad": 3}
+        best, rows = 0.0, []
+        for kind in ("copy", "triad"):
+            nn = n["copy" if kind == "copy" else "triad"] if isinstance(n, dict) else n
+            nn = max(4, nn - nn % 4)
+            count = rotation_count(4 * nn * per[kind]) if rotate else 1
+            sets = [tuple(kh.Buffer(4 * nn) for _ in range(per[kind])) for _ in range(count)]
+            for s_ in sets:
+                s_[0].fill(1.0, stream)
+                if kind == "triad":
+                    s_[1].fill(2.0, stream)
+            for gname, g in grids(nn).items():
+                r = stream_rate(kind, nn, sets, g, reps)
+                rows.append({"kernel": kind, "floats": nn, "bytes": (12 if kind == "triad" else 8) * nn,
+                             "grid": gname, "buffer_sets": len(sets), "gbps": r})
+                best = max(best, r)
+            for s_ in sets:
+                for b in s_:
+                    b.free()
+        return best, rows
+
+    big_best, big_rows = streams(1 << 28, 5, rotate=False)
+    per_case = {}
+    for c in hbm_cases:
+        best, rows = streams({"copy": int(c.work // 8), "triad": int(c.work // 12)}, steps, rotate=True)
+        per_case[c.name] = {"gbps": max(big_best, best), "own_size_best": best, "streams": rows}
+
+    blocks, iters = cu * 2, 4096
+    out = kh.Buffer(4 * blocks * 256)
+    flops = float(blocks) * 4 * iters * 8 * 4096
+    kh.roofline_mfma(out, blocks, iters, stream)
+    t_mfma = time_queued(kh, stream, [lambda: kh.roofline_mfma(out, blocks, iters, stream)] * 5, prime)
+    out.free()
+    return {"hbm_3GiB_best_gbps": big_best, "hbm_3GiB_streams": big_rows, "hbm_per_kernel": per_case,
+            "fp32_mfma_tflops": flops / (t_mfma * 1e-3) / 1e12,
+            "mfma_config": f"{blocks} workgroups x 4 waves x {iters} x 8 v_mfma_f32_32x32x2f32"}
+
+
+def _median_runs(fn, runs=3, long_s=10.0):
+    """Median of `runs` timed calls of fn() (seconds), or the first alone
+    when it ran longer than long_s."""
+    times = []
+    for _ in range(runs):
         t = time.perf_counter()
-        O.ref_gemm(A, B, M, M, M, row0=done, nrows=rows)
-        dt += time.perf_counter() - t
-        done += rows
-        rows = max(rows, int(rows * min(4.0, 0.9 * (budget_s - dt) / max(time.perf_counter() - t, 1e-3))))
-    return 2.0 * done * M * M / dt / 1e12, done, dt
+        fn()
+        times.append(time.perf_counter() - t)
+        if times[0] > long_s:
+            break
+    return float(np.median(times)), len(times)
 
 
 def cpu_baseline(budget_s: float):
     """The oracle's fp64 references (CPU restatements of the reference's
-    e2e checks) timed on this host: the GEMM reference (e2e_gemm_test.cpp:
-    92-110) on a row sample of the 8192^3 problem on all cores via OpenMP
-    (the headline, in `value`'s unit) and on one core, plus all-core rates
-    of the softmax and scan references at the BASELINE sizes."""
+    e2e checks) timed on this host, built for its widest x86-64 level (the
+    stand-in for -march=native). Each rate is the median of 3 runs (1 when a
+    run exceeds 10 s): the GEMM reference (e2e_gemm_test.cpp:92-110) on a row
+    sample of the 8192^3 problem on all cores via OpenMP (the headline, in
+    `value`'s unit) and on one core; the softmax reference on all cores and
+    one core; the scan prefix (serial) on one core."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle as O
+    isa = O.host_isa()
+    O.use_isa(isa)
     cores = len(os.sched_getaffinity(0))
     M = 8192
     rng = np.random.default_rng(7)
     A = u24(rng, M * M, -1, 1)
     B = u24(rng, M * M, -1, 1)
-    tf_all, rows_all, s_all = _gemm_rows_rate(O, A, B, M, cores, 0.6 * budget_s)
-    tf_one, rows_one, s_one = _gemm_rows_rate(O, A, B, M, 1, 0.25 * budget_s)
+
+    def gemm_rate(threads, share):
+        # Size the row sample so that one run takes about share * budget / 3.
+        O.set_threads(threads)
+        target = share * budget_s / 3
+        rows = max(threads, 2)
+        while True:
+            t = time.perf_counter()
+            O.ref_gemm(A, B, M, M, M, row0=0, nrows=rows)
+            dt = time.perf_counter() - t
+            if dt >= 0.05 or rows >= M:
+                break
+            rows = min(M, rows * 4)
+        rows = int(min(M, max(threads, rows * target / dt)))
+        med, k = _median_runs(lambda: O.ref_gemm(A, B, M, M, M, row0=0, nrows=rows))
+        return 2.0 * rows * M * M / med / 1e12, rows, med, k
+
+    tf_all, rows_all, s_all, k_all = gemm_rate(cores, 0.5)
+    tf_one, rows_one, s_one, k_one = gemm_rate(1, 0.3)
     del A, B
-    O.set_threads(cores)
     x = (rng.standard_normal(4096 * 1024) * 4.0).astype(np.float32)
-    t = time.perf_counter()
-    O.ref_softmax(x, 4096, 1024)
-    sm = 8.0 * x.size / (time.perf_counter() - t) / 1e9
+    O.set_threads(cores)
+    sm_all, _ = _median_runs(lambda: O.ref_softmax(x, 4096, 1024))
+    O.set_threads(1)
+    sm_one, _ = _median_runs(lambda: O.ref_softmax(x, 4096, 1024))
     xs = u24(rng, 1 << 26, 0, 1)
-    t = time.perf_counter()
-    O.ref_scan(xs)
-    sc = 8.0 * xs.size / (time.perf_counter() - t) / 1e9
+    sc_one, _ = _median_runs(lambda: O.ref_scan(xs))
+    O.set_threads(cores)
     return {"value": tf_all, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"fp64 rank-1 GEMM reference (oracle kho_ref_gemm): {rows_all} of 8192 rows of the "
-                      f"8192^3 problem in {s_all:.1f} s on {cores} threads",
+            "sample": f"fp64 rank-1 GEMM reference (oracle kho_ref_gemm, built for {isa}): rows 0..{rows_all} of "
+                      f"the 8192^3 problem on {cores} threads, median of {k_all} runs of {s_all:.2f} s",
             "single_thread": {"value": tf_one, "unit": "TFLOP/s", "cores": 1,
-                              "sample": f"{rows_one} rows in {s_one:.1f} s"},
-            "other_kernels": {"softmax_4096x1024_gbps": sm, "scan_2^26_gbps_single_thread": sc,
-                              "note": "fp64 references, same inputs as the GPU rows; scan is serial"}}
+                              "sample": f"{rows_one} rows, median of {k_one} runs of {s_one:.2f} s"},
+            "other_kernels": {"softmax_4096x1024_gbps": {"all_cores": 8.0 * x.size / sm_all / 1e9,
+                                                         "single_thread": 8.0 * x.size / sm_one / 1e9},
+                              "scan_2^26_gbps_single_thread": 8.0 * xs.size / sc_one / 1e9,
+                              "note": "fp64 references, same input distributions as the GPU rows; the scan "
+                                      "prefix is serial; medians of 3 runs"},
+            "isa": isa}
 
 
 def main() -> int:
@@ -228,7 +342,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--kernels", default="", help="comma list to restrict the suite")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-rotate", action="store_true", help="reuse one buffer set (cache-warm)")
     ap.add_argument("--no-ceilings", action="store_true", help="skip the measured roofline microbenchmarks")
     a = ap.parse_args()
@@ -247,10 +361,10 @@ def main() -> int:
     stream = kh.Stream()
 
     for c in cases:
-        c.sets = [c.setup()]
-        if not a.no_rotate:
-            while set_bytes([b for s in c.sets for b in s]) < ROTATE_BYTES and len(c.sets) < 64:
-                c.sets.append(c.setup())
+        h = c.host()
+        first = c.device(h)
+        count = 1 if a.no_rotate else rotation_count(set_bytes(first))
+        c.sets = [first] + [c.device(h) for _ in range(count - 1)]
         log(f"[bench] {c.name}: {len(c.sets)} buffer set(s), "
             f"{set_bytes([b for s in c.sets for b in s]) / 2**20:.0f} MiB")
 
@@ -284,27 +398,20 @@ def main() -> int:
 
     # GPU-side launch duration: the same K back-to-back launches, queued
     # behind a ~0.35 ms copy so that the host has enqueued them all before
-    # the first one starts. Microsecond-scale kernels are otherwise timed at
-    # the host's submission rate (Python + launch API), not the GPU's.
+    # the first one starts.
     prime_n = 1 << 27
-    pa, pb = kh.Buffer(4 * prime_n), kh.Buffer(4 * prime_n)
+    prime = (kh.Buffer(4 * prime_n), kh.Buffer(4 * prime_n), prime_n)
     for c in cases:
-        e0, e1 = ev[c.name]
-        kh.roofline_copy(pa, pb, prime_n, stream)
-        e0.record(stream)
-        for i in range(a.steps):
-            c.launch(c.sets[(a.warmup + i) % len(c.sets)], stream)
-        e1.record(stream)
-        e1.synchronize()
-        c.ms = [e0.elapsed_ms(e1) / a.steps]
-    pa.free()
-    pb.free()
+        c.ms = [time_queued(kh, stream, [lambda c=c, i=i: c.launch(c.sets[(a.warmup + i) % len(c.sets)], stream)
+                                         for i in range(a.steps)], prime)]
 
     ceilings = None
     if not a.no_ceilings:
-        ceilings = measure_ceilings(kh, stream)
-        log(f"[bench] measured ceilings: triad {ceilings['hbm_triad_gbps']:.0f} GB/s, copy "
-            f"{ceilings['hbm_copy_gbps']:.0f} GB/s, fp32 MFMA {ceilings['fp32_mfma_tflops']:.1f} TFLOP/s")
+        ceilings = measure_ceilings(kh, stream, [c for c in cases if c.bound == "hbm"], prime, a.steps)
+        log(f"[bench] measured ceilings: HBM streams at 3 GiB {ceilings['hbm_3GiB_best_gbps']:.0f} GB/s, "
+            f"fp32 MFMA {ceilings['fp32_mfma_tflops']:.1f} TFLOP/s")
+    prime[0].free()
+    prime[1].free()
 
     kernels = {}
     for c in cases:
@@ -312,20 +419,28 @@ def main() -> int:
         rate = c.work / (ms * 1e-3) / (1e12 if c.unit == "TFLOP/s" else 1e9)
         peak = FP32_MFMA_PEAK_TFLOPS if c.bound == "mfma" else HBM_PEAK_GBPS
         rate_host = c.work / (c.ms_host * 1e-3) / (1e12 if c.unit == "TFLOP/s" else 1e9)
-        kernels[c.name] = {"config": c.config, "ms_mean": ms, "ms_host_paced": c.ms_host,
-                           "rate": rate, "rate_host_paced": rate_host, "unit": c.unit,
-                           "bound": c.bound, "peak": peak, "frac": rate / peak,
-                           "algorithmic_work_per_launch": c.work, "buffer_sets": len(c.sets)}
+        k = {"config": c.config, "ms_mean": ms, "ms_host_paced": c.ms_host,
+             "rate": rate, "rate_host_paced": rate_host, "unit": c.unit,
+             "bound": c.bound, "peak": peak, "frac": rate / peak,
+             "algorithmic_work_per_launch": c.work, "buffer_sets": len(c.sets)}
         if ceilings:
-            meas = ceilings["fp32_mfma_tflops"] if c.bound == "mfma" else ceilings["hbm_triad_gbps"]
-            kernels[c.name]["measured_ceiling"] = meas
-            kernels[c.name]["frac_of_measured"] = rate / meas
+            if c.bound == "mfma":
+                k["measured_ceiling"] = ceilings["fp32_mfma_tflops"]
+                k["measured_ceiling_source"] = "fp32 MFMA microbenchmark"
+            else:
+                pc = ceilings["hbm_per_kernel"][c.name]
+                k["measured_ceiling"] = pc["gbps"]
+                k["measured_ceiling_source"] = ("best of copy/triad streams at 3 GiB and at this kernel's "
+                                                f"{int(c.work)} B per launch (own size best {pc['own_size_best']:.0f})")
+            k["frac_of_measured"] = rate / k["measured_ceiling"]
         if c.name in PMC_TRAFFIC_BYTES:
-            kernels[c.name]["traffic_bytes_pmc"] = PMC_TRAFFIC_BYTES[c.name]
-        if c.traffic_note:
-            kernels[c.name]["note"] = c.traffic_note
-        log(f"[bench] {c.name:10s} {ms:9.4f} ms  {rate:9.1f} {c.unit}  ({100 * rate / peak:5.1f}% of peak"
-            + (f", {100 * kernels[c.name]['frac_of_measured']:5.1f}% of measured)" if ceilings else ")"))
+            k["traffic_bytes_pmc"] = PMC_TRAFFIC_BYTES[c.name]
+            k["traffic_source"] = PMC_TRAFFIC_SOURCE
+        if c.note:
+            k["note"] = c.note
+        kernels[c.name] = k
+        log(f"[bench] {c.name:20s} {ms:9.4f} ms  {rate:9.1f} {c.unit}  ({100 * rate / peak:5.1f}% of peak"
+            + (f", {100 * k['frac_of_measured']:5.1f}% of measured)" if ceilings else ")"))
 
     head = "gemm" if "gemm" in kernels else (cases[0].name if cases else None)
     hk = kernels.get(head, {})
@@ -337,15 +452,17 @@ def main() -> int:
         "ms_per_step": wall * 1e3 / max(1, a.steps),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
-        "config": {"workload": f"kernel.h seven templates at BASELINE sizes; value = {head} "
+        "config": {"workload": f"kernel.h seven templates at all 13 BASELINE configurations; value = {head} "
                                "(gemm m=n=k=8192 fp32); per-kernel rates under 'kernels'",
-                   "gemm": "m=n=k=8192", "softmax": "rows=4096,cols=1024", "scan": "n=2^26",
-                   "vecadd": "n=2^24", "layernorm": "rows=4096,cols=1024", "fused_gelu": "n=2^26",
-                   "attention": "batch=4,heads=16,seq=4096,head_dim=64",
+                   "gemm": "m=n=k=8192; also 512^3, 2048^3, 8192x8192x256",
+                   "softmax": "rows=4096,cols=1024", "scan": "n=2^26; also 10^6",
+                   "vecadd": "n=2^24", "layernorm": "rows=4096,cols=1024", "fused_gelu": "n=2^26; also 2^22",
+                   "attention": "batch=4,heads=16,head_dim=64, seq=4096; also 1024",
                    "buffer_rotation": not a.no_rotate},
         "roofline": None if not hk else {
             "bound": hk["bound"], "achieved": hk["rate"], "peak": hk["peak"],
-            "unit": hk["unit"], "frac": hk["frac"], "traffic": PMC_TRAFFIC_BYTES.get(head), "kernel": head},
+            "unit": hk["unit"], "frac": hk["frac"], "traffic": PMC_TRAFFIC_BYTES.get(head), "kernel": head,
+            "traffic_source": PMC_TRAFFIC_SOURCE if head in PMC_TRAFFIC_BYTES else None},
         "kernels": kernels,
         "measured_ceilings": ceilings,
         "device": {"name": info["name"], "arch": info["arch"], "cu_count": info["cu_count"]},

@@ -35,44 +35,52 @@
 // Look-back state lives in the caller's totals buffers (the reference ABI
 // has no separate workspace) and needs no clearing between calls:
 //
-//   totals_lo, from its first 8-byte boundary: a 40-byte Header
-//       counter  64-bit ticket counter; it only ever grows, across calls
-//       base     the counter value at the start of the current call: the
-//                ticket `base + i` is tile i
-//       nonce    device real-time clock when these buffers were first seen
-//       done     workgroups of the current call that have finished
-//       failed   bounded waits that ran out (diagnostic; y is NaN there)
+//   totals_lo, from its first 8-byte boundary: a 32-byte Header, read by
+//   every workgroup at its start,
+//       base     low 32 bits: the call's first ticket (ticket base + i is
+//                tile i); high 32 bits: the call's generation
+//       nonce    device real-time clock when the session began
 //       check    mix(base, nonce, header address): the header is recognised
-//                only when it matches
-//   totals_hi, from its first 8-byte boundary: one 24-byte Record per tile
-//       0 .. ntiles-2 (the last tile has no successor): {aggregate,
-//       inclusive prefix, check}, the values as fp64 bit patterns. Once the
-//       aggregate is out, check = aggregate ^ tag_agg(t); once the inclusive
-//       prefix is out, check = aggregate ^ inclusive ^ tag_inc(t), where t is
-//       the tile's absolute ticket and the tags derive from a session key.
+//                only when it matches (and the tickets handed out fit it)
+//       failed   bounded waits that ran out (diagnostic; y is NaN there)
+//   and 16 B of Counters, updated by every workgroup with atomics, 256 B
+//   further on where totals_lo has room (another cache line), else right
+//   after the header:
+//       counter  32-bit ticket counter, continuing across calls
+//       done     workgroups of the current call that have taken their last
+//                ticket, and the tickets they took
+//   totals_hi, from its first 8-byte boundary: one 16-byte Record per tile
+//       0 .. ntiles-2 (the last tile has no successor): {value, check}, the
+//       value an fp64 bit pattern. First the tile's aggregate with
+//       check = value ^ tag_agg(t), then its inclusive prefix (overwriting
+//       it) with check = value ^ tag_inc(t), where t = (generation << 32) |
+//       tile and the tags derive from a session key.
 //
-// A value counts as published only when the record's words satisfy one of
-// those equations for this call's ticket of that tile. Tickets are never
-// reused on one header and the session key differs per header address and
-// per nonce, so stale records of earlier calls, zero-filled or NaN-filled
-// memory and leftovers of other kernels all read as "not yet published" (a
-// random 64-bit match is the only way through). The words are separate
-// relaxed atomics; a reader that sees some new and some old words sees a
-// mismatch and polls again. They are written and polled with relaxed
-// agent-scope atomics (coherent across the 8 XCD L2s without the L2
-// write-back/invalidate an acquire/release pair would cost on every poll).
+// A value counts as published only when the record's two words satisfy one
+// of those equations for this call's generation and tile. Generations never
+// repeat within a session (2^32 calls) and the session key differs per
+// header address and per nonce, so stale records of earlier calls, zero- or
+// NaN-filled memory and leftovers of other kernels all read as "not yet
+// published" (a random 64-bit match is the only way through). A record
+// moves as one 16-byte access with the sc1 cache policy (agent scope,
+// coherent across the 8 XCD L2s without the L2 write-back/invalidate an
+// acquire/release pair would cost on every poll); such an access is not
+// guaranteed single-copy atomic, and a torn read simply fails the check and
+// is polled again.
 //
 // Calls that run one after another on the same buffers (stream order) need
-// nothing from the host: the last workgroup of a call to finish sets
-// base := counter and re-signs the header for the next call. A header that
-// is not recognised (fresh, zeroed, garbage) is claimed by one workgroup with
-// a compare-and-swap; it starts a new session (base := counter, nonce := the
-// real-time clock) while the others wait for the signature. Tickets taken
-// before that point are told apart by base and taken again. Two calls that
-// overlap in time on the same totals buffers race (as with any shared
-// output buffer); calls on different buffers are independent.
+// nothing from the host: the last workgroup of a call to count itself done
+// moves the first ticket on by the call's tickets (the counter's value),
+// adds one to the generation and re-signs the header for the next call. A
+// header that is not recognised (fresh, zeroed, garbage, or with a counter
+// another kernel wrote) is claimed by one workgroup with a compare-and-swap;
+// it starts a new session (first ticket := counter, nonce := the real-time
+// clock) while the others wait for the signature. Tickets taken before that
+// point are told apart and taken again. Two calls that overlap in time on
+// the same totals buffers race (as with any shared output buffer); calls on
+// different buffers are independent.
 //
-// Capacity: 40 B (+4 for alignment) of totals_lo and 24 B per tile but one
+// Capacity: 48 B (+4 for alignment) of totals_lo and 16 B per tile but one
 // (+4) of totals_hi, both with unit stride; the reference's T = ceil(n/256)
 // floats always suffice (a tile is at least 3072 elements, 48 B of T).
 // Anything else is refused by writing NaN to y without touching the totals.
@@ -95,17 +103,34 @@ constexpr int kWindow = KH_SCAN_WINDOW;  // predecessors polled per lane per loo
 constexpr uint32_t kSpinLimit = 1u << 22;
 constexpr uint64_t kEmpty = ~0ull;
 
+// The header proper, read by every workgroup at its start, and the two
+// words every workgroup updates with atomics (Counters). Where totals_lo has
+// room, Counters sit 256 B past the header, in another cache line, so the
+// header loads do not queue behind the ticket atomics; otherwise right
+// after it.
 struct Header {
-  uint64_t counter, base, nonce;
-  uint32_t done, failed;
-  uint64_t check;
+  uint64_t base;  // low 32 bits: the call's first ticket; high 32: its generation
+  uint64_t nonce, check;
+  uint32_t failed, pad;
 };
-static_assert(sizeof(Header) == 40, "header layout");
+struct Counters {
+  uint32_t counter, pad;  // tickets, mod 2^32 (a call takes far fewer)
+  uint64_t done;          // low 32 bits: workgroups done; high 32: their tickets
+};
+static_assert(sizeof(Header) == 32 && sizeof(Counters) == 16, "header layout");
+constexpr int64_t kCountersApart = 256;  // bytes from the header, when there is room
+
+__device__ __forceinline__ Counters *counters_of(Header *h, int64_t bytes) {
+  char *p = reinterpret_cast<char *>(h);
+  return reinterpret_cast<Counters *>(p + (bytes >= kCountersApart + (int64_t)sizeof(Counters)
+                                               ? kCountersApart
+                                               : (int64_t)sizeof(Header)));
+}
 
 struct Record {
-  uint64_t agg, inc, check;
+  uint64_t value, check;
 };
-static_assert(sizeof(Record) == 24, "record layout");
+static_assert(sizeof(Record) == 16, "record layout");
 
 // Stafford's mix13 finaliser of SplitMix64: a bijection of 64-bit words.
 __device__ __forceinline__ uint64_t mix64(uint64_t z) {
@@ -130,12 +155,15 @@ __device__ __forceinline__ uint64_t claim_mark(const Header *h) {
   return nonzero(mix64(reinterpret_cast<uintptr_t>(h) ^ 0xc1a1bedc1a1bedull));
 }
 
-// Record tags of the tile with absolute ticket t: a session key XOR t. An
-// aggregate-only record has check = agg ^ agg_tag, a complete one
-// check = agg ^ inc ^ inc_tag. Within a session, distinct t give distinct
-// tags; the two kinds use unrelated keys, and a record written under
-// another session (or never written) passes only if its words happen to XOR
-// to a value fixed by unrelated mix64 outputs.
+// Record tags of tile i of the call with generation g: a session key XOR
+// t = (g << 32) | i, one key per kind of value. A record holds the tile's
+// aggregate with check = value ^ agg_tag, and later its inclusive prefix
+// (overwriting it) with check = value ^ inc_tag. Within a session (the
+// generation counts its calls), distinct t give distinct tags; the two kinds use unrelated keys, and a record written under another
+// session (or never written) passes only if its words happen to XOR to a
+// value fixed by unrelated mix64 outputs. A read torn between the two words
+// of one publication passes only when both values are equal (and then it
+// reads that value correctly).
 struct Keys {
   uint64_t agg, inc;
 };
@@ -161,28 +189,41 @@ __device__ __forceinline__ T fetch_add(T *p, T v) {
 
 __device__ __forceinline__ uint64_t bits(double v) { return (uint64_t)__double_as_longlong(v); }
 
-// Publishes the aggregate of tile t (absolute ticket).
-__device__ __forceinline__ void publish_aggregate(Record *r, const Keys &k, uint64_t t, double agg) {
-  st(&r->agg, bits(agg));
-  st(&r->check, bits(agg) ^ tag(k.agg, t));
+// Records move as one 16-byte buffer access each, with the sc1 cache policy
+// (agent scope, coherent across the XCDs' L2s: the bits relaxed agent-scope
+// atomics carry). Such an access is not guaranteed to be single-copy atomic;
+// a torn one fails the check and is polled again.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kSc1 = 16;  // cache-policy operand of the buffer builtins: sc1
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t record_rsrc(const Record *r) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<Record *>(r), (short)0, 0x7fffffff, 0x00020000);
 }
 
-// Publishes the inclusive prefix of tile t, whose aggregate is agg (written
-// again here: tile 0 publishes both at once).
-__device__ __forceinline__ void publish_inclusive(Record *r, const Keys &k, uint64_t t, double agg, double inc) {
-  st(&r->agg, bits(agg));
-  st(&r->inc, bits(inc));
-  st(&r->check, bits(agg) ^ bits(inc) ^ tag(k.inc, t));
+// Publishes one value of tile t (absolute ticket): its aggregate (key
+// keys.agg) or its inclusive prefix (key keys.inc, replacing the aggregate).
+__device__ __forceinline__ void publish(Record *r, uint64_t key, uint64_t t, double v) {
+  const uint64_t b = bits(v), c = b ^ tag(key, t);
+  const u32x4 w = {(unsigned)b, (unsigned)(b >> 32), (unsigned)c, (unsigned)(c >> 32)};
+  __builtin_amdgcn_raw_buffer_store_b128(w, record_rsrc(r), 0, 0, kSc1);
 }
 
-// The call's view of the state: where it is, the ticket of tile 0 and the
-// session key the record tags derive from.
+// The call's view of the state: where it is, the ticket of tile 0 (low 32
+// bits of `base`) and the generation (high 32), and the session keys the
+// record tags derive from.
 struct Session {
   Header *h;
+  Counters *c;
   Record *rec;
   uint64_t base;
   Keys keys;
 };
+
+__device__ __forceinline__ uint32_t first_ticket(uint64_t base) { return (uint32_t)base; }
+// Tag input of tile i: (generation << 32) | i.
+__device__ __forceinline__ uint64_t tag_of(uint64_t base, int64_t tile) {
+  return (base & 0xffffffff00000000ull) | (uint32_t)tile;
+}
 
 // Run by one thread per workgroup at the start of a multi-tile call. Takes
 // the workgroup's first two tickets (t0 < t1, both >= base) and the
@@ -190,43 +231,53 @@ struct Session {
 // wait. The header loads and the ticket atomics go out together, so a
 // recognised header costs one round trip.
 struct Opened {
-  uint64_t base, nonce, t0, t1;
+  uint64_t base, nonce;
+  uint32_t t0, t1;
   bool ok;
 };
 
-__device__ __forceinline__ Opened open_session(Header *h) {
+__device__ __forceinline__ Opened open_session(Header *h, Counters *c, int64_t ntiles) {
   Opened o;
   o.ok = true;
   o.base = ld(&h->base);
   o.nonce = ld(&h->nonce);
-  uint64_t seen = ld(&h->check);
-  o.t0 = fetch_add(&h->counter, uint64_t(1));
-  o.t1 = fetch_add(&h->counter, uint64_t(1));
+  const uint64_t seen0 = ld(&h->check);
+  o.t0 = fetch_add(&c->counter, 1u);
+  o.t1 = fetch_add(&c->counter, 1u);
+  // A call takes every ticket below ntiles once and at most two more per
+  // workgroup, all >= base: a ticket outside that range means the counter
+  // was changed behind the header's back (another kernel wrote it), and the
+  // header is not taken as valid even though its check matches.
+  const uint64_t span = (uint64_t)ntiles + 2ull * gridDim.x * gridDim.y * gridDim.z + 4;
+  const bool signed0 = seen0 == header_check(h, o.base, o.nonce);
+  const bool in_range = (uint32_t)(o.t1 - first_ticket(o.base)) < span;
   // Valid: the header is stable for the whole call (only the last workgroup
   // to finish changes it), so the three words belong together.
-  if (seen == header_check(h, o.base, o.nonce)) return o;
+  if (signed0 && in_range) return o;
   // Not recognised (or read while a claimant was writing it). `check` is
   // read with acquire ordering before base and nonce: when it is a
   // claimant's signature, the base and nonce read after it are the ones it
-  // signs. A workgroup claims the header only from an unsigned check value,
-  // with a compare-and-swap, so exactly one claims it; the others wait for
-  // the signature.
+  // signs. A workgroup claims the header only from a check value that is
+  // unsigned (or the signature found with an inconsistent counter), with a
+  // compare-and-swap, so exactly one claims it; the others wait for the new
+  // signature.
   const uint64_t mark = claim_mark(h);
   for (uint32_t spins = 0;; ++spins) {
-    seen = __hip_atomic_load(&h->check, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t seen = __hip_atomic_load(&h->check, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
     o.base = ld(&h->base);
     o.nonce = ld(&h->nonce);
-    if (seen == header_check(h, o.base, o.nonce)) break;
+    if (seen == header_check(h, o.base, o.nonce) && !(signed0 && seen == seen0)) break;
     uint64_t expect = seen;
     if (seen != mark && __hip_atomic_compare_exchange_strong(&h->check, &expect, mark, __ATOMIC_RELAXED,
                                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-      // A read-modify-write, so every ticket before it is < base and every
-      // ticket after it >= base.
-      o.base = fetch_add(&h->counter, uint64_t(0));
+      // A read-modify-write, so every ticket before it precedes the
+      // session's first ticket and every ticket after it follows. The
+      // generation may start anywhere: the session key carries the nonce.
       o.nonce = __builtin_amdgcn_s_memrealtime();
+      o.base = ((uint64_t)(uint32_t)o.nonce << 32) | fetch_add(&c->counter, 0u);
       st(&h->base, o.base);
       st(&h->nonce, o.nonce);
-      st(&h->done, 0u);
+      st(&c->done, uint64_t(0));
       st(&h->failed, 0u);
       __hip_atomic_store(&h->check, header_check(h, o.base, o.nonce), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
       break;
@@ -243,25 +294,38 @@ __device__ __forceinline__ Opened open_session(Header *h) {
     __builtin_amdgcn_s_sleep(2);
   }
   // Tickets taken before the session began are not tiles of this call.
-  if ((int64_t)(o.t1 - o.base) < 0) {
-    o.t0 = fetch_add(&h->counter, uint64_t(1));
-    o.t1 = fetch_add(&h->counter, uint64_t(1));
-  } else if ((int64_t)(o.t0 - o.base) < 0) {
+  if ((int32_t)(o.t1 - first_ticket(o.base)) < 0) {
+    o.t0 = fetch_add(&c->counter, 1u);
+    o.t1 = fetch_add(&c->counter, 1u);
+  } else if ((int32_t)(o.t0 - first_ticket(o.base)) < 0) {
     o.t0 = o.t1;
-    o.t1 = fetch_add(&h->counter, uint64_t(1));
+    o.t1 = fetch_add(&c->counter, 1u);
   }
   return o;
 }
 
-// Run by one thread per workgroup after its last ticket has returned. The
-// last workgroup of the call re-signs the header with base := counter, which
-// is the first ticket the next call will see.
-__device__ __forceinline__ void close_session(Header *h, uint64_t nonce) {
-  const uint32_t blocks = gridDim.x * gridDim.y * gridDim.z;
-  if (fetch_add(&h->done, 1u) != blocks - 1) return;
-  const uint64_t next = fetch_add(&h->counter, uint64_t(0));
+// Counts a workgroup as finished with the call's tickets, adding the
+// number it took (`tickets`: its first two plus one per tile-loop step that
+// took one, all >= base). Issued by one thread as soon as the workgroup's
+// last ticket has come back (one at or past the last tile).
+__device__ __forceinline__ uint64_t count_done(Counters *c, uint32_t tickets) {
+  return fetch_add(&c->done, ((uint64_t)tickets << 32) | 1u);
+}
+
+// Run when the workgroup ends, with count_done's result. The last workgroup
+// of the call to count itself (every ticket of the call has then come back)
+// re-signs the header for the next call: its first ticket is this call's
+// plus all the tickets of this call (the counter's value), its generation
+// one more.
+__device__ __forceinline__ void close_session(Header *h, Counters *c, uint64_t base, uint64_t nonce,
+                                              uint64_t done_before,
+                                              uint32_t tickets) {
+  if ((uint32_t)done_before != gridDim.x * gridDim.y * gridDim.z - 1) return;
+  const uint32_t next_ticket = first_ticket(base) + (uint32_t)(done_before >> 32) + tickets;
+  const uint64_t next = ((base & 0xffffffff00000000ull) + (1ull << 32)) | next_ticket;
+  st(&c->counter, next_ticket);  // already its value, unless something else wrote it
   st(&h->base, next);
-  st(&h->done, 0u);
+  st(&c->done, uint64_t(0));
   st(&h->check, header_check(h, next, nonce));
 }
 
@@ -318,14 +382,17 @@ constexpr int kRows = kPerThread / 4;
 static_assert(kPerThread % 4 == 0, "rows of float4");
 constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor: 32-bit data format
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const float *base, int64_t elems) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, (int)(elems * 4), kRsrcWord3);
 }
 
+// The dword path passes `lane` through an empty asm, so that its sixteen
+// per-dword offsets are computed where the accesses are issued instead of
+// being hoisted out of the tile loop, where they would hold sixteen
+// registers for its whole length (a 1024-thread workgroup has 128).
 template <bool VEC>
 __device__ __forceinline__ void load_seg(float (&v)[kPerThread], __amdgpu_buffer_rsrc_t r, int seg, int lane) {
+  if (!VEC) asm volatile("" : "+v"(lane));
 #pragma unroll
   for (int k = 0; k < kRows; ++k) {
     const int e = seg + 256 * k + 4 * lane;
@@ -343,6 +410,7 @@ __device__ __forceinline__ void load_seg(float (&v)[kPerThread], __amdgpu_buffer
 template <bool VEC>
 __device__ __forceinline__ void store_seg(const float (&o)[kPerThread], __amdgpu_buffer_rsrc_t r, int seg,
                                           int lane) {
+  if (!VEC) asm volatile("" : "+v"(lane));
 #pragma unroll
   for (int k = 0; k < kRows; ++k) {
     const int e = seg + 256 * k + 4 * lane;
@@ -359,63 +427,74 @@ __device__ __forceinline__ void store_seg(const float (&o)[kPerThread], __amdgpu
 }
 
 // One look-back window: predecessors end, end-1, ..., end - 64 kWindow + 1;
-// lane l, slot j holds distance d = l + 64 j behind `end`. Unpublished
-// values read as kEmpty (never an fp64 sum of fp32 inputs: those keep the
-// low 29 mantissa bits of every operand clear, and fp64 addition yields only
-// canonical or propagated NaNs). Slots before tile 0 act as an inclusive
-// prefix of value 0.
+// lane l, slot j holds distance d = l + 64 j behind `end`. A poll only
+// issues the loads of the records' two words; `decode` reads them (waiting
+// for the loads there, not at the poll), so the first poll of a look-back
+// can be issued before a barrier and land while the workgroup works.
 struct Window {
-  uint64_t inc[kWindow], ag[kWindow];
+  uint64_t value[kWindow], chk[kWindow];
 };
 
 __device__ __forceinline__ void poll_window(Window &w, const Session &s, int64_t end, int lane) {
   // Byte offsets of the records from the (wave-uniform) record base: 32-bit,
-  // as no device holds 2^32 B of records (that would be 2^27 tiles).
-  uint64_t ag[kWindow], inc[kWindow], chk[kWindow];
+  // as no device holds 2^32 B of records (that would be 2^28 tiles).
 #pragma unroll
   for (int j = 0; j < kWindow; ++j) {
     const int64_t idx = end - lane - kh::kWave * j;
-    const Record *r = reinterpret_cast<const Record *>(reinterpret_cast<const char *>(s.rec) +
-                                                       (uint32_t)(idx >= 0 ? idx : 0) * (uint32_t)sizeof(Record));
-    ag[j] = ld(&r->agg);
-    inc[j] = ld(&r->inc);
-    chk[j] = ld(&r->check);
+    // The empty asm keeps a repeated poll of the same records from being
+    // merged with the previous one (the loads are not marked volatile).
+    uint32_t off = (uint32_t)(idx >= 0 ? idx : 0) * (uint32_t)sizeof(Record);
+    asm volatile("" : "+v"(off));
+    const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(record_rsrc(s.rec), off, 0, kSc1);
+    w.value[j] = ((uint64_t)q.y << 32) | q.x;
+    w.chk[j] = ((uint64_t)q.w << 32) | q.z;
   }
+}
+
+// Published values of a polled window, kEmpty where unpublished (never an
+// fp64 sum of fp32 inputs: those keep the low 29 mantissa bits of every
+// operand clear, and fp64 addition yields only canonical or propagated
+// NaNs). inc: the inclusive prefix where published; ag: the aggregate where
+// only that is. Slots before tile 0 act as an inclusive prefix of value 0.
+__device__ __forceinline__ void decode(const Window &w, const Session &s, int64_t end, int lane,
+                                       uint64_t (&inc)[kWindow], uint64_t (&ag)[kWindow]) {
 #pragma unroll
   for (int j = 0; j < kWindow; ++j) {
     const int64_t idx = end - lane - kh::kWave * j;
-    const uint64_t t = s.base + (uint64_t)idx;
+    const uint64_t t = tag_of(s.base, idx);
     const bool before = idx < 0;
-    const bool has_inc = (chk[j] ^ ag[j] ^ inc[j]) == tag(s.keys.inc, t);
-    const bool has_ag = has_inc || (chk[j] ^ ag[j]) == tag(s.keys.agg, t);
-    w.inc[j] = before ? 0ull : (has_inc ? inc[j] : kEmpty);
-    w.ag[j] = before ? kEmpty : (has_ag ? ag[j] : kEmpty);
+    const uint64_t x = w.chk[j] ^ w.value[j];
+    inc[j] = before ? 0ull : (x == tag(s.keys.inc, t) ? w.value[j] : kEmpty);
+    ag[j] = before ? kEmpty : (x == tag(s.keys.agg, t) ? w.value[j] : kEmpty);
   }
 }
 
 // Exclusive prefix of `tile` from its predecessors' published records (run
 // by one whole wave; the result is wave-uniform), starting from window `w`,
-// already polled for end = tile - 1. Records only ever go from unpublished to
-// their final value within a call, so an early poll is a valid (if possibly
-// incomplete) observation. NaN if the bounded wait ran out.
+// already polled for end = tile - 1. Records only ever go from unpublished
+// to aggregate to inclusive prefix within a call, so an early poll is a
+// valid (if possibly incomplete) observation. NaN if the bounded wait ran
+// out.
 __device__ __forceinline__ double look_back(const Session &s, int64_t tile, int lane, Window w) {
   double excl = 0.0;
   int64_t end = tile - 1;  // newest predecessor still to account for
   uint32_t spins = 0;
   for (;;) {
+    uint64_t inc[kWindow], ag[kWindow];
+    decode(w, s, end, lane, inc, ag);
     // Nearest inclusive prefix, and whether every nearer predecessor has at
     // least published its aggregate.
     int first = kWindow * kh::kWave;
 #pragma unroll
     for (int j = kWindow - 1; j >= 0; --j) {
-      const uint64_t m = __ballot(w.inc[j] != kEmpty);
+      const uint64_t m = __ballot(inc[j] != kEmpty);
       if (m) first = kh::kWave * j + __builtin_ctzll(m);
     }
     bool pending = false;
 #pragma unroll
     for (int j = 0; j < kWindow; ++j) {
       const int d = lane + kh::kWave * j;
-      if (d < first && w.ag[j] == kEmpty) pending = true;
+      if (d < first && ag[j] == kEmpty) pending = true;
     }
     if (__ballot(pending) != 0) {
       if (++spins > kSpinLimit) {
@@ -431,9 +510,9 @@ __device__ __forceinline__ double look_back(const Session &s, int64_t tile, int 
     for (int j = 0; j < kWindow; ++j) {
       const int d = lane + kh::kWave * j;
       if (d < first) {
-        contrib += __longlong_as_double((long long)w.ag[j]);
+        contrib += __longlong_as_double((long long)ag[j]);
       } else if (d == first) {
-        contrib += __longlong_as_double((long long)w.inc[j]);
+        contrib += __longlong_as_double((long long)inc[j]);
       }
     }
     excl += wave_sum_f64(contrib);
@@ -443,11 +522,11 @@ __device__ __forceinline__ double look_back(const Session &s, int64_t tile, int 
   }
 }
 
-// Tile index of an absolute ticket; tickets past the call's tiles map to
-// ntiles (the loop's end marker).
-__device__ __forceinline__ int64_t tile_of(uint64_t ticket, uint64_t base, int64_t ntiles) {
-  const uint64_t i = ticket - base;
-  return i < (uint64_t)ntiles ? (int64_t)i : ntiles;
+// Tile index of a ticket; tickets past the call's tiles map to ntiles (the
+// loop's end marker).
+__device__ __forceinline__ int64_t tile_of(uint32_t ticket, uint64_t base, int64_t ntiles) {
+  const uint32_t i = ticket - first_ticket(base);
+  return (int64_t)i < ntiles ? (int64_t)i : ntiles;
 }
 
 // The tile loop of one persistent workgroup, a three-stage pipeline. In
@@ -467,10 +546,16 @@ __device__ __forceinline__ int64_t tile_of(uint64_t ticket, uint64_t base, int64
 // Deadlock-free: the lowest tile in look-back only needs aggregates of lower
 // tiles, and each of those is either finished or in the reduce stage of a
 // workgroup that publishes it without waiting on anything.
+// The control wave takes the workgroup's tickets from the third on, so it
+// also counts the workgroup done (count_done), in the step after a ticket at
+// or past the last tile came back: its one atomic of a step then goes to
+// `done` instead of `counter`. The result lands in s_done[0], the
+// workgroup's ticket count in s_done[1], before that step's barrier B.
 template <bool VEC>
 __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *__restrict__ Y, const Session &ses,
                                            int64_t n, int64_t tr, int64_t tn, bool single, uint64_t *s_raw,
-                                           double *s_wave_total, double *s_prefix, double *s_off) {
+                                           double *s_wave_total, double *s_prefix, double *s_off,
+                                           uint64_t *s_done) {
   const int tid = threadIdx.x;
   const int lane = kh::lane_id();
   const int wave = tid / kh::kWave;
@@ -485,6 +570,11 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
   auto elems = [&](int64_t t) { return n - t * tile_elems < tile_elems ? n - t * tile_elems : tile_elems; };
 
   int64_t tc = -1;       // no tile to finish in the first iteration
+  // Tickets are taken until one comes back at or past the last tile (the
+  // starting pair included); uniform across the workgroup.
+  bool taking = !single && tn < ntiles;
+  bool counting = !single && !taking;  // count_done due in the next step
+  uint32_t tickets = 2;  // control wave, lane 0
   double agg_c = 0.0;    // control wave: aggregate of tile tc
   double wexcl_c = 0.0;  // data waves: sum of earlier waves' totals in tile tc
   int slot = 0;
@@ -494,6 +584,8 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
   // rotates the three register buffers instead of copying them.
   auto step = [&](float (&vc)[kPerThread], float (&vr)[kPerThread], float (&vn)[kPerThread])
       __attribute__((always_inline)) -> bool {
+    const bool take = taking, count = counting;
+    counting = false;
     // Defined only where it is used (control wave, lane 0): a default value
     // on the data path would be a register write that must wait for the
     // pending atomic, i.e. for all of that wave's outstanding memory ops.
@@ -504,7 +596,11 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
     // Defined on the control wave only, like `raw`.
     Window w;
     if (ctrl) {
-      if (lane == 0 && !single) raw = fetch_add(&ses.h->counter, uint64_t(1));
+      if (lane == 0 && (take || count)) {
+        // One atomic either way: the next ticket, or the done count.
+        raw = take ? (uint64_t)fetch_add(&ses.c->counter, 1u) : fetch_add(&ses.c->done, ((uint64_t)tickets << 32) | 1u);
+        tickets += take;
+      }
       if (tc > 0) poll_window(w, ses, tc - 1, lane);
     } else if (tr < ntiles) {
       // ---- reduce tile tr: per-row lane sums (fp64), wave scans, wave total ---
@@ -530,11 +626,7 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
       if (tr < ntiles) {
         agg_r = wave_sum_f64(lane < ndata ? s_wave_total[lane] : 0.0);
         if (!single && lane == 0 && tr < ntiles - 1) {
-          Record *r = ses.rec + tr;
-          if (tr == 0)
-            publish_inclusive(r, ses.keys, ses.base, agg_r, agg_r);
-          else
-            publish_aggregate(r, ses.keys, ses.base + tr, agg_r);
+          publish(ses.rec + tr, tr == 0 ? ses.keys.inc : ses.keys.agg, tag_of(ses.base, tr), agg_r);
         }
       }
       // ---- decoupled look-back for tile tc -------------------------------------
@@ -542,13 +634,17 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
       if (tc > 0) {
         excl = look_back(ses, tc, lane, w);
         if (lane == 0 && tc < ntiles - 1) {
-          publish_inclusive(ses.rec + tc, ses.keys, ses.base + tc, agg_c, excl + agg_c);
+          publish(ses.rec + tc, ses.keys.inc, tag_of(ses.base, tc), excl + agg_c);
         }
       }
       agg_c = agg_r;
       if (lane == 0) {
         *s_prefix = excl;
-        s_raw[slot] = single ? 0ull : raw;
+        s_raw[slot] = take ? raw : 0ull;
+        if (count) {
+          s_done[0] = raw;
+          s_done[1] = tickets;
+        }
       }
     } else {
       // ---- tile tn's loads go out now and land during the look-back ----------
@@ -558,7 +654,11 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
         for (int w = 0; w < wave; ++w) wexcl_r += s_wave_total[w];
     }
     kh::lds_barrier();  // barrier B
-    const int64_t after = single ? ntiles : tile_of(s_raw[slot], ses.base, ntiles);
+    const int64_t after = take ? tile_of((uint32_t)s_raw[slot], ses.base, ntiles) : ntiles;
+    if (take && after >= ntiles) {
+      taking = false;  // the workgroup's last ticket is back
+      counting = true;
+    }
 
     if (!ctrl && tc >= 0) {
       // ---- y = fl32(prefix + row offset + running sum within the float4) -----
@@ -640,18 +740,22 @@ scan(KH_MEMREF1(const float, x), KH_MEMREF1(float, y), KH_MEMREF1(float, y_lo),
                         blockDim.z == 1;
   const int64_t tile_elems = (int64_t)((int)blockDim.x - kh::kWave) * kPerThread;
   const int64_t ntiles = shape_ok ? (n + tile_elems - 1) / tile_elems : 0;
-  const bool room = ntiles == 1 ||
-                    (bytes_from_align8(KH_PTR(totals_lo), totals_lo_n0, totals_lo_s0) >= (int64_t)sizeof(Header) &&
+  const int64_t lo_bytes = bytes_from_align8(KH_PTR(totals_lo), totals_lo_n0, totals_lo_s0);
+  // (Tickets and tile indices are 32-bit: ntiles < 2^31 always holds for a
+  // device's memory; refused otherwise.)
+  const bool room = ntiles < (int64_t(1) << 31) && (ntiles == 1 ||
+                    (lo_bytes >= (int64_t)(sizeof(Header) + sizeof(Counters)) &&
                      bytes_from_align8(KH_PTR(totals_hi), totals_hi_n0, totals_hi_s0) >=
-                         (int64_t)sizeof(Record) * (ntiles - 1));
+                         (int64_t)sizeof(Record) * (ntiles - 1)));
   __shared__ bool s_refuse;
   bool refuse = !shape_ok || !room;
-  Session ses{align8<Header>(KH_PTR(totals_lo)), align8<Record>(KH_PTR(totals_hi)), 0, Keys{0, 0}};
+  Session ses{align8<Header>(KH_PTR(totals_lo)), nullptr, align8<Record>(KH_PTR(totals_hi)), 0, Keys{0, 0}};
+  ses.c = counters_of(ses.h, lo_bytes);
   const bool single = ntiles == 1;  // one tile: one workgroup, no look-back state
   Opened o{0, 0, 0, 0, true};
   if (!refuse && !single) {
     if (tid == 0) {
-      o = open_session(ses.h);
+      o = open_session(ses.h, ses.c, ntiles);
       s_session[0] = o.base;
       s_session[1] = session_key(ses.h, o.nonce);
       s_ticket[0] = tile_of(o.t0, o.base, ntiles);
@@ -681,15 +785,19 @@ scan(KH_MEMREF1(const float, x), KH_MEMREF1(float, y), KH_MEMREF1(float, y_lo),
   const int64_t second = s_ticket[1];
   ses.base = s_session[0];
   ses.keys = record_keys(s_session[1]);
-  if (first < ntiles) {
-    if (kh::aligned16(X) && kh::aligned16(Y) && (n & 3) == 0)
-      scan_tiles<true>(X, Y, ses, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off);
-    else
-      scan_tiles<false>(X, Y, ses, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off);
+  if (first >= ntiles) {
+    // No tile for this workgroup: both its tickets are past the end.
+    if (tid == 0) close_session(ses.h, ses.c, ses.base, o.nonce, count_done(ses.c, 2), 2);
+    return;
   }
-  // Every ticket this workgroup took has returned by now (the last one was
-  // read through LDS before the final barrier).
-  if (!single && tid == 0) close_session(ses.h, o.nonce);
+  __shared__ uint64_t s_done[2];
+  if (kh::aligned16(X) && kh::aligned16(Y) && (n & 3) == 0)
+    scan_tiles<true>(X, Y, ses, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off, s_done);
+  else
+    scan_tiles<false>(X, Y, ses, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off, s_done);
+  // s_done was written before the last barrier B; the nonce is in thread 0's
+  // registers.
+  if (!single && tid == 0) close_session(ses.h, ses.c, ses.base, o.nonce, s_done[0], (uint32_t)s_done[1]);
 }
 
 // The reference's second pass (scan.cpp:350-453). With the single-pass

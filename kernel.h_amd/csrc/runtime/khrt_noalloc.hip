@@ -31,13 +31,14 @@
 
 namespace {
 
-// 256 B for the scan's 40-byte header, then 24 B per tile of
-// KH_SCAN_TILE elements for every tile but the last: 2^31 elements need
-// 139,811 tiles, 3.36 MB.
+// 512 B for the scan's header (its ticket counters 256 B past its signed
+// words, in another cache line), then 16 B per tile of KH_SCAN_TILE
+// elements for every tile but the last: 2^31 elements need 139,811 tiles,
+// 2.24 MB.
 constexpr size_t kScratchBytes = size_t(4) << 20;
-constexpr size_t kHeaderBytes = 256;
+constexpr size_t kHeaderBytes = 512;
 constexpr int64_t kMaxElements = int64_t(1) << 31;
-static_assert(kHeaderBytes + 24 * ((kMaxElements + KH_SCAN_TILE - 1) / KH_SCAN_TILE) <= kScratchBytes,
+static_assert(kHeaderBytes + 16 * ((kMaxElements + KH_SCAN_TILE - 1) / KH_SCAN_TILE) <= kScratchBytes,
               "scratch holds the state of the largest accepted scan");
 
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
@@ -127,7 +128,10 @@ extern "C" int kh_scan_noalloc(const float *x, float *y, int64_t n, void *stream
     if (int rc = khrt_pack_memref(slots + 5 * i, 5, args[i].ptr, 1, &args[i].count)) return rc;
   }
   for (int i = 0; i < 25; ++i) params[i] = &slots[i];
+  // As kh_scan: at most one resident round of workgroups, each given the
+  // same number of tiles.
   const int64_t tiles = (n + KH_SCAN_TILE - 1) / KH_SCAN_TILE;
-  const unsigned grid = static_cast<unsigned>(tiles < s.resident ? tiles : s.resident);
+  const int64_t rounds = (tiles + s.resident - 1) / s.resident;
+  const unsigned grid = static_cast<unsigned>((tiles + rounds - 1) / rounds);
   return khrt_launch_raw(s.function, khrt_dim3{grid, 1, 1}, khrt_dim3{KH_SCAN_THREADS, 1, 1}, 0, stream, params);
 }

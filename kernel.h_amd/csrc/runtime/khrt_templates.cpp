@@ -301,9 +301,14 @@ int launch_template(const char *name, khrt::LaunchArgs &args, const Shape &shape
   if (int rc = get_function(t->co, launch_symbol(t, shape), &fn)) return rc;
   if (std::strcmp(name, "scan") == 0) {
     // The look-back scan is persistent: one resident wave of workgroups
-    // loops over tiles, so launch no more workgroups than fit at once.
+    // loops over tiles, so launch no more workgroups than fit at once, and
+    // as many as give every workgroup the same number of tiles (grid.x is
+    // the tile count here): 4370 tiles at n = 2^26 run as 18 full rounds of
+    // 243 workgroups, not 17 rounds of 256 and an 18th of 18 tiles, during
+    // which HBM idles.
     if (const int64_t resident = resident_workgroups(fn, block.x); resident > 0) {
-      grid.x = static_cast<unsigned>(std::min<int64_t>(grid.x, resident));
+      const int64_t tiles = grid.x, rounds = ceil_div(tiles, resident);
+      grid.x = static_cast<unsigned>(ceil_div(tiles, rounds));
     }
   }
   return khrt::verified_launch(fn, grid, block, 0, stream, args.params(), args.count());

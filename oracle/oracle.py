@@ -15,6 +15,8 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "_build", "liboracle.so")
 _lib = None
+# Builds of the same source for wider vector ISAs (oracle/Makefile).
+_ISA_LIBS = {"x86-64-v2": "liboracle.so", "x86-64-v3": "liboracle_v3.so", "x86-64-v4": "liboracle_v4.so"}
 
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
@@ -25,6 +27,35 @@ _u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
 def build() -> None:
     """Compile liboracle.so from oracle.c (always recompiles)."""
     subprocess.run(["make", "-B", "-s", "-C", _HERE], check=True)
+
+
+def host_isa() -> str:
+    """The widest x86-64 level this host's CPU flags support (v4: AVX-512
+    F/BW/CD/DQ/VL; v3: AVX2 + FMA + BMI2 + MOVBE), as the CPU baseline's
+    stand-in for -march=native on a host the oracle was not built on."""
+    flags = set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    flags = set(line.split(":", 1)[1].split())
+                    break
+    except OSError:
+        return "x86-64-v2"
+    if {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"} <= flags:
+        return "x86-64-v4"
+    if {"avx2", "fma", "bmi2", "movbe"} <= flags:
+        return "x86-64-v3"
+    return "x86-64-v2"
+
+
+def use_isa(level: str) -> str:
+    """Loads the oracle build for x86-64 level `level` (must not exceed the
+    host's, see host_isa) in place of the portable one; returns the path."""
+    global _LIB_PATH, _lib
+    _LIB_PATH = os.path.join(_HERE, "_build", _ISA_LIBS[level])
+    _lib = None
+    return _LIB_PATH
 
 
 def lib():

@@ -170,14 +170,14 @@ def test_scan_refuses_without_touching_totals(dev, short):
     """Too little room for the look-back state, or a workgroup shape the tile
     loop does not take: y becomes NaN and the totals (and the memory past
     them) keep their contents."""
-    n = 200000  # 66 tiles of 3072 at 256 threads: 65 records of 24 B = 390 floats
+    n = 200000  # 66 tiles of 3072 at 256 threads: 65 records of 16 B = 260 floats
     T = kh.scan_workspace_floats(n)
     x = O.uniform(n, 5, 0.0, 1.0)
     guard = 4096
     th, tl = empty(T + guard, 5.0), empty(T + guard, 6.0)
     t_hi, t_lo, block = T, T, 256
     if short == "totals_hi":
-        t_hi = 300
+        t_hi = 200
     elif short == "totals_lo":
         t_lo = 9  # 36 B: the 40-byte header does not fit
     else:
