@@ -89,6 +89,15 @@ KHRT_API int khrt_fill_f32(void *dst, float value, size_t count, void *stream);
 /* Module lifecycle (gpu_module.hpp:17-42): a corrupted or truncated image
  * is a typed error, never a crash. */
 KHRT_API int khrt_module_load_data(void **module, const void *image, size_t size);
+/* Extent in bytes of an AMDGPU ELF64 code object, read from its own
+ * headers: the end of the ELF header, both header tables and every segment
+ * and section with file contents. For callers that hold an image without
+ * its size, as Backend::module_load_data(const void *image) does
+ * (backend.hpp:75; hipModuleLoadData takes no size either): it trusts, as
+ * that loader does, that the bytes the headers name are there. Not an ELF
+ * code object, malformed tables or an extent beyond 1 GiB -> KHRT_E_INVALID.
+ * No device needed. */
+KHRT_API int khrt_elf_image_size(const void *image, size_t *size);
 KHRT_API int khrt_module_get_function(void **function, void *module, const char *name);
 KHRT_API int khrt_module_unload(void *module);
 /* Raw launch (Backend::launch_kernel): no verification. */

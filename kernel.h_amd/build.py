@@ -9,6 +9,8 @@ Outputs under kernel.h_amd/build/:
   gen/kh_cli_embed.S   .incbin of the CLI-only code objects (hipref, gemm_tune)
   libkhrt.so           the C-ABI runtime (include/khrt.h)
   kernelh              the CLI (compile / bench / occupancy)
+  khrt_raii_check, khrt_backend_check, co/mfma_probe.hsaco
+                       test fixtures (sources under tests/)
 
 Usage: python kernel.h_amd/build.py [-j N] [-v]
 """
@@ -43,8 +45,17 @@ OBJ = os.path.join(BUILD, "obj")
 
 # Product code objects embedded in libkhrt.so (order = kh_embed.S order).
 PRODUCT = ["vecadd", "fused_gelu", "softmax", "layernorm", "scan", "gemm", "attention", "util", "roofline"]
-# Test-only code objects (loaded by tests through khrt_module_load_data).
+# Test fixtures, built here so that no GPU run compiles anything:
+#   tests/fixtures/<name>.hip -> co/<name>.hsaco, loaded by tests through
+#     khrt_module_load_data (never embedded in the runtime);
+#   tests/cpp/<name>.cpp -> build/<name>, C++ programs over include/khrt.hpp
+#     and over the reference-side Backend binding.
+TDIR = os.path.join(REPO, "tests")
 PROBES = ["mfma_probe"]
+CPP_CHECKS = {
+    "khrt_raii_check": ["cpp/raii_check.cpp"],
+    "khrt_backend_check": ["cpp/backend_check.cpp", "../kernel.h_amd/integration/backend_khrt.cpp"],
+}
 # CLI-only code objects, embedded in the kernelh executable: the bench
 # comparators (csrc/cli/hipref.hip) and the GEMM tune candidates
 # (csrc/kernels/gemm_tune.hip, built from the product's GEMM templates).
@@ -163,11 +174,14 @@ def build(jobs: int = 8, verbose: bool = False) -> None:
     for d in (CO, GEN, OBJ):
         os.makedirs(d, exist_ok=True)
 
-    srcs = [n for n in PRODUCT + PROBES if os.path.exists(os.path.join(KDIR, n + ".hip"))]
+    srcs = [n for n in PRODUCT if os.path.exists(os.path.join(KDIR, n + ".hip"))]
+    fixture_dir = os.path.join(TDIR, "fixtures")
+    probes = [n for n in PROBES if os.path.exists(os.path.join(fixture_dir, n + ".hip"))]
     cli_dirs = {n: (CLIDIR if d == "cli" else KDIR) for n, d in CLI_CODE_OBJECTS.items()}
     cli_cos = [n for n in CLI_CODE_OBJECTS if os.path.exists(os.path.join(cli_dirs[n], n + ".hip"))]
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         outs = dict(zip(srcs, ex.map(lambda n: compile_co(n, verbose), srcs)))
+        list(ex.map(lambda n: compile_co(n, verbose, fixture_dir), probes))
         cli_outs = dict(zip(cli_cos, ex.map(lambda n: compile_co(n, verbose, cli_dirs[n]), cli_cos)))
     present = {n: p for n, p in outs.items() if n in PRODUCT}
 
@@ -225,6 +239,14 @@ def build(jobs: int = 8, verbose: bool = False) -> None:
         run([CXX, *HOST_FLAGS, "-o", os.path.join(BUILD, "kernelh"), *cli_srcs, cli_embed_obj, f"-L{BUILD}",
              "-lkhrt", "-ldl", "-Wl,-rpath,$ORIGIN", f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib"],
             verbose)
+    # The C++ check programs (test fixtures) over the installed interface:
+    # include/ plus, for the Backend binding, tests/cpp/restated.
+    for exe, parts in CPP_CHECKS.items():
+        cpp = [os.path.normpath(os.path.join(TDIR, p)) for p in parts]
+        if all(os.path.exists(p) for p in cpp):
+            run([CXX, "-O1", "-g", "-std=c++20", "-Wall", "-Wextra", f"-I{REPO}/include",
+                 f"-I{os.path.join(TDIR, 'cpp', 'restated')}", "-o", os.path.join(BUILD, exe), *cpp,
+                 f"-L{BUILD}", "-lkhrt", "-Wl,-rpath,$ORIGIN"], verbose)
     if verbose:
         print("built", lib)
 

@@ -139,7 +139,13 @@ std::string exe_dir() {
 
 const char *code_object_of(const std::string &kernel) { return kernel == "scan_totals" ? "scan" : kernel.c_str(); }
 
-// Occupancy of a template at its launcher block size (256; scan 1024).
+// resources.json: the reference's keys (kernel, target, vgpr_count,
+// sgpr_count, lds_bytes, wavefront_size, occupancy_estimate;
+// resource_reporter.hpp:50-58) plus this build's extras. occupancy_estimate
+// is the reference's register-limited waves per CU,
+// floor(reg_file_per_cu / (registers x wavefront_size)) clamped to
+// [1, waves_per_cu] (resource_reporter.cpp:232-255), where registers counts
+// the VGPRs and AGPRs that share gfx950's register file.
 std::string resources_json(const std::string &kernel, const std::string &shape) {
   // Resources of the symbol the launcher runs at this shape (a template may
   // carry variants, e.g. gemm_small_pf2 or softmax_wide).
@@ -162,6 +168,7 @@ std::string resources_json(const std::string &kernel, const std::string &shape) 
      << "  \"vgpr_count\": " << r.vgpr_count << ",\n  \"agpr_count\": " << r.agpr_count << ",\n"
      << "  \"sgpr_count\": " << r.sgpr_count << ",\n  \"lds_bytes\": " << r.lds_bytes << ",\n"
      << "  \"scratch_bytes\": " << r.private_segment_bytes << ",\n  \"wavefront_size\": " << r.wavefront_size
+     << ",\n  \"occupancy_estimate\": " << rep.vgpr_limited_waves
      << ",\n  \"max_flat_workgroup_size\": " << r.max_flat_workgroup_size << ",\n"
      << "  \"launch\": {\"grid\": [" << grid.x << ", " << grid.y << ", " << grid.z << "], \"block\": [" << block.x
      << ", " << block.y << ", " << block.z << "]},\n"

@@ -8,6 +8,7 @@
 // message, nothing throws across the boundary.
 #include "kernelh/khrt_internal.hpp"
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -278,6 +279,48 @@ int khrt_module_load_data(void **module, const void *image, size_t size) {
     g_images.emplace(static_cast<void *>(m), std::move(copy));
   }
   *module = m;
+  return 0;
+}
+
+int khrt_elf_image_size(const void *image, size_t *size) {
+  if (image == nullptr || size == nullptr) return fail(KHRT_E_INVALID, "khrt_elf_image_size: null argument");
+  *size = 0;
+  const unsigned char *b = static_cast<const unsigned char *>(image);
+  if (!(b[0] == 0x7f && b[1] == 'E' && b[2] == 'L' && b[3] == 'F')) {
+    return fail(KHRT_E_INVALID, "khrt_elf_image_size: image is not an ELF code object");
+  }
+  auto rd16 = [&](size_t off) { uint16_t v; std::memcpy(&v, b + off, 2); return v; };
+  auto rd32 = [&](size_t off) { uint32_t v; std::memcpy(&v, b + off, 4); return v; };
+  auto rd64 = [&](size_t off) { uint64_t v; std::memcpy(&v, b + off, 8); return v; };
+  if (b[4] != 2 || b[5] != 1 || rd16(18) != 0xE0) {
+    return fail(KHRT_E_INVALID, "khrt_elf_image_size: image is not a 64-bit little-endian AMDGPU code object");
+  }
+  // No code object of this runtime comes near this; larger extents come
+  // from headers that are not a code object's.
+  constexpr uint64_t kMax = uint64_t(1) << 30;
+  const uint64_t phoff = rd64(32), shoff = rd64(40);
+  const uint16_t phentsize = rd16(54), phnum = rd16(56), shentsize = rd16(58), shnum = rd16(60);
+  if ((phnum > 0 && (phentsize < 56 || phoff > kMax)) || (shnum > 0 && (shentsize < 64 || shoff > kMax))) {
+    return fail(KHRT_E_INVALID, "khrt_elf_image_size: malformed header tables");
+  }
+  uint64_t end = 64;
+  auto extend = [&](uint64_t off, uint64_t len) {
+    if (off > kMax || len > kMax) return false;
+    end = std::max(end, off + len);
+    return true;
+  };
+  bool ok = extend(phoff, uint64_t(phentsize) * phnum) && extend(shoff, uint64_t(shentsize) * shnum);
+  for (uint16_t i = 0; ok && i < phnum; ++i) {
+    const size_t p = phoff + size_t(i) * phentsize;
+    ok = extend(rd64(p + 8), rd64(p + 32));
+  }
+  for (uint16_t i = 0; ok && i < shnum; ++i) {
+    const size_t sh = shoff + size_t(i) * shentsize;
+    const uint32_t type = rd32(sh + 4);
+    if (type != 8 /* SHT_NOBITS */ && type != 0) ok = extend(rd64(sh + 24), rd64(sh + 32));
+  }
+  if (!ok || end > kMax) return fail(KHRT_E_INVALID, "khrt_elf_image_size: extent beyond 1 GiB");
+  *size = static_cast<size_t>(end);
   return 0;
 }
 

@@ -111,6 +111,7 @@ SIGNATURES = {
     "khrt_memcpy_d2d": (_i, [_vp, _vp, _sz]),
     "khrt_fill_f32": (_i, [_vp, ctypes.c_float, _sz, _vp]),
     "khrt_module_load_data": (_i, [ctypes.POINTER(_vp), _vp, _sz]),
+    "khrt_elf_image_size": (_i, [_vp, ctypes.POINTER(_sz)]),
     "khrt_module_get_function": (_i, [ctypes.POINTER(_vp), _vp, ctypes.c_char_p]),
     "khrt_module_unload": (_i, [_vp]),
     "khrt_launch_raw": (_i, [_vp, Dim3, Dim3, _sz, _vp, ctypes.POINTER(_vp)]),

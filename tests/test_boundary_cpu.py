@@ -359,3 +359,32 @@ def test_truncated_images_rejected_before_the_runtime(name):
     with pytest.raises(kh.KhrtError) as e:
         kh.GpuModule(bytes(bad))
     assert "not an AMDGPU code object" in e.value.message
+
+
+def _elf_extent(blob: bytes):
+    buf = ctypes.create_string_buffer(blob, len(blob))
+    size = ctypes.c_size_t(0)
+    rc = kh.lib.khrt_elf_image_size(buf, ctypes.byref(size))
+    return rc, size.value
+
+
+@pytest.mark.parametrize("name", ["vecadd", "fused_gelu", "softmax", "layernorm", "scan", "gemm", "attention"])
+def test_elf_image_size_is_the_code_object_length(name):
+    """Backend::module_load_data passes an image without its size
+    (backend.hpp:75); the extent read from the ELF headers is the length
+    of the code object, also with bytes after it in the caller's buffer."""
+    blob = kh.code_object(name)
+    assert _elf_extent(blob) == (0, len(blob))
+    assert _elf_extent(blob + b"\xff" * 4096) == (0, len(blob))
+
+
+def test_elf_image_size_refuses_what_is_not_a_code_object():
+    blob = bytearray(kh.code_object("vecadd"))
+    assert _elf_extent(b"\x00" * 128)[0] == kh.KHRT_E_INVALID
+    x86 = bytearray(blob)
+    x86[18] = 0x3E
+    assert _elf_extent(bytes(x86))[0] == kh.KHRT_E_INVALID
+    far = bytearray(blob)
+    far[40:48] = struct.pack("<Q", 1 << 40)  # e_shoff far beyond any code object
+    rc, _ = _elf_extent(bytes(far))
+    assert rc == kh.KHRT_E_INVALID and "khrt_elf_image_size" in kh.lib.khrt_last_error().decode()

@@ -67,6 +67,35 @@ def test_compiled_isa_carries_the_design_instructions(tmp_path, kernel):
     assert '"scratch_bytes": 0' in res  # no register spills
 
 
+@pytest.mark.parametrize("kernel", sorted(DESIGN_INSTRUCTIONS) + ["scan_totals"])
+def test_resources_json_reference_schema(tmp_path, kernel):
+    """resources.json parses as JSON and carries the reference's contract keys
+    with their types (resource_reporter.hpp:50-58); occupancy_estimate is the
+    reference's register-limited waves per CU (resource_reporter.cpp:232-255)
+    over gfx950's register file of 4 SIMDs x 512 registers x 64 lanes, capped
+    at 32 waves. The hardware allocates registers in granules of 8, 4 SIMDs
+    of 512 each, so its resident count, 4 * floor(512 / roundup8(registers)),
+    is never above the estimate and equals it on a multiple of 8 below 64."""
+    import json
+    shape = DESIGN_INSTRUCTIONS.get(kernel, ("n=1000000",))[0]
+    r = run("compile", "--kernel", kernel, "--shape", shape, "--out", str(tmp_path), "--resources")
+    assert r.returncode == 0, r.stdout
+    res = json.loads((tmp_path / "resources.json").read_text())
+    for key, typ in (("kernel", str), ("target", str), ("vgpr_count", int), ("sgpr_count", int),
+                     ("lds_bytes", int), ("wavefront_size", int), ("occupancy_estimate", int)):
+        assert isinstance(res[key], typ), (key, res.get(key))
+    assert res["kernel"] == kernel and res["target"] == "amdgcn-gfx950" and res["wavefront_size"] == 64
+    regs = res["vgpr_count"] + res["agpr_count"]
+    assert 0 < regs <= 512
+    est = res["occupancy_estimate"]
+    assert est == min(32, max(1, (4 * 512 * 64) // (regs * 64)))
+    hw = min(32, 4 * (512 // (-(-regs // 8) * 8)))
+    assert hw <= est and (regs % 8 or regs >= 64 or hw == est)
+    # The launch the launcher makes at this shape fits those waves.
+    threads = res["launch"]["block"][0] * res["launch"]["block"][1] * res["launch"]["block"][2]
+    assert res["occupancy_estimate"] * 64 >= threads
+
+
 def test_compile_bogus_target_exit_1(tmp_path):
     r = run("compile", "--kernel", "vecadd", "--shape", "n=1024", "--target", "bogus-target", "--out", str(tmp_path))
     assert r.returncode == 1
