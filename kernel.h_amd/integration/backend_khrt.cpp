@@ -20,9 +20,12 @@ Result<void> ok(int rc) {
   if (rc != 0) return fail<void>(rc);
   return {};
 }
-template <class T>
-Result<T> ok_or(int rc, T v) {
-  if (rc != 0) return fail<T>(rc);
+// Runs `call` (which writes its out-parameter) first, then reads the value.
+// Passing the value as a second argument instead would let the compiler read
+// it before the call: argument evaluation order is unspecified.
+template <class T, class Call>
+Result<T> ok_or(Call &&call, const T &v) {
+  if (int rc = call()) return fail<T>(rc);
   return v;
 }
 
@@ -40,7 +43,7 @@ class KhrtBackend final : public Backend {
 
   Result<void *> malloc(size_t bytes) override {
     void *p = nullptr;
-    return ok_or(khrt_malloc(&p, bytes), p);
+    return ok_or([&] { return khrt_malloc(&p, bytes); }, p);
   }
   Result<void> free(void *ptr) override { return ok(khrt_free(ptr)); }
   Result<void> memcpy_h2d(void *dst, const void *src, size_t bytes) override {
@@ -58,11 +61,11 @@ class KhrtBackend final : public Backend {
     size_t size = 0;
     if (int rc = khrt_elf_image_size(image, &size)) return fail<void *>(rc);
     void *m = nullptr;
-    return ok_or(khrt_module_load_data(&m, image, size), m);
+    return ok_or([&] { return khrt_module_load_data(&m, image, size); }, m);
   }
   Result<void *> module_get_function(void *module, const char *name) override {
     void *f = nullptr;
-    return ok_or(khrt_module_get_function(&f, module, name), f);
+    return ok_or([&] { return khrt_module_get_function(&f, module, name); }, f);
   }
   Result<void> module_unload(void *module) override { return ok(khrt_module_unload(module)); }
 
@@ -76,7 +79,7 @@ class KhrtBackend final : public Backend {
 
   Result<EventHandle> event_create() override {
     void *e = nullptr;
-    return ok_or<EventHandle>(khrt_event_create(&e), e);
+    return ok_or<EventHandle>([&] { return khrt_event_create(&e); }, e);
   }
   Result<void> event_record(EventHandle event, StreamHandle stream) override {
     return ok(khrt_event_record(event, stream));
@@ -84,7 +87,7 @@ class KhrtBackend final : public Backend {
   Result<void> event_synchronize(EventHandle event) override { return ok(khrt_event_synchronize(event)); }
   Result<float> event_elapsed_time(EventHandle start, EventHandle end) override {
     float ms = 0.0f;
-    return ok_or(khrt_event_elapsed_ms(&ms, start, end), ms);
+    return ok_or([&] { return khrt_event_elapsed_ms(&ms, start, end); }, ms);
   }
   Result<void> event_destroy(EventHandle event) override { return ok(khrt_event_destroy(event)); }
 };

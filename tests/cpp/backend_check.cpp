@@ -99,9 +99,10 @@ void gpu_checks(Backend &be) {
   size_t vsize = 0, ssize = 0;
   const void *vimage = image_of("vecadd", &vsize);
   auto vm = be.module_load_data(vimage);  // no size passed
-  expect(vm.has_value(), "module_load_data(vecadd image)");
+  expect(vm.has_value(), "module_load_data(vecadd image of " + std::to_string(vsize) + " B)" +
+                             (vm ? std::string() : ": " + vm.error().message));
   auto vf = be.module_get_function(*vm, "vecadd");
-  expect(vf.has_value(), "module_get_function(vecadd)");
+  expect(vf.has_value(), "module_get_function(vecadd)" + (vf ? std::string() : ": " + vf.error().message));
 
   const int64_t n = 1000003;
   std::vector<float> a(n), b(n), c(n);
