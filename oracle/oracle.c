@@ -242,6 +242,90 @@ KHO_API void kho_ref_scan(const float *x, float *y, size_t n, int exclusive) {
   }
 }
 
+/* Correctly rounded (round-to-nearest-even) fp32 inclusive prefix of any
+ * finite fp32 inputs: the exact value the fp64 reference above approximates
+ * (e2e_scan_test.cpp:159-173) and the template's double-float + 3-word
+ * expansion aims for (scan.cpp:25-38). Every finite fp32 is an integer
+ * multiple of 2^-149, so the running sum is kept exactly as a 320-bit
+ * two's-complement integer in units of 2^-149 (a long accumulator: 277 bits
+ * span the fp32 range, the rest hold the carries of up to 2^40 terms), and
+ * each prefix is rounded from it once. `acc_abs` (optional) receives the
+ * fp64 running sum of |x|, which error bounds for inexact summation use.
+ * Pinned against Python's exact rational arithmetic (tests/test_oracle.py). */
+#define KHO_LIMBS 5
+static void acc_add(uint64_t *a, const uint64_t *b) {
+  unsigned __int128 c = 0;
+  for (int i = 0; i < KHO_LIMBS; ++i) {
+    c += (unsigned __int128)a[i] + b[i];
+    a[i] = (uint64_t)c;
+    c >>= 64;
+  }
+}
+static void acc_neg(uint64_t *a) {
+  unsigned __int128 c = 1;
+  for (int i = 0; i < KHO_LIMBS; ++i) {
+    c += (uint64_t)~a[i];
+    a[i] = (uint64_t)c;
+    c >>= 64;
+  }
+}
+static float acc_round_f32(const uint64_t *acc) {
+  uint64_t m[KHO_LIMBS];
+  memcpy(m, acc, sizeof m);
+  const int neg = (int)(m[KHO_LIMBS - 1] >> 63);
+  if (neg) acc_neg(m);
+  int top = -1;  /* index of the highest set bit of |acc| */
+  for (int i = KHO_LIMBS - 1; i >= 0 && top < 0; --i)
+    if (m[i]) top = 64 * i + 63 - __builtin_clzll(m[i]);
+  if (top < 0) return 0.0f;
+  float r;
+  if (top <= 23) {
+    /* below 2^24 units of 2^-149: subnormal or the smallest normals, exact */
+    r = ldexpf((float)m[0], -149);
+  } else {
+    /* keep 24 bits [top-23, top]; round the rest to nearest, ties to even */
+    const int lo = top - 23;
+    uint64_t keep = 0;
+    for (int b = 0; b < 24; ++b) {
+      const int bit = lo + b;
+      keep |= ((m[bit >> 6] >> (bit & 63)) & 1ull) << b;
+    }
+    const int half = lo - 1;
+    const int hbit = (int)((m[half >> 6] >> (half & 63)) & 1ull);
+    int sticky = 0;
+    for (int bit = 0; bit < half && !sticky; ++bit) sticky = (int)((m[bit >> 6] >> (bit & 63)) & 1ull);
+    if (hbit && (sticky || (keep & 1ull))) keep += 1;
+    r = ldexpf((float)keep, lo - 149);  /* keep <= 2^24: exact; overflow gives inf */
+  }
+  return neg ? -r : r;
+}
+KHO_API void kho_ref_scan_exact(const float *x, float *y, size_t n, double *acc_abs) {
+  uint64_t acc[KHO_LIMBS] = {0};
+  double sabs = 0.0;
+  for (size_t i = 0; i < n; ++i) {
+    uint32_t bits;
+    memcpy(&bits, &x[i], 4);
+    const uint32_t ebits = (bits >> 23) & 0xffu;
+    uint64_t mant = bits & 0x7fffffu;
+    int shift = 0;  /* x = mant * 2^(shift - 149) */
+    if (ebits != 0) {
+      mant |= 0x800000u;
+      shift = (int)ebits - 1;
+    }
+    uint64_t t[KHO_LIMBS] = {0};
+    const int limb = shift >> 6, off = shift & 63;
+    t[limb] = mant << off;
+    if (off > 40 && limb + 1 < KHO_LIMBS) t[limb + 1] = mant >> (64 - off);
+    if (bits >> 31) acc_neg(t);
+    acc_add(acc, t);
+    y[i] = acc_round_f32(acc);
+    if (acc_abs) {
+      sabs += fabs((double)x[i]);
+      acc_abs[i] = sabs;
+    }
+  }
+}
+
 /* gelu_reference (test/unit/e2e_fused_gelu_test.cpp:59-70): t = 1.5x + 0.5,
  * 0.5 t (1 + tanh(0.7978845608 (t + 0.044715 t^3))), fp64, with the
  * template's constants. with_tanh = 0 gives the negative control's

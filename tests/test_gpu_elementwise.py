@@ -66,14 +66,15 @@ def test_vecadd_unaligned_and_offset_descriptors(dev):
     assert np.array_equal(got[1:], O.ref_vecadd(a[1:], b[1:]))
 
 
-@pytest.mark.parametrize("n", [4194304, 1048576, 1000, 7, 1 << 26])
-def test_fused_gelu_vs_fp64_reference(dev, n):
+@pytest.mark.parametrize("n,dist", [(4194304, "lcg"), (1048576, "lcg"), (1000, "lcg"), (7, "lcg"),
+                                    (1 << 22, "normal"), (1 << 26, "normal")])
+def test_fused_gelu_vs_fp64_reference(dev, n, dist):
     seed = 0x3A5F91
-    # Reference sizes use the reference's LCG fill; the BASELINE 2^26 case
-    # uses the N(0,1) bench inputs.
-    x, _ = O.lcg_fill(n, seed) if n <= (1 << 22) else (O.normal(n, 0x6E1, 0.0, 1.0), 0)
+    # The reference's own sizes use its LCG fill (U[-1,1) on a 2^-15 grid);
+    # the BASELINE configurations 2^22 and 2^26 use N(0,1) inputs.
+    x, _ = O.lcg_fill(n, seed) if dist == "lcg" else (O.normal(n, 0x6E1 + n, 0.0, 1.0), 0)
     dx, dtmp, do = up(x), empty(4, None), empty(n)
-    say(f"fused_gelu n={n}")
+    say(f"fused_gelu n={n} {dist}")
     kh.fused_gelu(dx, dtmp, do, n)
     got = down(do, n).astype(np.float64)
     ref = O.ref_gelu(x)

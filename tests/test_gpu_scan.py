@@ -217,3 +217,49 @@ def test_scan_negative_control_exclusive(dev):
     x = O.mt19937_fill(n, 0x51AC0D3E)
     got, _ = _scan(x, n)
     assert np.max(np.abs(got.astype(np.float64) - O.ref_scan(x, exclusive=True))) > 1e-4
+
+
+# Off the grid: inputs whose partial sums fp64 cannot hold exactly. y is then
+# fl32 of an fp64 tree sum, not always the correctly rounded prefix r. Every
+# fp64 partial sum S_i is a sum of the x_j (j <= i) through a tree in which no
+# input passes more than D additions, so |S_i - P_i| <= gamma_D A_i, with P_i
+# the exact prefix, A_i = sum |x_j| and gamma_D = D u/(1 - D u), u = 2^-53
+# (Higham, Accuracy and Stability of Numerical Algorithms, 2nd ed., 4.2).
+# Rounding both S_i and P_i to fp32 (unit 2^-24) gives
+#     |y_i - r_i| <= 2^-23 |r_i| / (1 - 2^-24) + (1 + 2^-24) gamma_D A_i.
+# D for this kernel: an element passes 3 additions into its float4 row sum,
+# 6 in the wave's DPP scan, 1 in `inc - sk`, 4 over its wave's rows, 14 over
+# earlier waves, 6 in the tile aggregate, 4 in its own float4, 2 with the
+# prefix; a tile's inclusive prefix adds at most 1 + 6 + (windows walked) to
+# its nearest published predecessor's, which in the worst case is the tile
+# just before it. D = 10 ntiles + 64 bounds all of this; ntiles is counted
+# for the smallest tile the kernel accepts (256-thread workgroups: 3 data
+# waves x 64 lanes x 16 elements), so the bound holds for any launch shape.
+def _offgrid(kind, n):
+    rng = np.random.default_rng(0x0FF6)
+    x = rng.standard_normal(n)
+    if kind == "wide":
+        x = x * np.exp2(rng.integers(-20, 21, n).astype(np.float64))
+    return x.astype(np.float32)
+
+
+@pytest.mark.parametrize("kind", ["normal", "wide"])
+def test_scan_off_grid_inputs_within_derived_bound(dev, kind):
+    n = 1 << 20
+    x = _offgrid(kind, n)
+    got, _ = _scan(x, n)
+    r, A = O.ref_scan_exact(x, with_abs=True)
+    tile = 3 * 64 * 16
+    D = 10 * ((n + tile - 1) // tile) + 64
+    u = 2.0 ** -53
+    gamma = D * u / (1 - D * u)
+    r64 = r.astype(np.float64)
+    tol = 2.0 ** -23 * np.abs(r64) / (1 - 2.0 ** -24) + (1 + 2.0 ** -24) * gamma * A
+    err = np.abs(got.astype(np.float64) - r64)
+    assert np.all(np.isfinite(got))
+    worst = int(np.argmax(err / tol))
+    emu = O.emu_scan_template(x)
+    say(f"scan off-grid {kind}: {int(np.sum(got != r))} of {n} differ from the correctly rounded prefix, "
+        f"{int(np.sum(emu != r))} for the template emulator, {int(np.sum(got != emu))} GPU vs emulator; "
+        f"worst err/tol {err[worst] / tol[worst]:.3g} at {worst}")
+    assert np.all(err <= tol), f"element {worst}: |y - r| = {err[worst]:.3e} > {tol[worst]:.3e}"

@@ -159,6 +159,50 @@ def test_scan_reference_exact_rational_tiny():
     assert np.array_equal(y, np.array(exact).astype(np.float32))
 
 
+def _f32_round_exact(q: Fraction) -> float:
+    """Round a rational to the nearest fp32 (ties to even) by rational
+    arithmetic alone: quantum 2^(e-23) for 2^e <= |q| < 2^(e+1), never below
+    the subnormal quantum 2^-149."""
+    if q == 0:
+        return 0.0
+    sign, q = (-1.0 if q < 0 else 1.0), abs(q)
+    e = q.numerator.bit_length() - q.denominator.bit_length()
+    if Fraction(2) ** e > q:
+        e -= 1
+    quantum = Fraction(2) ** (max(e, -126) - 23)
+    t = q / quantum
+    k = t.numerator // t.denominator
+    rem = t - k
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and k % 2 == 1):
+        k += 1
+    return sign * float(k * quantum)  # k <= 2^24: exact in fp32 and fp64
+
+
+def test_scan_exact_reference_vs_rationals():
+    # Wide exponents (subnormals to 2^100), both signs, cancellation, and
+    # hand-made ties: 1 + 2^-24 rounds to even (1.0), 1 + 3*2^-24 up to
+    # 1 + 2^-22, and 1 + 2^-24 + 2^-60 just above the tie, to 1 + 2^-23,
+    # which an fp64 running sum (2^-60 lost below its ulp) rounds to 1.0.
+    rng = np.random.default_rng(7)
+    wide = (rng.standard_normal(1500) * np.exp2(rng.integers(-140, 100, 1500).astype(np.float64))).astype(np.float32)
+    ties = np.array([1.0, 2.0 ** -24, -1.0, -(2.0 ** -24), 1.0, 3 * 2.0 ** -24, -1.0, -3 * 2.0 ** -24,
+                     1.0, 2.0 ** -24, 2.0 ** -60, np.float32(1e-45), -np.float32(1e-45)], np.float32)
+    for x in (wide, ties, np.concatenate([wide[:200], -wide[:200]])):
+        y, a = O.ref_scan_exact(x, with_abs=True)
+        acc, sabs, exact = Fraction(0), 0.0, []
+        for v in x:
+            acc += Fraction(float(v))
+            exact.append(_f32_round_exact(acc))
+        assert np.array_equal(y, np.array(exact, np.float32))
+        assert np.allclose(a, np.cumsum(np.abs(x.astype(np.float64))), rtol=1e-12, atol=0)
+    y = O.ref_scan_exact(ties)
+    assert y[1] == 1.0 and y[5] == np.float32(1 + 2.0 ** -22) and y[10] == np.float32(1 + 2.0 ** -23)
+    assert O.ref_scan(ties)[10] == 1.0  # the fp64 prefix misses it: the exact one is needed off the grid
+    # On the tests' grid inputs the fp64 prefix is exact, so the two agree.
+    g = O.mt19937_fill(1 << 16, 0x29C0FFEE)
+    assert np.array_equal(O.ref_scan_exact(g), O.ref_scan(g))
+
+
 def test_scan_reference_vs_numpy_and_exclusive():
     x = O.uniform(1 << 20, 42, 0.0, 1.0)
     y = O.ref_scan(x)
