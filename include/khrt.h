@@ -239,6 +239,53 @@ KHRT_API int khrt_template_launch_symbol(const char *name, const char *shape, ch
  * once per process from the embedded image). */
 KHRT_API int khrt_template_function(const char *name, void **function);
 
+/* GEMM candidates: the launcher's own `gemm` symbols (product = 1) followed by
+ * the gfx950 tune space that `kernelh tune` evaluates, which re-prunes the
+ * reference's BM/BN x BK x waves x unroll x vec space (autotuner.hpp:36-41,
+ * autotuner.cpp:754-799) for wave64, MFMA 32x32 / 16x16 tiles and 160 KiB of
+ * LDS. Every candidate takes the `gemm` template's 21 memref slots and is
+ * correct for every shape and grid. No reference counterpart beyond that
+ * space: the reference compiles one kernel per sampled config instead. */
+typedef struct khrt_gemm_candidate {
+  char symbol[64];
+  char code_object[16];   /* embedded code object holding the symbol */
+  char pipeline[16];      /* regs, lds-dma, prefetch2, persistent, ksplit, ksplit-deep */
+  int32_t mfma;           /* 32: v_mfma_f32_32x32x2f32; 16: v_mfma_f32_16x16x4f32 */
+  int32_t waves;          /* wave64s per workgroup */
+  int32_t wave_grid_m, wave_grid_n;  /* waves along m and n (K-split: 1 x 1) */
+  int32_t wave_tile_m, wave_tile_n;  /* C elements per wave */
+  int32_t bm, bn, bk;     /* C tile per workgroup; K slab depth (K-split: k group) */
+  int32_t unroll;         /* slabs (K-split: 32-k batches) in flight ahead of the MFMAs */
+  int32_t prio;           /* waves raise their priority while issuing MFMAs */
+  int32_t persistent;     /* grid = min(tiles, two per CU); workgroups loop over tiles */
+  int32_t k_split;        /* the workgroup's waves split K, summed in a fixed order */
+  int32_t product;        /* one of the launcher's own symbols */
+} khrt_gemm_candidate;
+KHRT_API int khrt_gemm_candidate_count(void);
+KHRT_API int khrt_gemm_candidate_get(int i, khrt_gemm_candidate *out);
+/* Launch geometry of a candidate at m x n x k (grid.x workgroups). */
+KHRT_API int khrt_gemm_candidate_geometry(const char *symbol, int64_t m, int64_t n, int64_t k,
+                                          khrt_dim3 *grid, khrt_dim3 *block);
+/* Loaded function of a candidate on the current device. */
+KHRT_API int khrt_gemm_candidate_function(const char *symbol, void **function);
+/* Tune cache the GEMM launcher consults (main.cpp:1320-1420 keeps the
+ * reference's cache for its own CLI only): the JSON-lines file `kernelh tune`
+ * writes, keyed by khrt_tune_cache_key("gemm", "m=..,n=..,k=.."). When set,
+ * kh_gemm, khrt_template_geometry and khrt_template_launch_symbol use the
+ * cached best candidate for a shape that has an entry and the built-in
+ * choice otherwise. NULL or "" turns it off. Until this is called the path
+ * is taken from the KHRT_TUNE_CACHE environment variable (unset: off). The
+ * file is read once per path set. */
+KHRT_API int khrt_set_tune_cache(const char *path);
+/* Cache key of a tuning run (main.cpp:1353-1358 keys it by kernel, shape and
+ * device name, with sha256): FNV-1a 64 of "kernel|shape|device token", as 16
+ * hex digits + NUL (cap >= 17). */
+KHRT_API int khrt_tune_cache_key(const char *kernel, const char *shape, char *out, size_t cap);
+/* "<marketing name> (<arch>) cu=<count>" of the current device, the device
+ * part of the cache key ("AMD Instinct MI355X" when the runtime reports no
+ * marketing name). */
+KHRT_API int khrt_device_token(char *out, size_t cap);
+
 /* One entry point per template. Device pointers, element counts, an optional
  * stream (NULL = default stream). Each packs the reference's memref argument
  * list (2N+3 slots per buffer, same order and ranks), computes the launcher's

@@ -6,7 +6,7 @@ Outputs under kernel.h_amd/build/:
   co/<name>.notes.json resource notes per kernel symbol
   gen/kh_embed.S       .incbin of every product code object
   gen/kh_resources.inc resource table compiled into the runtime
-  gen/kh_cli_embed.S   .incbin of the CLI-only code objects (hipref, gemm_tune)
+  gen/kh_cli_embed.S   .incbin of the CLI-only code objects (hipref)
   libkhrt.so           the C-ABI runtime (include/khrt.h)
   kernelh              the CLI (compile / bench / occupancy)
   khrt_raii_check, khrt_backend_check, co/mfma_probe.hsaco
@@ -43,8 +43,15 @@ CO = os.path.join(BUILD, "co")
 GEN = os.path.join(BUILD, "gen")
 OBJ = os.path.join(BUILD, "obj")
 
+# GEMM tune candidates: csrc/kernels/gemm_tune.hip compiled once per part of
+# its list (gemm_tune_list.h, KH_GEMM_TUNE_PARTS = 4), so the parts compile
+# in parallel. Embedded in the runtime: the launcher runs a candidate when a
+# tune cache names it, and `kernelh tune` evaluates them through the runtime.
+TUNE_PARTS = 4
+VARIANTS = {f"gemm_tune{p}": ("gemm_tune", [f"-DKH_GEMM_TUNE_PART={p}"]) for p in range(TUNE_PARTS)}
 # Product code objects embedded in libkhrt.so (order = kh_embed.S order).
-PRODUCT = ["vecadd", "fused_gelu", "softmax", "layernorm", "scan", "gemm", "attention", "util", "roofline"]
+PRODUCT = ["vecadd", "fused_gelu", "softmax", "layernorm", "scan", "gemm", "attention", "util", "roofline",
+           *VARIANTS]
 # Test fixtures, built here so that no GPU run compiles anything:
 #   tests/fixtures/<name>.hip -> co/<name>.hsaco, loaded by tests through
 #     khrt_module_load_data (never embedded in the runtime);
@@ -57,9 +64,8 @@ CPP_CHECKS = {
     "khrt_backend_check": ["cpp/backend_check.cpp", "../kernel.h_amd/integration/backend_khrt.cpp"],
 }
 # CLI-only code objects, embedded in the kernelh executable: the bench
-# comparators (csrc/cli/hipref.hip) and the GEMM tune candidates
-# (csrc/kernels/gemm_tune.hip, built from the product's GEMM templates).
-CLI_CODE_OBJECTS = {"hipref": "cli", "gemm_tune": "kernels"}
+# comparators (csrc/cli/hipref.hip).
+CLI_CODE_OBJECTS = {"hipref": "cli"}
 
 DEVICE_FLAGS = [
     "-x", "hip", f"--offload-arch={ARCH}", "--cuda-device-only", "--no-gpu-bundle-output",
@@ -96,9 +102,10 @@ def run(cmd, verbose=False, **kw):
 
 
 def compile_co(name: str, verbose: bool, srcdir: str = "") -> str:
-    src = os.path.join(srcdir or KDIR, name + ".hip")
+    base, defs = VARIANTS.get(name, (name, []))
+    src = os.path.join(srcdir or KDIR, base + ".hip")
     out = os.path.join(CO, name + ".hsaco")
-    run([HIPCC, *DEVICE_FLAGS, *EXTRA_DEVICE_FLAGS.get(name, []), "-c", src, "-o", out], verbose)
+    run([HIPCC, *DEVICE_FLAGS, *EXTRA_DEVICE_FLAGS.get(base, []), *defs, "-c", src, "-o", out], verbose)
     isa = run([OBJDUMP, "-d", f"--mcpu={ARCH}", out])
     with open(os.path.join(CO, name + ".isa"), "w") as f:
         f.write(isa)
@@ -174,7 +181,7 @@ def build(jobs: int = 8, verbose: bool = False) -> None:
     for d in (CO, GEN, OBJ):
         os.makedirs(d, exist_ok=True)
 
-    srcs = [n for n in PRODUCT if os.path.exists(os.path.join(KDIR, n + ".hip"))]
+    srcs = [n for n in PRODUCT if os.path.exists(os.path.join(KDIR, VARIANTS.get(n, (n,))[0] + ".hip"))]
     fixture_dir = os.path.join(TDIR, "fixtures")
     probes = [n for n in PROBES if os.path.exists(os.path.join(fixture_dir, n + ".hip"))]
     cli_dirs = {n: (CLIDIR if d == "cli" else KDIR) for n, d in CLI_CODE_OBJECTS.items()}

@@ -1,5 +1,7 @@
-// `kernelh tune`: GEMM tile autotune over the gfx950 candidate space
-// (gemm_tune_list.h), with the reference's evaluator contract
+// `kernelh tune`: GEMM tile autotune over the gfx950 candidates (the
+// launcher's own symbols and the tune space of gemm_tune_list.h, both listed
+// by the runtime: khrt_gemm_candidate_get), with the reference's evaluator
+// contract
 // (tools/kernelh/main.cpp:649-673, 1320-1420; lib/compiler/autotuner.cpp):
 //   * every candidate is evaluated in a child process with a wall-clock
 //     deadline; a hung or crashed candidate is recorded ("timeout",
@@ -9,17 +11,18 @@
 //     capped at 128) against an fp64 host product, relative Frobenius
 //     <= 1e-5, then times it at the tuning shape: warmup 3, median of 10;
 //   * results go to <out>/tune-results.csv (the reference's columns, then
-//     symbol, wave_tile, prio, lds_dma, gflops) and to a cache file keyed by
-//     kernel|shape|device, so a second run with the same key is served from
-//     the cache.
+//     symbol, mfma, wave_grid, wave_tile, pipeline, prio, product, gflops)
+//     and to a cache file keyed by kernel|shape|device, so a second run with
+//     the same key is served from the cache. The runtime's GEMM launcher
+//     reads the same file when pointed at it (KHRT_TUNE_CACHE or
+//     khrt_set_tune_cache) and then runs the cached best for that shape.
 // Differences, each stated in the usage text: the space is a fixed set of
 // precompiled instantiations (no per-candidate compilation), so it is
 // evaluated exhaustively up to --max-candidates instead of sampled and
-// refined, and the cache key is an FNV-1a 64-bit hash.
+// refined, and the cache key is an FNV-1a 64-bit hash (khrt_tune_cache_key).
 #include "tune.hpp"
 
 #include "khrt.h"
-#include "gemm_tune_list.h"
 
 #include <poll.h>
 #include <signal.h>
@@ -44,28 +47,18 @@
 
 extern char **environ;
 
-// The candidate code object, embedded by build.py (gen/kh_cli_embed.S).
-extern "C" const unsigned char kh_cli_co_gemm_tune[];
-extern "C" const unsigned char kh_cli_co_gemm_tune_end[];
-
 namespace khcli {
 namespace {
 
 namespace fs = std::filesystem;
 
-struct Candidate {
-  int wtm, wtn, bk, prio, dma;
-  const char *symbol;
-  int bm() const { return 64 * wtm; }
-  int bn() const { return 64 * wtn; }
-};
+using Candidate = khrt_gemm_candidate;
 
-#define KH_STR2(x) #x
-#define KH_STR(x) KH_STR2(x)
-#define KH_TUNE_ROW(WTM, WTN, BK, PRIO, DMA) \
-  {WTM, WTN, BK, PRIO, DMA, KH_STR(KH_GEMM_TUNE_SYMBOL(WTM, WTN, BK, PRIO, DMA))},
-const Candidate kCandidates[] = {KH_GEMM_TUNE_CONFIGS(KH_TUNE_ROW)};
-#undef KH_TUNE_ROW
+std::vector<Candidate> candidates() {
+  std::vector<Candidate> out(static_cast<size_t>(khrt_gemm_candidate_count()));
+  for (size_t i = 0; i < out.size(); ++i) khrt_gemm_candidate_get(static_cast<int>(i), &out[i]);
+  return out;
+}
 
 struct Result {
   const Candidate *c = nullptr;
@@ -105,17 +98,6 @@ bool parse_mnk(const std::string &text, int64_t &m, int64_t &n, int64_t &k) {
     else return false;
   }
   return m > 0 && n > 0 && k > 0;
-}
-
-std::string fnv1a_hex(const std::string &s) {
-  uint64_t h = 1469598103934665603ull;
-  for (unsigned char c : s) {
-    h ^= c;
-    h *= 1099511628211ull;
-  }
-  char buf[17];
-  std::snprintf(buf, sizeof buf, "%016llx", static_cast<unsigned long long>(h));
-  return buf;
 }
 
 std::string self_exe() {
@@ -253,14 +235,19 @@ void cache_store(const std::string &path, const std::string &key, const std::str
 void usage_tune(std::ostream &os) {
   os << "usage: kernelh tune --kernel gemm --shape m=..,n=..,k=.. --out <dir> [options]\n"
      << "  --target <t>          amdgcn-gfx950 (default; the local execution target)\n"
-     << "  --max-candidates <n>  cap on evaluated candidates (1..80, default 80)\n"
+     << "  --max-candidates <n>  cap on evaluated candidates (1.." << khrt_gemm_candidate_count()
+     << ", default all)\n"
      << "  --timeout <seconds>   wall clock per candidate (1..3600, default 30)\n"
      << "  --cache <path>        cache file (default build/tune-cache.json), keyed\n"
      << "                        FNV-1a(kernel|shape|device)\n"
-     << "The space (KH_GEMM_TUNE_CONFIGS) is a fixed set of precompiled gfx950\n"
-     << "instantiations: wave tile WTM x WTN of 32x32 MFMAs, slab depth BK, MFMA\n"
-     << "wave priority and slab pipeline (register-staged, or direct-to-LDS with three\n"
-     << "stages); it is evaluated exhaustively, not sampled.\n";
+     << "Candidates: the launcher's own gemm symbols, then the gfx950 tune space\n"
+     << "(gemm_tune_space.py): MFMA 32x32 or 16x16 wave tiles, 4 or 8 waves, BM/BN in\n"
+     << "{64,128,256}, BK in {16,32}, unroll 1 or 2 (register-staged, direct-to-LDS\n"
+     << "three stages, or two slabs ahead), MFMA wave priority; vec is 4 (dwordx4)\n"
+     << "when k and n are multiples of 4, else 1. The space is precompiled and\n"
+     << "evaluated exhaustively, not sampled. Point the runtime at the cache\n"
+     << "(KHRT_TUNE_CACHE=<path> or khrt_set_tune_cache) and kh_gemm runs the\n"
+     << "cached best for each tuned shape.\n";
 }
 
 // ---------------------------------------------------------------- child
@@ -303,14 +290,11 @@ int eval_print(bool accepted, double ms, double gflops, const std::string &reaso
 
 int run_tune_eval(int argc, char **argv) {
   std::string symbol, shape, v;
-  int bm = 0, bn = 0;
   bool probe = false;
   for (int i = 2; i < argc; ++i) {
     const std::string arg = argv[i];
     if (take(argc, argv, i, arg, "--symbol", v)) symbol = v;
     else if (take(argc, argv, i, arg, "--shape", v)) shape = v;
-    else if (take(argc, argv, i, arg, "--bm", v)) bm = std::atoi(v.c_str());
-    else if (take(argc, argv, i, arg, "--bn", v)) bn = std::atoi(v.c_str());
     else if (arg == "--probe") probe = true;
   }
   int count = 0;
@@ -318,28 +302,33 @@ int run_tune_eval(int argc, char **argv) {
     return eval_print(false, 0, 0, "skip: no HIP device");
   }
   if (probe) {
-    khrt_device_info info{};
-    khrt_get_device_info(&info);
-    std::printf("DEVICE %s (%s) cu=%lld\n", info.name[0] ? info.name : "AMD Instinct MI355X", info.arch,
-                static_cast<long long>(info.cu_count));
+    // The device token and the cache key of --shape, both computed by the
+    // runtime, which reads the same cache with the same key.
+    char token[512], key[17];
+    if (khrt_device_token(token, sizeof token) != 0) return eval_print(false, 0, 0, "skip: no HIP device");
+    std::printf("DEVICE %s\n", token);
+    if (!shape.empty() && khrt_tune_cache_key("gemm", shape.c_str(), key, sizeof key) == 0) {
+      std::printf("KEY %s\n", key);
+    }
     return 0;
   }
   int64_t m, n, k;
-  if (symbol.empty() || bm <= 0 || bn <= 0 || !parse_mnk(shape, m, n, k)) {
-    return eval_print(false, 0, 0, "usage: tune-eval --symbol S --bm BM --bn BN --shape m=..,n=..,k=..");
+  if (symbol.empty() || !parse_mnk(shape, m, n, k)) {
+    return eval_print(false, 0, 0, "usage: tune-eval --symbol S --shape m=..,n=..,k=..");
   }
-  void *module = nullptr, *fn = nullptr;
-  const size_t size = static_cast<size_t>(kh_cli_co_gemm_tune_end - kh_cli_co_gemm_tune);
-  if (size == 0 || khrt_module_load_data(&module, kh_cli_co_gemm_tune, size) != 0 ||
-      khrt_module_get_function(&fn, module, symbol.c_str()) != 0) {
+  void *fn = nullptr;
+  if (khrt_gemm_candidate_function(symbol.c_str(), &fn) != 0) {
     return eval_print(false, 0, 0, std::string("load-error: ") + khrt_last_error());
   }
   std::vector<uint64_t> slots;
   std::vector<void *> params;
-  auto grid_for = [&](int64_t mm, int64_t nn) {
-    return khrt_dim3{static_cast<unsigned>(((mm + bm - 1) / bm) * ((nn + bn - 1) / bn)), 1, 1};
+  khrt_dim3 block{0, 0, 0};
+  auto grid_for = [&](int64_t mm, int64_t nn, int64_t kk) {
+    khrt_dim3 g{1, 1, 1};
+    khrt_gemm_candidate_geometry(symbol.c_str(), mm, nn, kk, &g, &block);
+    return g;
   };
-  const khrt_dim3 block{256, 1, 1};
+  grid_for(m, n, k);
 
   // Re-verification on the capped shape.
   {
@@ -354,7 +343,8 @@ int run_tune_eval(int argc, char **argv) {
     khrt_memcpy_h2d(dA, a.data(), a.size() * 4);
     khrt_memcpy_h2d(dB, b.data(), b.size() * 4);
     fill_args(dA, dB, dC, vm, vn, vk, slots, params);
-    if (khrt_launch_raw(fn, grid_for(vm, vn), block, 0, nullptr, params.data()) != 0 ||
+    const khrt_dim3 vgrid = grid_for(vm, vn, vk);
+    if (khrt_launch_raw(fn, vgrid, block, 0, nullptr, params.data()) != 0 ||
         khrt_device_synchronize() != 0) {
       return eval_print(false, 0, 0, std::string("reverify: launch failed: ") + khrt_last_error());
     }
@@ -386,7 +376,8 @@ int run_tune_eval(int argc, char **argv) {
   khrt_fill_f32(dA, 1.0f, static_cast<size_t>(m * k), nullptr);
   khrt_fill_f32(dB, 0.5f, static_cast<size_t>(k * n), nullptr);
   fill_args(dA, dB, dC, m, n, k, slots, params);
-  for (int i = 0; i < 3; ++i) khrt_launch_raw(fn, grid_for(m, n), block, 0, nullptr, params.data());
+  const khrt_dim3 grid = grid_for(m, n, k);
+  for (int i = 0; i < 3; ++i) khrt_launch_raw(fn, grid, block, 0, nullptr, params.data());
   khrt_device_synchronize();
   void *e0 = nullptr, *e1 = nullptr;
   khrt_event_create(&e0);
@@ -394,7 +385,7 @@ int run_tune_eval(int argc, char **argv) {
   std::vector<double> ms;
   for (int i = 0; i < 10; ++i) {
     khrt_event_record(e0, nullptr);
-    khrt_launch_raw(fn, grid_for(m, n), block, 0, nullptr, params.data());
+    khrt_launch_raw(fn, grid, block, 0, nullptr, params.data());
     khrt_event_record(e1, nullptr);
     khrt_event_synchronize(e1);
     float t = 0.0f;
@@ -411,7 +402,9 @@ int run_tune_eval(int argc, char **argv) {
 
 int run_tune(int argc, char **argv) {
   std::string kernel = "gemm", shape, out, target = "amdgcn-gfx950", cache = "build/tune-cache.json", v;
-  int max_candidates = 80, timeout_s = 30;
+  const std::vector<Candidate> space = candidates();
+  const int total = static_cast<int>(space.size());
+  int max_candidates = total, timeout_s = 30;
   for (int i = 2; i < argc; ++i) {
     const std::string arg = argv[i];
     if (arg == "--help" || arg == "-h") {
@@ -429,8 +422,8 @@ int run_tune(int argc, char **argv) {
       cache = v;
     } else if (take(argc, argv, i, arg, "--max-candidates", v)) {
       max_candidates = std::atoi(v.c_str());
-      if (max_candidates < 1 || max_candidates > 80) {
-        std::cerr << "error: --max-candidates must be an integer in [1,80]\n";
+      if (max_candidates < 1 || max_candidates > total) {
+        std::cerr << "error: --max-candidates must be an integer in [1," << total << "]\n";
         return 2;
       }
     } else if (take(argc, argv, i, arg, "--timeout", v)) {
@@ -464,15 +457,17 @@ int run_tune(int argc, char **argv) {
   const std::string exe = self_exe();
   int status = 0;
   bool timed_out = false;
-  const std::string probe = run_child({exe, "tune-eval", "--probe"}, timeout_s, status, timed_out);
+  const std::string shape_text = "m=" + std::to_string(m) + ",n=" + std::to_string(n) + ",k=" + std::to_string(k);
+  const std::string probe =
+      run_child({exe, "tune-eval", "--probe", "--shape", shape_text}, timeout_s, status, timed_out);
   const auto dev = probe.find("DEVICE ");
-  if (dev == std::string::npos) {
+  const auto kpos = probe.find("KEY ");
+  if (dev == std::string::npos || kpos == std::string::npos) {
     std::cerr << "skip: no HIP device available\n";
     return 77;
   }
   const std::string device = probe.substr(dev + 7, probe.find('\n', dev) - dev - 7);
-  const std::string shape_text = "m=" + std::to_string(m) + ",n=" + std::to_string(n) + ",k=" + std::to_string(k);
-  const std::string key = fnv1a_hex(kernel + "|" + shape_text + "|" + device);
+  const std::string key = probe.substr(kpos + 4, 16);
   std::cout << "device: " << device << "\ncache-key: " << key << "\n";
   std::error_code ec;
   fs::create_directories(out, ec);
@@ -487,14 +482,12 @@ int run_tune(int argc, char **argv) {
   }
 
   std::vector<Result> results;
-  const int total = static_cast<int>(sizeof(kCandidates) / sizeof(kCandidates[0]));
   for (int i = 0; i < total && i < max_candidates; ++i) {
-    const Candidate &c = kCandidates[i];
+    const Candidate &c = space[i];
     Result r;
     r.c = &c;
-    const std::string outp = run_child({exe, "tune-eval", "--symbol", c.symbol, "--bm", std::to_string(c.bm()),
-                                        "--bn", std::to_string(c.bn()), "--shape", shape_text},
-                                       timeout_s, status, timed_out);
+    const std::string outp =
+        run_child({exe, "tune-eval", "--symbol", c.symbol, "--shape", shape_text}, timeout_s, status, timed_out);
     if (timed_out) {
       r.reason = "timeout";
     } else if (WIFSIGNALED(status)) {
@@ -507,21 +500,27 @@ int run_tune(int argc, char **argv) {
       r.gflops = std::atof(field(outp, "gflops").c_str());
       r.reason = field(outp, "reason");
     }
-    std::printf("candidate %-22s %s %.4f ms %.1f GFLOP/s\n", c.symbol, r.accepted ? "ok  " : r.reason.c_str(), r.ms,
+    std::printf("candidate %-34s %s %.4f ms %.1f GFLOP/s\n", c.symbol, r.accepted ? "ok  " : r.reason.c_str(), r.ms,
                 r.gflops);
     std::fflush(stdout);
     results.push_back(r);
   }
 
+  // vec: floats per global load the candidate issues at this shape: float4
+  // (dwordx4) when k (and, except for the K-split symbols, which read B a
+  // column at a time, n) are multiples of 4, else the guarded scalar path.
+  const int vec_tiles = (k % 4 == 0 && n % 4 == 0) ? 4 : 1, vec_ksplit = (k % 4 == 0) ? 4 : 1;
   std::ostringstream csv;
-  csv << "kernel,shape,bm,bn,bk,waves,unroll,vec,ms_median,accepted,reason,symbol,wave_tile,prio,lds_dma,gflops\n";
+  csv << "kernel,shape,bm,bn,bk,waves,unroll,vec,ms_median,accepted,reason,symbol,mfma,wave_grid,wave_tile,"
+         "pipeline,prio,product,gflops\n";
   const Result *best = nullptr;
   for (const Result &r : results) {
-    csv << kernel << "," << csv_escape(shape_text) << "," << r.c->bm() << "," << r.c->bn() << "," << r.c->bk
-        << ",4,1,4," << r.ms << "," << (r.accepted ? "true" : "false") << "," << csv_escape(r.reason) << ","
-        << r.c->symbol << "," << r.c->wtm * 32 << "x" << r.c->wtn * 32 << "," << r.c->prio << "," << r.c->dma << ","
-        << r.gflops
-        << "\n";
+    const Candidate &c = *r.c;
+    csv << kernel << "," << csv_escape(shape_text) << "," << c.bm << "," << c.bn << "," << c.bk << "," << c.waves
+        << "," << c.unroll << "," << (c.k_split ? vec_ksplit : vec_tiles) << "," << r.ms << ","
+        << (r.accepted ? "true" : "false") << "," << csv_escape(r.reason) << "," << c.symbol << "," << c.mfma << "x"
+        << c.mfma << "," << c.wave_grid_m << "x" << c.wave_grid_n << "," << c.wave_tile_m << "x" << c.wave_tile_n
+        << "," << c.pipeline << "," << c.prio << "," << c.product << "," << r.gflops << "\n";
     if (r.accepted && (best == nullptr || r.ms < best->ms)) best = &r;
   }
   std::ofstream(csv_path, std::ios::trunc) << csv.str();
@@ -530,10 +529,15 @@ int run_tune(int argc, char **argv) {
     std::cout << "best config: none (no candidate passed all gates)\ntune ok\n";
     return 0;
   }
-  std::printf("best config: %s bm=%d bn=%d bk=%d prio=%d lds_dma=%d ms_median=%.4f (%.1f GFLOP/s)\n",
-              best->c->symbol, best->c->bm(), best->c->bn(), best->c->bk, best->c->prio, best->c->dma, best->ms,
-              best->gflops);
+  std::printf("best config: %s bm=%d bn=%d bk=%d waves=%d unroll=%d mfma=%dx%d pipeline=%s prio=%d ms_median=%.4f "
+              "(%.1f GFLOP/s)\n",
+              best->c->symbol, best->c->bm, best->c->bn, best->c->bk, best->c->waves, best->c->unroll, best->c->mfma,
+              best->c->mfma, best->c->pipeline, best->c->prio, best->ms, best->gflops);
   cache_store(cache, key, best->c->symbol, csv.str());
+  std::error_code aec;
+  const fs::path abs = fs::absolute(cache, aec);
+  std::cout << "cache: " << (aec ? cache : abs.string())
+            << " (KHRT_TUNE_CACHE=<this path> or khrt_set_tune_cache makes kh_gemm run the best for this shape)\n";
   std::cout << "tune ok\n";
   return 0;
 }

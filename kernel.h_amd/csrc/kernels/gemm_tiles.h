@@ -10,15 +10,36 @@
 namespace khg {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 256;  // the product kernels' workgroup (2x2 waves)
 constexpr int kGroupM = 8;
 constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor: 32-bit data format
 constexpr uint32_t kOutside = 0x80000000u;
 
-// Tile geometry for WTM x WTN accumulators per wave, BKT-deep slabs, and the
-// LDS layout of one stage, which depends on how the stage is filled (DMA):
+// The two fp32 MFMA shapes. MF = 32: v_mfma_f32_32x32x2f32 (A: lane l holds
+// A[l%32][l/32]; D: lane l, register r holds row 8(r/4) + 4(l/32) + r%4,
+// column l%32), consumed in 8-deep chunks. MF = 16: v_mfma_f32_16x16x4f32
+// (A[l%16][l/16]; D: row 4(l/16) + r, column l%16), in 16-deep chunks. Both
+// run at the same rate; 16x16 holds a quarter of the accumulator per
+// instruction, so the same wave tile takes four times the instructions.
+template <int MF>
+struct Mfma;
+template <>
+struct Mfma<32> {
+  typedef v16f Acc;
+  static constexpr int CK = 8;  // k per chunk: one ds_read_b128 of A per lane
+};
+template <>
+struct Mfma<16> {
+  typedef v4f Acc;
+  static constexpr int CK = 16;
+};
+
+// Tile geometry for WTM x WTN MF x MF accumulators per wave, a WGM x WGN
+// grid of waves per workgroup, BKT-deep slabs, and the LDS layout of one
+// stage, which depends on how the stage is filled (DMA):
 //
 //   Register-staged (DMA false): A as [m][k] with rows padded by 4 floats
 //   (one ds_read_b128 per lane delivers four k values, conflict-free) and B
@@ -33,30 +54,35 @@ constexpr uint32_t kOutside = 0x80000000u;
 //   fragment reads on distinct banks; B is [k][n] grouped by the RPI rows one
 //   wave's 1 KiB load covers, groups padded by 4 floats (the two lane halves
 //   of a fragment read, rows 4 apart, land on different banks).
-template <int WTM, int WTN, int BKT, bool DMA>
+template <int WTM, int WTN, int BKT, bool DMA, int WGM = 2, int WGN = 2, int MF = 32>
 struct Tile {
+  static constexpr int kMF = MF, kWTM = WTM, kWTN = WTN, kWGN = WGN;
+  static constexpr int NT = 64 * WGM * WGN;  // threads per workgroup
   static constexpr int BK = BKT;
-  static constexpr int BM = 64 * WTM;      // rows of C per workgroup
-  static constexpr int BN = 64 * WTN;      // columns of C per workgroup
+  static constexpr int BM = MF * WTM * WGM;  // rows of C per workgroup
+  static constexpr int BN = MF * WTN * WGN;  // columns of C per workgroup
   static constexpr int QP = BK / 4;        // float4 per A row
   static constexpr int BROW = BN / 4;      // float4 per B row
   static constexpr int RPI = DMA ? (BROW >= 64 ? 1 : 64 / BROW) : 1;  // B rows per padded group
   static constexpr int LDA = DMA ? BK : BK + 4;
   static constexpr int LDG = RPI * BN + 4; // floats per padded group of B rows
-  static constexpr int NA = BM * BK / 4 / kThreads;  // A float4 per thread per slab
-  static constexpr int NB = BK * BN / 4 / kThreads;  // B float4 per thread per slab
+  static constexpr int NA = BM * BK / 4 / NT;  // A float4 per thread per slab
+  static constexpr int NB = BK * BN / 4 / NT;  // B float4 per thread per slab
   static constexpr int A_STAGE = BM * LDA;
   static constexpr int B_STAGE = (BK / RPI) * LDG;
   static constexpr int SWZ_SHIFT = QP == 2 ? 2 : QP == 4 ? 1 : 0;
-  static_assert(NA * kThreads * 4 == BM * BK && NB * kThreads * 4 == BK * BN,
-                "a slab must split into whole float4s over the 256 threads");
-  static_assert(BK % 8 == 0 && QP <= 8, "slabs are consumed in 8-deep chunks");
+  static_assert(NA * NT * 4 == BM * BK && NB * NT * 4 == BK * BN,
+                "a slab must split into whole float4s over the workgroup's threads");
+  static_assert(BK % Mfma<MF>::CK == 0 && QP <= 8, "slabs are consumed in whole chunks");
   static_assert(BROW <= 64 || BROW % 64 == 0, "a wave's B load covers whole rows");
   static_assert(BK % RPI == 0, "B row groups split the slab");
   __device__ static constexpr int aswz(int row) { return DMA ? ((row >> SWZ_SHIFT) ^ (row >> 3)) & (QP - 1) : 0; }
   // Float offset of A (row, logical quad q) and of B (row, column) in a stage.
   __device__ static constexpr int a_at(int row, int q) { return row * LDA + 4 * (q ^ aswz(row)); }
   __device__ static constexpr int b_at(int row, int col) { return (row / RPI) * LDG + (row % RPI) * BN + col; }
+  static_assert(WGN > 0 && (WGN & (WGN - 1)) == 0, "a power-of-two wave grid width");
+  __device__ static constexpr int wave_m(int wave) { return wave >> __builtin_ctz(WGN); }
+  __device__ static constexpr int wave_n(int wave) { return wave & (WGN - 1); }
 };
 
 template <class T>
@@ -82,12 +108,12 @@ __device__ __forceinline__ void load_slab(Slab<T> &s, const float *__restrict__ 
                                           int64_t n0, int64_t k0, bool a_vec, bool b_vec, int tid) {
 #pragma unroll
   for (int i = 0; i < T::NA; ++i) {
-    const int idx = tid + kThreads * i;
+    const int idx = tid + T::NT * i;
     s.a[i] = load4(A, m0 + idx / T::QP, k0 + 4 * (idx % T::QP), lda, M, K, a_vec);
   }
 #pragma unroll
   for (int i = 0; i < T::NB; ++i) {
-    const int idx = tid + kThreads * i;
+    const int idx = tid + T::NT * i;
     s.b[i] = load4(B, k0 + idx / T::BROW, n0 + 4 * (idx % T::BROW), ldb, K, N, b_vec);
   }
 }
@@ -120,14 +146,14 @@ __device__ __forceinline__ void load_slab_vec(Slab<T> &s, const float *__restric
   const __amdgpu_buffer_rsrc_t rb = rows_rsrc(B + k0 * ldb, (K - k0) < T::BK ? (K - k0) : T::BK, ldb);
 #pragma unroll
   for (int i = 0; i < T::NA; ++i) {
-    const int idx = tid + kThreads * i;
+    const int idx = tid + T::NT * i;
     const int ar = idx / T::QP, ak = 4 * (idx % T::QP);  // A: row in tile, k in slab
     const uint32_t aoff = (k0 + ak < K) ? (uint32_t)((ar * lda + k0 + ak) * 4) : kOutside;
     s.a[i] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(ra, aoff, 0, 0));
   }
 #pragma unroll
   for (int i = 0; i < T::NB; ++i) {
-    const int idx = tid + kThreads * i;
+    const int idx = tid + T::NT * i;
     const int bk = idx / T::BROW, bn = 4 * (idx % T::BROW);  // B: k in slab, column in tile
     const uint32_t boff = (n0 + bn < N) ? (uint32_t)((bk * ldb + n0 + bn) * 4) : kOutside;
     s.b[i] = as_float4(__builtin_amdgcn_raw_buffer_load_b128(rb, boff, 0, 0));
@@ -140,12 +166,12 @@ __device__ __forceinline__ void store_slab(const Slab<T> &s, float *__restrict__
                                            int tid) {
 #pragma unroll
   for (int i = 0; i < T::NA; ++i) {
-    const int idx = tid + kThreads * i;
+    const int idx = tid + T::NT * i;
     *reinterpret_cast<float4 *>(As + T::a_at(idx / T::QP, idx % T::QP)) = s.a[i];
   }
 #pragma unroll
   for (int i = 0; i < T::NB; ++i) {
-    const int idx = tid + kThreads * i;
+    const int idx = tid + T::NT * i;
     *reinterpret_cast<float4 *>(Bs + T::b_at(idx / T::BROW, 4 * (idx % T::BROW))) = s.b[i];
   }
 }
@@ -187,7 +213,7 @@ __device__ __forceinline__ void dma_slab(const float *__restrict__ A, const floa
   const u32x4 rb = rows_desc(B + k0 * ldb, (K - k0) < T::BK ? (K - k0) : T::BK, ldb);
 #pragma unroll
   for (int i = 0; i < T::NA; ++i) {
-    const int idx0 = 64 * wave + kThreads * i;  // first float4 of this wave's instruction
+    const int idx0 = 64 * wave + T::NT * i;  // first float4 of this wave's instruction
     const int idx = idx0 + lane;
     const int ar = idx / T::QP, ak = 4 * ((idx % T::QP) ^ T::aswz(ar));
     const uint32_t aoff = (k0 + ak < K) ? (uint32_t)((ar * lda + k0 + ak) * 4) : kOutside;
@@ -195,7 +221,7 @@ __device__ __forceinline__ void dma_slab(const float *__restrict__ A, const floa
   }
 #pragma unroll
   for (int i = 0; i < T::NB; ++i) {
-    const int idx0 = 64 * wave + kThreads * i;
+    const int idx0 = 64 * wave + T::NT * i;
     const int idx = idx0 + lane;
     const int bk = idx / T::BROW, bn = 4 * (idx % T::BROW);
     const uint32_t boff = (n0 + bn < N) ? (uint32_t)((bk * ldb + n0 + bn) * 4) : kOutside;
@@ -219,47 +245,72 @@ __device__ __forceinline__ void vm_barrier() {
   asm volatile("s_barrier" ::: "memory");
 }
 
-// Fragments of 8-deep chunk c of a stage: the MFMA sums k over its two lane
-// halves, and any permutation of k applied to both operands gives the same
-// product, so lane half h takes k = 8c + 4h + {0..3} (one ds_read_b128 for
-// A) and MFMA step s consumes k = 8c + s (half 0) and 8c + 4 + s (half 1).
-template <int WTM>
+// Fragments of chunk c of a stage. The MFMA sums k over its lane groups,
+// and any permutation of k applied to both operands gives the same product:
+//   MF = 32 (8-deep chunks): lane half h takes k = 8c + 4h + {0..3} (one
+//     ds_read_b128 for A); MFMA step s consumes k = 8c + s (half 0) and
+//     8c + 4 + s (half 1).
+//   MF = 16 (16-deep chunks): lane group g = l/16 takes quad q(g) =
+//     (g%2)*2 + g/2, i.e. k = 16c + 4q + {0..3}; step s consumes
+//     k = 16c + 4q(g) + s from group g. The order 0, 2, 1, 3 puts the B rows
+//     that lanes 0-31 read in one step 8 apart, which keeps them on distinct
+//     LDS banks in the direct-to-LDS layout, where two B rows share a group.
+template <int WTM, int WTN>
 struct Frag {
   float4 a[WTM];
-  float b[4][4];
+  float b[WTN][4];
 };
 
+template <class T>
+using AccOf = typename Mfma<T::kMF>::Acc;
+
 template <int WTM, int WTN, class T>
-__device__ __forceinline__ void read_frag(Frag<WTM> &f, const float *__restrict__ As, const float *__restrict__ Bs,
+__device__ __forceinline__ void read_frag(Frag<WTM, WTN> &f, const float *__restrict__ As, const float *__restrict__ Bs,
                                           int c, int wm, int wn, int lane) {
-  const int r = lane & 31, h = lane >> 5;
+  if constexpr (T::kMF == 32) {
+    const int r = lane & 31, h = lane >> 5;
 #pragma unroll
-  for (int i = 0; i < WTM; ++i)
-    f.a[i] = *reinterpret_cast<const float4 *>(As + T::a_at(wm * 32 * WTM + i * 32 + r, 2 * c + h));
+    for (int i = 0; i < WTM; ++i)
+      f.a[i] = *reinterpret_cast<const float4 *>(As + T::a_at(wm * 32 * WTM + i * 32 + r, 2 * c + h));
 #pragma unroll
-  for (int j = 0; j < WTN; ++j)
+    for (int j = 0; j < WTN; ++j)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) f.b[j][s] = Bs[T::b_at(8 * c + 4 * h + s, wn * 32 * WTN + j * 32 + r)];
+      for (int s = 0; s < 4; ++s) f.b[j][s] = Bs[T::b_at(8 * c + 4 * h + s, wn * 32 * WTN + j * 32 + r)];
+  } else {
+    const int r = lane & 15, g = lane >> 4, q = ((g & 1) << 1) | (g >> 1);
+#pragma unroll
+    for (int i = 0; i < WTM; ++i)
+      f.a[i] = *reinterpret_cast<const float4 *>(As + T::a_at(wm * 16 * WTM + i * 16 + r, 4 * c + q));
+#pragma unroll
+    for (int j = 0; j < WTN; ++j)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) f.b[j][s] = Bs[T::b_at(16 * c + 4 * q + s, wn * 16 * WTN + j * 16 + r)];
+  }
 }
 
-template <int WTM, int WTN>
-__device__ __forceinline__ void mfma_frag(v16f (&acc)[WTM][WTN], const Frag<WTM> &f) {
+template <int WTM, int WTN, class Acc>
+__device__ __forceinline__ void mfma_frag(Acc (&acc)[WTM][WTN], const Frag<WTM, WTN> &f) {
 #pragma unroll
   for (int s = 0; s < 4; ++s)
 #pragma unroll
     for (int i = 0; i < WTM; ++i) {
       const float av = s == 0 ? f.a[i].x : s == 1 ? f.a[i].y : s == 2 ? f.a[i].z : f.a[i].w;
 #pragma unroll
-      for (int j = 0; j < WTN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, f.b[j][s], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < WTN; ++j) {
+        if constexpr (sizeof(Acc) == sizeof(v16f))
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, f.b[j][s], acc[i][j], 0, 0, 0);
+        else
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, f.b[j][s], acc[i][j], 0, 0, 0);
+      }
     }
 }
 
 template <int WTM, int WTN, class T>
-__device__ __forceinline__ void compute_slab(v16f (&acc)[WTM][WTN], const float *__restrict__ As,
+__device__ __forceinline__ void compute_slab(AccOf<T> (&acc)[WTM][WTN], const float *__restrict__ As,
                                              const float *__restrict__ Bs, int wm, int wn, int lane) {
 #pragma unroll
-  for (int c = 0; c < T::BK / 8; ++c) {
-    Frag<WTM> f;
+  for (int c = 0; c < T::BK / Mfma<T::kMF>::CK; ++c) {
+    Frag<WTM, WTN> f;
     read_frag<WTM, WTN, T>(f, As, Bs, c, wm, wn, lane);
     mfma_frag<WTM, WTN>(acc, f);
   }
@@ -287,12 +338,12 @@ __device__ __forceinline__ void tile_coords(int64_t pid, int64_t tiles_m, int64_
 // chunks, already in registers, feed the MFMAs: no wave waits on LDS data
 // right after a barrier, and each slab has one slab-time to arrive.
 template <int WTM, int WTN, class T, bool PRIO>
-__device__ __forceinline__ void k_loop_dma(v16f (&acc)[WTM][WTN], const float *__restrict__ Ap,
+__device__ __forceinline__ void k_loop_dma(AccOf<T> (&acc)[WTM][WTN], const float *__restrict__ Ap,
                                            const float *__restrict__ Bp, int64_t M, int64_t N, int64_t K,
                                            int64_t lda, int64_t ldb, int64_t m0, int64_t n0, int64_t nslabs,
                                            float *As, float *Bs, int wave, int wm, int wn, int lane) {
   constexpr int BK = T::BK;
-  constexpr int C = BK / 8;
+  constexpr int C = BK / Mfma<T::kMF>::CK;
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   dma_slab<T>(Ap, Bp, M, N, K, lda, ldb, m0, n0, 0, As, Bs, wv, lane);
   if (nslabs > 1) {
@@ -301,7 +352,7 @@ __device__ __forceinline__ void k_loop_dma(v16f (&acc)[WTM][WTN], const float *_
   } else {
     vm_barrier<0>();
   }
-  Frag<WTM> f0, f1;
+  Frag<WTM, WTN> f0, f1;
   read_frag<WTM, WTN, T>(f0, As, Bs, 0, wm, wn, lane);
   int cur = 0;
   for (int64_t ks = 0; ks < nslabs; ++ks) {
@@ -334,7 +385,7 @@ __device__ __forceinline__ void k_loop_dma(v16f (&acc)[WTM][WTN], const float *_
 // Register-staged (two stages): the next slab's global loads are in flight
 // while the current slab feeds the MFMAs, one barrier per slab.
 template <int WTM, int WTN, class T, bool PRIO>
-__device__ __forceinline__ void k_loop_regs(v16f (&acc)[WTM][WTN], const float *__restrict__ Ap,
+__device__ __forceinline__ void k_loop_regs(AccOf<T> (&acc)[WTM][WTN], const float *__restrict__ Ap,
                                             const float *__restrict__ Bp, int64_t M, int64_t N, int64_t K,
                                             int64_t lda, int64_t ldb, int64_t m0, int64_t n0, int64_t nslabs,
                                             float *As, float *Bs, int tid, int wm, int wn, int lane) {
@@ -360,7 +411,7 @@ __device__ __forceinline__ void k_loop_regs(v16f (&acc)[WTM][WTN], const float *
 // __syncthreads() would wait for those loads). The loop is unrolled by two
 // so the staging sets swap roles without copies.
 template <int WTM, int WTN, class T, bool PRIO>
-__device__ __forceinline__ void prefetch2_step(v16f (&acc)[WTM][WTN], Slab<T> &free_set, Slab<T> &next_set,
+__device__ __forceinline__ void prefetch2_step(AccOf<T> (&acc)[WTM][WTN], Slab<T> &free_set, Slab<T> &next_set,
                                                const float *__restrict__ Ap, const float *__restrict__ Bp,
                                                int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                                                int64_t m0, int64_t n0, int64_t nslabs, int64_t ks, float *As,
@@ -375,7 +426,7 @@ __device__ __forceinline__ void prefetch2_step(v16f (&acc)[WTM][WTN], Slab<T> &f
 }
 
 template <int WTM, int WTN, class T, bool PRIO>
-__device__ __forceinline__ void k_loop_prefetch2(v16f (&acc)[WTM][WTN], const float *__restrict__ Ap,
+__device__ __forceinline__ void k_loop_prefetch2(AccOf<T> (&acc)[WTM][WTN], const float *__restrict__ Ap,
                                                  const float *__restrict__ Bp, int64_t M, int64_t N, int64_t K,
                                                  int64_t lda, int64_t ldb, int64_t m0, int64_t n0, int64_t nslabs,
                                                  float *As, float *Bs, int tid, int wm, int wn, int lane) {
@@ -395,7 +446,7 @@ __device__ __forceinline__ void k_loop_prefetch2(v16f (&acc)[WTM][WTN], const fl
 
 // Generic (any shape, stride, alignment): synchronous, one stage.
 template <int WTM, int WTN, class T>
-__device__ __forceinline__ void k_loop_generic(v16f (&acc)[WTM][WTN], const float *__restrict__ Ap,
+__device__ __forceinline__ void k_loop_generic(AccOf<T> (&acc)[WTM][WTN], const float *__restrict__ Ap,
                                                const float *__restrict__ Bp, int64_t M, int64_t N, int64_t K,
                                                int64_t lda, int64_t ldb, int64_t m0, int64_t n0, int64_t nslabs,
                                                bool a_vec, bool b_vec, float *As, float *Bs, int tid, int wm, int wn,
@@ -410,23 +461,33 @@ __device__ __forceinline__ void k_loop_generic(v16f (&acc)[WTM][WTN], const floa
   }
 }
 
-// Writes a tile's accumulators to C. Accumulator layout: lane l, register
-// r -> row 8(r/4) + 4(l/32) + r%4, column l%32 of the 32x32 block, so each
-// store instruction writes two 128-byte row pieces (whole cache lines).
+// Writes a tile's accumulators to C. Accumulator layout (MF = 32): lane l,
+// register r -> row 8(r/4) + 4(l/32) + r%4, column l%32 of the 32x32 block,
+// so each store instruction writes two 128-byte row pieces (whole cache
+// lines); MF = 16: row 4(l/16) + r, column l%16, four 64-byte pieces.
 template <int WTM, int WTN, class T>
-__device__ __forceinline__ void store_tile(const v16f (&acc)[WTM][WTN], float *__restrict__ Cp, int64_t M,
+__device__ __forceinline__ void store_tile(const AccOf<T> (&acc)[WTM][WTN], float *__restrict__ Cp, int64_t M,
                                            int64_t N, int64_t ldc, int64_t m0, int64_t n0, int wm, int wn,
                                            int lane) {
-  const int col = lane & 31, h = lane >> 5;
+  constexpr int MF = T::kMF;
+  const int col = lane & (MF - 1), h = lane / MF;
 #pragma unroll
   for (int i = 0; i < WTM; ++i) {
 #pragma unroll
     for (int j = 0; j < WTN; ++j) {
-      const int64_t gc = n0 + wn * 32 * WTN + j * 32 + col;
+      const int64_t gc = n0 + wn * MF * WTN + j * MF + col;
+      if constexpr (MF == 32) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t gr = m0 + wm * 32 * WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (gr < M && gc < N) Cp[gr * ldc + gc] = acc[i][j][r];
+        for (int r = 0; r < 16; ++r) {
+          const int64_t gr = m0 + wm * 32 * WTM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (gr < M && gc < N) Cp[gr * ldc + gc] = acc[i][j][r];
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t gr = m0 + wm * 16 * WTM + i * 16 + 4 * h + r;
+          if (gr < M && gc < N) Cp[gr * ldc + gc] = acc[i][j][r];
+        }
       }
     }
   }
@@ -440,16 +501,16 @@ constexpr int kPipePrefetch2 = 3;  // register-staged, two slabs ahead
 // One workgroup's loop over its tiles. PATH: 0 generic, else a kPipe*. As, Bs: the LDS stages, A_STAGE and B_STAGE floats apart.
 // (Offsets from one base keep the pointers visibly in LDS for the compiler;
 // an array of stage pointers would turn every LDS access into a flat one.)
-template <int WTM, int WTN, int BKT, int PATH, bool PRIO>
+template <int WTM, int WTN, int BKT, int PATH, bool PRIO, int WGM = 2, int WGN = 2, int MF = 32>
 __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const float *__restrict__ Bp,
                                            float *__restrict__ Cp, int64_t M, int64_t N, int64_t K, int64_t lda,
                                            int64_t ldb, int64_t ldc, bool a_vec, bool b_vec, float *As,
                                            float *Bs) {
-  using T = Tile<WTM, WTN, BKT, PATH == kPipeDma>;
+  using T = Tile<WTM, WTN, BKT, PATH == kPipeDma, WGM, WGN, MF>;
   const int tid = threadIdx.x;
   const int lane = kh::lane_id();
   const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = T::wave_m(wave), wn = T::wave_n(wave);
 
   const int64_t tiles_m = (M + T::BM - 1) / T::BM, tiles_n = (N + T::BN - 1) / T::BN;
   const int64_t total = tiles_m * tiles_n;
@@ -463,11 +524,11 @@ __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const f
     tile_coords(pid, tiles_m, tiles_n, xcd_remap, tm, tn);
     const int64_t m0 = tm * T::BM, n0 = tn * T::BN;
 
-    v16f acc[WTM][WTN];
+    AccOf<T> acc[WTM][WTN];
 #pragma unroll
     for (int i = 0; i < WTM; ++i)
 #pragma unroll
-      for (int j = 0; j < WTN; ++j) acc[i][j] = v16f{};
+      for (int j = 0; j < WTN; ++j) acc[i][j] = AccOf<T>{};
 
     if constexpr (PATH == kPipeDma)
       k_loop_dma<WTM, WTN, T, PRIO>(acc, Ap, Bp, M, N, K, lda, ldb, m0, n0, nslabs, As, Bs, wave, wm, wn, lane);
@@ -495,12 +556,12 @@ __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const f
 // has landed and stage fut is free), the fetch of a later slab into stage
 // fut, slab q+1's first fragments, then this slab's remaining chunks.
 template <int WTM, int WTN, class T, bool PRIO>
-__device__ __forceinline__ void flat_step(v16f (&acc)[WTM][WTN], Frag<WTM> &f0, Frag<WTM> &f1, int &cur,
+__device__ __forceinline__ void flat_step(AccOf<T> (&acc)[WTM][WTN], Frag<WTM, WTN> &f0, Frag<WTM, WTN> &f1, int &cur,
                                           const float *__restrict__ Ap, const float *__restrict__ Bp, int64_t M,
                                           int64_t N, int64_t K, int64_t lda, int64_t ldb, bool dma, int64_t dm0,
                                           int64_t dn0, int64_t dk0, bool read_next, float *As, float *Bs, int wv,
                                           int wm, int wn, int lane) {
-  constexpr int C = T::BK / 8;
+  constexpr int C = T::BK / Mfma<T::kMF>::CK;
   const int nxt = cur == 2 ? 0 : cur + 1;
   const int fut = nxt == 2 ? 0 : nxt + 1;
   const float *sA = As + cur * T::A_STAGE, *sB = Bs + cur * T::B_STAGE;
@@ -528,16 +589,16 @@ __device__ __forceinline__ void flat_step(v16f (&acc)[WTM][WTN], Frag<WTM> &f0, 
 // tile's last two slabs, slab 0 or 1 of the next. The tile's C stores go
 // out after those fetches. Needs at least two slabs per tile (K > BK) and
 // fewer than 2^31 tiles.
-template <int WTM, int WTN, int BKT, bool PRIO>
+template <int WTM, int WTN, int BKT, bool PRIO, int WGM = 2, int WGN = 2, int MF = 32>
 __device__ __forceinline__ void gemm_tiles_flat(const float *__restrict__ Ap, const float *__restrict__ Bp,
                                                 float *__restrict__ Cp, int64_t M, int64_t N, int64_t K,
                                                 int64_t lda, int64_t ldb, int64_t ldc, float *As, float *Bs) {
-  using T = Tile<WTM, WTN, BKT, true>;
+  using T = Tile<WTM, WTN, BKT, true, WGM, WGN, MF>;
   constexpr int BK = T::BK;
   const int tid = threadIdx.x;
   const int lane = kh::lane_id();
   const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = T::wave_m(wave), wn = T::wave_n(wave);
   const int wv = __builtin_amdgcn_readfirstlane(wave);
 
   const int64_t tiles_m = (M + T::BM - 1) / T::BM, tiles_n = (N + T::BN - 1) / T::BN;
@@ -568,18 +629,18 @@ __device__ __forceinline__ void gemm_tiles_flat(const float *__restrict__ Ap, co
   dma_slab<T>(Ap, Bp, M, N, K, lda, ldb, cm0, cn0, 0, As, Bs, wv, lane);
   dma_slab<T>(Ap, Bp, M, N, K, lda, ldb, cm0, cn0, BK, As + T::A_STAGE, Bs + T::B_STAGE, wv, lane);
   vm_barrier<T::NA + T::NB>();
-  Frag<WTM> f0, f1;
+  Frag<WTM, WTN> f0, f1;
   read_frag<WTM, WTN, T>(f0, As, Bs, 0, wm, wn, lane);
   int cur = 0;
   for (int64_t t = 0; t < mine; ++t) {
     const bool has_next = t + 1 < mine;
     int64_t nm0 = 0, nn0 = 0;
     if (has_next) coords(t + 1, nm0, nn0);
-    v16f acc[WTM][WTN];
+    AccOf<T> acc[WTM][WTN];
 #pragma unroll
     for (int i = 0; i < WTM; ++i)
 #pragma unroll
-      for (int j = 0; j < WTN; ++j) acc[i][j] = v16f{};
+      for (int j = 0; j < WTN; ++j) acc[i][j] = AccOf<T>{};
     {
       // Slab 0 fetches slab 2 of this tile, or slab 0 of the next (ns = 2).
       const bool same = ns > 2;
@@ -612,10 +673,10 @@ __device__ __forceinline__ void gemm_tiles_flat(const float *__restrict__ Ap, co
 
 // LDS floats a configuration needs for A and for B: the fast pipeline's
 // stages (three for direct-to-LDS, two otherwise) or the generic path's one.
-template <int WTM, int WTN, int BKT, int PIPE>
+template <int WTM, int WTN, int BKT, int PIPE, int WGM = 2, int WGN = 2, int MF = 32>
 struct LdsNeed {
-  using T = Tile<WTM, WTN, BKT, PIPE == kPipeDma>;
-  using G = Tile<WTM, WTN, BKT, false>;
+  using T = Tile<WTM, WTN, BKT, PIPE == kPipeDma, WGM, WGN, MF>;
+  using G = Tile<WTM, WTN, BKT, false, WGM, WGN, MF>;
   static constexpr int kStages = PIPE == kPipeDma ? 3 : 2;
   static constexpr int A = kStages * T::A_STAGE > G::A_STAGE ? kStages * T::A_STAGE : G::A_STAGE;
   static constexpr int B = kStages * T::B_STAGE > G::B_STAGE ? kStages * T::B_STAGE : G::B_STAGE;
@@ -624,42 +685,42 @@ struct LdsNeed {
 // Kernel body over LDS the caller provides (LdsNeed floats each): the fast
 // pipeline PIPE for aligned operands with k and n multiples of 4 and 32-bit
 // tile offsets, the generic path otherwise.
-template <int WTM, int WTN, int BKT, bool PRIO, int PIPE>
+template <int WTM, int WTN, int BKT, bool PRIO, int PIPE, int WGM = 2, int WGN = 2, int MF = 32>
 __device__ __forceinline__ void gemm_body(const float *__restrict__ Ap, const float *__restrict__ Bp,
                                           float *__restrict__ Cp, int64_t M, int64_t N, int64_t K, int64_t lda,
                                           int64_t ldb, int64_t ldc, float *As, float *Bs) {
-  using T = Tile<WTM, WTN, BKT, PIPE == kPipeDma>;
+  using T = Tile<WTM, WTN, BKT, PIPE == kPipeDma, WGM, WGN, MF>;
   const bool a_vec = ((K & 3) == 0) && ((lda & 3) == 0) && kh::aligned16(Ap);
   const bool b_vec = ((N & 3) == 0) && ((ldb & 3) == 0) && kh::aligned16(Bp);
   // The fast loads address a tile's rows with 32-bit byte offsets.
   const bool fits32 = (int64_t)T::BM * lda * 4 < (1ll << 31) && (int64_t)T::BK * ldb * 4 < (1ll << 31);
   if (a_vec && b_vec && fits32)
-    gemm_tiles<WTM, WTN, BKT, PIPE, PRIO>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, As, Bs);
+    gemm_tiles<WTM, WTN, BKT, PIPE, PRIO, WGM, WGN, MF>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, As, Bs);
   else
-    gemm_tiles<WTM, WTN, BKT, 0, PRIO>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, As, Bs);
+    gemm_tiles<WTM, WTN, BKT, 0, PRIO, WGM, WGN, MF>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, a_vec, b_vec, As, Bs);
 }
 
 // Kernel body with its own LDS and fast pipeline PIPE.
-template <int WTM, int WTN, int BKT, bool PRIO, int PIPE>
+template <int WTM, int WTN, int BKT, bool PRIO, int PIPE, int WGM = 2, int WGN = 2, int MF = 32>
 __device__ __forceinline__ void gemm_entry_pipe(const float *__restrict__ Ap, const float *__restrict__ Bp,
                                                 float *__restrict__ Cp, int64_t M, int64_t N, int64_t K, int64_t lda,
                                                 int64_t ldb, int64_t ldc) {
-  using L = LdsNeed<WTM, WTN, BKT, PIPE>;
+  using L = LdsNeed<WTM, WTN, BKT, PIPE, WGM, WGN, MF>;
   __shared__ __attribute__((aligned(16))) float As[L::A];
   __shared__ __attribute__((aligned(16))) float Bs[L::B];
-  gemm_body<WTM, WTN, BKT, PRIO, PIPE>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, As, Bs);
+  gemm_body<WTM, WTN, BKT, PRIO, PIPE, WGM, WGN, MF>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, As, Bs);
 }
 
 // Kernel body of the persistent variant: gemm_tiles_flat when A and B are
 // 16-byte aligned with k and n multiples of 4, K > BK and the tile offsets
 // fit 32 bits; the direct-to-LDS per-tile pipeline (or the generic path)
 // otherwise. Same LDS as gemm_entry_pipe's direct-to-LDS form.
-template <int WTM, int WTN, int BKT, bool PRIO>
+template <int WTM, int WTN, int BKT, bool PRIO, int WGM = 2, int WGN = 2, int MF = 32>
 __device__ __forceinline__ void gemm_entry_flat(const float *__restrict__ Ap, const float *__restrict__ Bp,
                                                 float *__restrict__ Cp, int64_t M, int64_t N, int64_t K, int64_t lda,
                                                 int64_t ldb, int64_t ldc) {
-  using T = Tile<WTM, WTN, BKT, true>;
-  using L = LdsNeed<WTM, WTN, BKT, kPipeDma>;
+  using T = Tile<WTM, WTN, BKT, true, WGM, WGN, MF>;
+  using L = LdsNeed<WTM, WTN, BKT, kPipeDma, WGM, WGN, MF>;
   __shared__ __attribute__((aligned(16))) float As[L::A];
   __shared__ __attribute__((aligned(16))) float Bs[L::B];
   const bool vec = ((K & 3) == 0) && ((lda & 3) == 0) && kh::aligned16(Ap) && ((N & 3) == 0) &&
@@ -667,9 +728,9 @@ __device__ __forceinline__ void gemm_entry_flat(const float *__restrict__ Ap, co
   const bool fits32 = (int64_t)T::BM * lda * 4 < (1ll << 31) && (int64_t)T::BK * ldb * 4 < (1ll << 31);
   const int64_t tiles = ((M + T::BM - 1) / T::BM) * ((N + T::BN - 1) / T::BN);
   if (vec && fits32 && K > T::BK && tiles < (1ll << 31))
-    gemm_tiles_flat<WTM, WTN, BKT, PRIO>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, As, Bs);
+    gemm_tiles_flat<WTM, WTN, BKT, PRIO, WGM, WGN, MF>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, As, Bs);
   else
-    gemm_body<WTM, WTN, BKT, PRIO, kPipeDma>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, As, Bs);
+    gemm_body<WTM, WTN, BKT, PRIO, kPipeDma, WGM, WGN, MF>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, As, Bs);
 }
 
 // The same with DMA selecting the direct-to-LDS pipeline, else the

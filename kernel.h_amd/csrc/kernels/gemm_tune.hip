@@ -1,17 +1,49 @@
-// GEMM tune candidates for `kernelh tune`: one kernel per entry of
-// KH_GEMM_TUNE_CONFIGS, each with the template `gemm` arguments
+// GEMM tune candidates for `kernelh tune` and for the launcher's tune cache:
+// one kernel per entry of gemm_tune_list.h (the space and its prune rules
+// are stated in gemm_tune_space.py), each with the template `gemm` arguments
 // (A [m,k], B [k,n], C [m,n]; 21 parameters) and results, built from the
-// same blocks as the product kernels (gemm_tiles.h). Embedded in the CLI,
-// not in the product library.
+// same blocks as the product kernels (gemm_tiles.h). The list is compiled in
+// KH_GEMM_TUNE_PARTS code objects: this file with -DKH_GEMM_TUNE_PART=p
+// becomes gemm_tune<p>. Every candidate is correct for every shape and grid
+// (tiles are grid-strided; tails are zero-filled or guarded).
 #include "gemm_tiles.h"
 #include "gemm_tune_list.h"
 
-#define KH_GEMM_TUNE_KERNEL(WTM, WTN, BK, PRIO, DMA)                                                      \
-  extern "C" __global__ void __launch_bounds__(khg::kThreads) __attribute__((amdgpu_waves_per_eu(2)))    \
-  KH_GEMM_TUNE_SYMBOL(WTM, WTN, BK, PRIO, DMA)(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B),  \
-                                               KH_MEMREF2(float, C)) {                                  \
-    khg::gemm_entry<WTM, WTN, BK, PRIO != 0, DMA != 0>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, \
-                                                       A_s0, B_s0, C_s0);                                \
+#ifndef KH_GEMM_TUNE_PART
+#error "compile with -DKH_GEMM_TUNE_PART=<0 .. KH_GEMM_TUNE_PARTS-1>"
+#endif
+
+// A candidate's tile split assumes its own workgroup size (64 WGM WGN
+// threads, one-dimensional); any other launch is refused by writing NaN over
+// C instead of computing part of the tile.
+__device__ __forceinline__ void refuse_launch(float *C, int64_t M, int64_t N, int64_t ldc) {
+  const int64_t threads = (int64_t)blockDim.x * blockDim.y * blockDim.z;
+  const int64_t flat = ((int64_t)threadIdx.z * blockDim.y + threadIdx.y) * blockDim.x + threadIdx.x;
+  const int64_t block = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * gridDim.y * gridDim.z * threads;
+  for (int64_t i = block * threads + flat; i < M * N; i += stride) C[(i / N) * ldc + i % N] = __builtin_nanf("");
+}
+
+#define KH_GEMM_TUNE_KERNEL(PART, MF, WGM, WGN, WTM, WTN, BK, PRIO, PIPE, SYM)                               \
+  extern "C" __global__ void __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(2)))         \
+  SYM(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {                        \
+    if (blockDim.x != 64 * WGM * WGN || blockDim.y != 1 || blockDim.z != 1) {                                \
+      refuse_launch(KH_PTR(C), C_n0, C_n1, C_s0);                                                              \
+      return;                                                                                                  \
+    }                                                                                                          \
+    khg::gemm_entry_pipe<WTM, WTN, BK, PRIO != 0, PIPE, WGM, WGN, MF>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0,  \
+                                                                      B_n1, A_n1, A_s0, B_s0, C_s0);         \
   }
 
-KH_GEMM_TUNE_CONFIGS(KH_GEMM_TUNE_KERNEL)
+#if KH_GEMM_TUNE_PART == 0
+KH_GEMM_TUNE_PART0(KH_GEMM_TUNE_KERNEL)
+#elif KH_GEMM_TUNE_PART == 1
+KH_GEMM_TUNE_PART1(KH_GEMM_TUNE_KERNEL)
+#elif KH_GEMM_TUNE_PART == 2
+KH_GEMM_TUNE_PART2(KH_GEMM_TUNE_KERNEL)
+#elif KH_GEMM_TUNE_PART == 3
+KH_GEMM_TUNE_PART3(KH_GEMM_TUNE_KERNEL)
+#else
+#error "KH_GEMM_TUNE_PART out of range"
+#endif
+static_assert(KH_GEMM_TUNE_PARTS == 4, "one #if branch per part");

@@ -10,10 +10,15 @@
 // reference's geometry too), while the memref argument lists, symbol names
 // and the hipModuleLoadData / hipModuleLaunchKernel path are unchanged.
 #include "kernelh/khrt_internal.hpp"
+#include "gemm_tune_list.h"
 #include "kh_tiles.h"
 
 #include <algorithm>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <fstream>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -31,6 +36,11 @@ KH_DECLARE_CO(gemm)
 KH_DECLARE_CO(attention)
 KH_DECLARE_CO(util)
 KH_DECLARE_CO(roofline)
+KH_DECLARE_CO(gemm_tune0)
+KH_DECLARE_CO(gemm_tune1)
+KH_DECLARE_CO(gemm_tune2)
+KH_DECLARE_CO(gemm_tune3)
+static_assert(KH_GEMM_TUNE_PARTS == 4, "one code object per part of the tune list");
 
 namespace {
 
@@ -46,6 +56,10 @@ const CodeObject kCodeObjects[] = {
     {"scan", kh_co_scan, kh_co_scan_end},             {"gemm", kh_co_gemm, kh_co_gemm_end},
     {"attention", kh_co_attention, kh_co_attention_end}, {"util", kh_co_util, kh_co_util_end},
     {"roofline", kh_co_roofline, kh_co_roofline_end},
+    {"gemm_tune0", kh_co_gemm_tune0, kh_co_gemm_tune0_end},
+    {"gemm_tune1", kh_co_gemm_tune1, kh_co_gemm_tune1_end},
+    {"gemm_tune2", kh_co_gemm_tune2, kh_co_gemm_tune2_end},
+    {"gemm_tune3", kh_co_gemm_tune3, kh_co_gemm_tune3_end},
 };
 
 struct KernelResources {
@@ -147,13 +161,166 @@ int get_function(const char *co_name, const char *symbol, void **out) {
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// ---------------------------------------------------------------------------
+// GEMM candidates: the launcher's own symbols, then the tune space
+// (gemm_tune_list.h). Every one takes the template `gemm` arguments and
+// computes C = A B for every shape and grid.
+enum GemmPipe { kRegs = 1, kDma = 2, kPf2 = 3, kPersistent = 4, kKsplit = 5, kKsplitDeep = 6 };
+
+const char *pipe_name(int pipe) {
+  switch (pipe) {
+    case kRegs: return "regs";
+    case kDma: return "lds-dma";
+    case kPf2: return "prefetch2";
+    case kPersistent: return "persistent";
+    case kKsplit: return "ksplit";
+    case kKsplitDeep: return "ksplit-deep";
+    default: return "?";
+  }
+}
+
+struct GemmCandidate {
+  const char *symbol;
+  const char *co;
+  int mfma, wgm, wgn, wtm, wtn, bk, prio, pipe;
+  bool product;
+  bool ksplit() const { return pipe == kKsplit || pipe == kKsplitDeep; }
+  // K-split: each of the 8 waves holds the whole 32x32 tile for its K range.
+  int waves() const { return ksplit() ? KH_GEMM_KSPLIT_THREADS / 64 : wgm * wgn; }
+  int bm() const { return ksplit() ? KH_GEMM_KSPLIT_BM : mfma * wtm * wgm; }
+  int bn() const { return ksplit() ? KH_GEMM_KSPLIT_BN : mfma * wtn * wgn; }
+  // Slabs (K-split: batches of 32 k) in flight ahead of the MFMAs.
+  int unroll() const { return pipe == kRegs ? 1 : pipe == kKsplitDeep ? 3 : 2; }
+};
+
+#define KH_TUNE_CANDIDATE(PART, MF, WGM, WGN, WTM, WTN, BK, PRIO, PIPE, SYM) \
+  {#SYM, "gemm_tune" #PART, MF, WGM, WGN, WTM, WTN, BK, PRIO, PIPE, false},
+const GemmCandidate kGemmCandidates[] = {
+    {"gemm", "gemm", 32, 2, 2, 2, 4, 16, 1, kPersistent, true},
+    {"gemm_mid", "gemm", 32, 2, 2, 2, 2, 32, 1, kRegs, true},
+    {"gemm_small", "gemm", 32, 2, 2, 1, 1, 32, 0, kRegs, true},
+    {"gemm_small_pf2", "gemm", 32, 2, 2, 1, 1, 16, 0, kPf2, true},
+    {"gemm_ksplit", "gemm", 32, 1, 1, 1, 1, 8, 0, kKsplit, true},
+    {"gemm_ksplit_deep", "gemm", 32, 1, 1, 1, 1, 8, 0, kKsplitDeep, true},
+    KH_GEMM_TUNE_CONFIGS(KH_TUNE_CANDIDATE)};
+#undef KH_TUNE_CANDIDATE
+constexpr int kGemmCandidateCount = static_cast<int>(sizeof(kGemmCandidates) / sizeof(kGemmCandidates[0]));
+static_assert(kGemmCandidateCount == 6 + KH_GEMM_TUNE_COUNT, "candidate table");
+
+const GemmCandidate *find_gemm_candidate(const char *symbol) {
+  if (symbol == nullptr) return nullptr;
+  for (const auto &c : kGemmCandidates) {
+    if (std::strcmp(c.symbol, symbol) == 0) return &c;
+  }
+  return nullptr;
+}
+
+// Grid of a candidate at m x n: one workgroup per tile, except the
+// persistent `gemm`, which gets at most two per CU and loops.
+int64_t candidate_grid(const GemmCandidate &c, int64_t m, int64_t n) {
+  const int64_t tiles = ceil_div(m, c.bm()) * ceil_div(n, c.bn());
+  return c.pipe == kPersistent ? std::min<int64_t>(tiles, KH_GEMM_ROUND_BIG) : tiles;
+}
+
+// The tune cache `kernelh tune` writes: one JSON object per line,
+// {"key": "<16 hex>", "best": "<symbol>", "csv": "..."}, keyed by FNV-1a 64
+// of "gemm|m=..,n=..,k=..|<device token>". The launcher reads it only when a
+// path is set (khrt_set_tune_cache, or KHRT_TUNE_CACHE in the environment at
+// the first GEMM launch); the file is read once per path.
+std::string fnv1a_hex(const std::string &s) {
+  uint64_t h = 1469598103934665603ull;
+  for (unsigned char ch : s) {
+    h ^= ch;
+    h *= 1099511628211ull;
+  }
+  char buf[17];
+  std::snprintf(buf, sizeof buf, "%016llx", static_cast<unsigned long long>(h));
+  return buf;
+}
+
+// Asked once per device (hipGetDeviceProperties is not cheap enough to sit
+// on every launch).
+std::string device_token() {
+  static std::mutex mu;
+  static std::map<int, std::string> memo;
+  if (khrt::ensure_device() != 0) return "";
+  const int dev = khrt::current_device();
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = memo.find(dev);
+    if (it != memo.end()) return it->second;
+  }
+  khrt_device_info d{};
+  if (khrt_get_device_info(&d) != 0) return "";
+  const std::string token = std::string(d.name[0] ? d.name : "AMD Instinct MI355X") + " (" + d.arch + ") cu=" +
+                            std::to_string(static_cast<long long>(d.cu_count));
+  std::lock_guard<std::mutex> lock(mu);
+  memo[dev] = token;
+  return token;
+}
+
+std::string gemm_shape_text(int64_t m, int64_t n, int64_t k) {
+  return "m=" + std::to_string(m) + ",n=" + std::to_string(n) + ",k=" + std::to_string(k);
+}
+
+struct TuneCache {
+  std::mutex mu;
+  bool configured = false;  // khrt_set_tune_cache called, or the environment read
+  std::string path;
+  bool loaded = false;
+  std::map<std::string, std::string> best;  // key -> symbol
+};
+TuneCache g_tune;
+
+void load_tune_cache_locked() {
+  g_tune.best.clear();
+  g_tune.loaded = true;
+  if (g_tune.path.empty()) return;
+  std::ifstream f(g_tune.path);
+  std::string line;
+  const std::string kk = "{\"key\": \"", kb = "\"best\": \"";
+  while (std::getline(f, line)) {
+    if (line.rfind(kk, 0) != 0) continue;
+    const size_t ke = line.find('"', kk.size());
+    const size_t b = line.find(kb);
+    if (ke == std::string::npos || b == std::string::npos) continue;
+    const size_t be = line.find('"', b + kb.size());
+    if (be == std::string::npos) continue;
+    g_tune.best[line.substr(kk.size(), ke - kk.size())] = line.substr(b + kb.size(), be - b - kb.size());
+  }
+}
+
+// The tuned candidate for this GEMM shape, or nullptr (no cache, no entry,
+// or an entry naming a symbol this build does not have).
+const GemmCandidate *tuned_gemm(int64_t m, int64_t n, int64_t k) {
+  std::string key;
+  {
+    std::lock_guard<std::mutex> lock(g_tune.mu);
+    if (!g_tune.configured) {
+      const char *env = std::getenv("KHRT_TUNE_CACHE");
+      g_tune.path = env != nullptr ? env : "";
+      g_tune.configured = true;
+      g_tune.loaded = false;
+    }
+    if (g_tune.path.empty()) return nullptr;
+    if (!g_tune.loaded) load_tune_cache_locked();
+    if (g_tune.best.empty()) return nullptr;
+  }
+  const std::string dev = device_token();
+  if (dev.empty()) return nullptr;
+  key = fnv1a_hex("gemm|" + gemm_shape_text(m, n, k) + "|" + dev);
+  std::lock_guard<std::mutex> lock(g_tune.mu);
+  auto it = g_tune.best.find(key);
+  return it == g_tune.best.end() ? nullptr : find_gemm_candidate(it->second.c_str());
+}
+
 // GEMM tile choice: the largest tile whose grid still gives every CU work.
 // Rate x busy fraction of the last round of workgroups (kh_tiles.h).
 double gemm_score(int64_t tiles, int64_t round, double rate) {
   return rate * static_cast<double>(tiles) / static_cast<double>(ceil_div(tiles, round) * round);
 }
 
-const char *gemm_symbol(int64_t m, int64_t n, int64_t k) {
+const char *heuristic_gemm_symbol(int64_t m, int64_t n, int64_t k) {
   if (ceil_div(m, KH_GEMM_KSPLIT_BM) * ceil_div(n, KH_GEMM_KSPLIT_BN) <= KH_GEMM_CUS) {
     return k >= KH_GEMM_KSPLIT_DEEP_K ? "gemm_ksplit_deep" : "gemm_ksplit";
   }
@@ -169,13 +336,11 @@ const char *gemm_symbol(int64_t m, int64_t n, int64_t k) {
   return tiles64 >= KH_GEMM_SMALL_PF2_TILES ? "gemm_small_pf2" : "gemm_small";
 }
 
-// `gemm` is persistent: at most one workgroup per tile slot (two per CU).
-int64_t gemm_grid(int64_t m, int64_t n) {
-  const std::string sym = gemm_symbol(m, n, 0);
-  if (sym == "gemm") return std::min<int64_t>(ceil_div(m, KH_GEMM_BM) * ceil_div(n, KH_GEMM_BN), KH_GEMM_ROUND_BIG);
-  if (sym == "gemm_mid") return ceil_div(m, KH_GEMM_MID_BM) * ceil_div(n, KH_GEMM_MID_BN);
-  if (sym == "gemm_ksplit") return ceil_div(m, KH_GEMM_KSPLIT_BM) * ceil_div(n, KH_GEMM_KSPLIT_BN);  // and _deep
-  return ceil_div(m, KH_GEMM_SMALL_BM) * ceil_div(n, KH_GEMM_SMALL_BN);
+// The launcher's GEMM candidate: the tune cache's choice for this shape when
+// one is set and names a candidate, the heuristic's otherwise.
+const GemmCandidate &gemm_choice(int64_t m, int64_t n, int64_t k) {
+  if (const GemmCandidate *t = tuned_gemm(m, n, k)) return *t;
+  return *find_gemm_candidate(heuristic_gemm_symbol(m, n, k));
 }
 
 unsigned clamp_grid(int64_t g) { return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(g, 1 << 20))); }
@@ -221,8 +386,9 @@ int geometry(const char *name, const Shape &s, khrt_dim3 &grid, khrt_dim3 &block
     if (!need(s, "m", m) || !need(s, "n", n) || !need(s, "k", k)) {
       return khrt::fail(KHRT_E_INVALID, "gemm: shape attributes 'm', 'n' and 'k' are required and must be positive");
     }
-    grid.x = clamp_grid(gemm_grid(m, n));
-    if (std::string(gemm_symbol(m, n, k)).rfind("gemm_ksplit", 0) == 0) block.x = KH_GEMM_KSPLIT_THREADS;
+    const GemmCandidate &c = gemm_choice(m, n, k);
+    grid.x = clamp_grid(candidate_grid(c, m, n));
+    block.x = static_cast<unsigned>(64 * c.waves());
   } else if (t == "attention") {
     if (!need(s, "batch", b) || !need(s, "heads", h) || !need(s, "seq", seq) || !need(s, "head_dim", d)) {
       return khrt::fail(KHRT_E_INVALID,
@@ -255,9 +421,17 @@ const char *launch_symbol(const Template *t, const Shape &s) {
   }
   if (n == "gemm") {
     auto m = s.find("m"), nn = s.find("n"), k = s.find("k");
-    if (m != s.end() && nn != s.end()) return gemm_symbol(m->second, nn->second, k != s.end() ? k->second : 0);
+    if (m != s.end() && nn != s.end() && k != s.end()) return gemm_choice(m->second, nn->second, k->second).symbol;
   }
   return t->name;
+}
+
+// Code object holding the symbol the launcher runs for a template.
+const char *launch_co(const Template *t, const char *symbol) {
+  if (std::strcmp(t->name, "gemm") == 0) {
+    if (const GemmCandidate *c = find_gemm_candidate(symbol)) return c->co;
+  }
+  return t->co;
 }
 
 // Workgroups of `block` threads of `fn` resident on the whole device at
@@ -298,7 +472,8 @@ int launch_template(const char *name, khrt::LaunchArgs &args, const Shape &shape
   khrt_dim3 grid, block;
   if (int rc = geometry(name, shape, grid, block)) return rc;
   void *fn = nullptr;
-  if (int rc = get_function(t->co, launch_symbol(t, shape), &fn)) return rc;
+  const char *symbol = launch_symbol(t, shape);
+  if (int rc = get_function(launch_co(t, symbol), symbol, &fn)) return rc;
   if (std::strcmp(name, "scan") == 0) {
     // The look-back scan is persistent: one resident wave of workgroups
     // loops over tiles, so launch no more workgroups than fit at once, and
@@ -377,6 +552,86 @@ int khrt_template_function(const char *name, void **function) {
   const Template *t = find_template(name);
   if (t == nullptr) return unknown_template(name);
   return get_function(t->co, t->name, function);
+}
+
+int khrt_gemm_candidate_count(void) { return kGemmCandidateCount; }
+
+int khrt_gemm_candidate_get(int i, khrt_gemm_candidate *out) {
+  if (out == nullptr) return bad("khrt_gemm_candidate_get: null output");
+  if (i < 0 || i >= kGemmCandidateCount) {
+    return khrt::fail(KHRT_E_INVALID, "khrt_gemm_candidate_get: index " + std::to_string(i) + " outside [0, " +
+                                          std::to_string(kGemmCandidateCount) + ")");
+  }
+  const GemmCandidate &c = kGemmCandidates[i];
+  *out = khrt_gemm_candidate{};
+  std::snprintf(out->symbol, sizeof out->symbol, "%s", c.symbol);
+  std::snprintf(out->code_object, sizeof out->code_object, "%s", c.co);
+  std::snprintf(out->pipeline, sizeof out->pipeline, "%s", pipe_name(c.pipe));
+  out->mfma = c.mfma;
+  out->waves = c.waves();
+  out->wave_grid_m = c.ksplit() ? 1 : c.wgm;
+  out->wave_grid_n = c.ksplit() ? 1 : c.wgn;
+  out->wave_tile_m = c.ksplit() ? c.bm() : c.mfma * c.wtm;
+  out->wave_tile_n = c.ksplit() ? c.bn() : c.mfma * c.wtn;
+  out->bm = c.bm();
+  out->bn = c.bn();
+  out->bk = c.bk;
+  out->unroll = c.unroll();
+  out->prio = c.prio;
+  out->persistent = c.pipe == kPersistent;
+  out->k_split = c.ksplit();
+  out->product = c.product;
+  return 0;
+}
+
+int khrt_gemm_candidate_geometry(const char *symbol, int64_t m, int64_t n, int64_t k, khrt_dim3 *grid,
+                                 khrt_dim3 *block) {
+  (void)k;
+  if (grid == nullptr || block == nullptr) return bad("khrt_gemm_candidate_geometry: null output");
+  const GemmCandidate *c = find_gemm_candidate(symbol);
+  if (c == nullptr) {
+    return khrt::fail(KHRT_E_INVALID, std::string("unknown GEMM candidate '") + (symbol ? symbol : "(null)") + "'");
+  }
+  if (m <= 0 || n <= 0 || k <= 0) return bad("khrt_gemm_candidate_geometry: m, n and k must be positive");
+  *grid = khrt_dim3{clamp_grid(candidate_grid(*c, m, n)), 1, 1};
+  *block = khrt_dim3{static_cast<unsigned>(64 * c->waves()), 1, 1};
+  return 0;
+}
+
+int khrt_gemm_candidate_function(const char *symbol, void **function) {
+  if (function == nullptr) return bad("khrt_gemm_candidate_function: null output");
+  const GemmCandidate *c = find_gemm_candidate(symbol);
+  if (c == nullptr) {
+    return khrt::fail(KHRT_E_INVALID, std::string("unknown GEMM candidate '") + (symbol ? symbol : "(null)") + "'");
+  }
+  return get_function(c->co, c->symbol, function);
+}
+
+int khrt_set_tune_cache(const char *path) {
+  std::lock_guard<std::mutex> lock(g_tune.mu);
+  g_tune.configured = true;
+  g_tune.path = path != nullptr ? path : "";
+  g_tune.loaded = false;
+  return 0;
+}
+
+int khrt_tune_cache_key(const char *kernel, const char *shape, char *out, size_t cap) {
+  if (kernel == nullptr || shape == nullptr || out == nullptr) return bad("khrt_tune_cache_key: null argument");
+  if (cap < 17) return bad("khrt_tune_cache_key: output buffer too small (17 bytes needed)");
+  const std::string dev = device_token();
+  if (dev.empty()) return khrt::fail(KHRT_E_INVALID, "khrt_tune_cache_key: no device");
+  const std::string key = fnv1a_hex(std::string(kernel) + "|" + shape + "|" + dev);
+  std::memcpy(out, key.c_str(), 17);
+  return 0;
+}
+
+int khrt_device_token(char *out, size_t cap) {
+  if (out == nullptr || cap == 0) return bad("khrt_device_token: null output");
+  const std::string dev = device_token();
+  if (dev.empty()) return khrt::fail(KHRT_E_INVALID, "khrt_device_token: no device");
+  if (dev.size() + 1 > cap) return bad("khrt_device_token: output buffer too small");
+  std::memcpy(out, dev.c_str(), dev.size() + 1);
+  return 0;
 }
 
 int khrt_fill_f32(void *dst, float value, size_t count, void *stream) {

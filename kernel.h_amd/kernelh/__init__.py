@@ -90,6 +90,16 @@ class KernelResources(ctypes.Structure):
                 ("wavefront_size", ctypes.c_int32), ("max_flat_workgroup_size", ctypes.c_int32)]
 
 
+class GemmCandidate(ctypes.Structure):
+    _fields_ = [("symbol", ctypes.c_char * 64), ("code_object", ctypes.c_char * 16),
+                ("pipeline", ctypes.c_char * 16), ("mfma", ctypes.c_int32), ("waves", ctypes.c_int32),
+                ("wave_grid_m", ctypes.c_int32), ("wave_grid_n", ctypes.c_int32),
+                ("wave_tile_m", ctypes.c_int32), ("wave_tile_n", ctypes.c_int32),
+                ("bm", ctypes.c_int32), ("bn", ctypes.c_int32), ("bk", ctypes.c_int32),
+                ("unroll", ctypes.c_int32), ("prio", ctypes.c_int32), ("persistent", ctypes.c_int32),
+                ("k_split", ctypes.c_int32), ("product", ctypes.c_int32)]
+
+
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
 _i64 = ctypes.c_int64
@@ -143,6 +153,14 @@ SIGNATURES = {
     "khrt_template_geometry": (_i, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(Dim3), ctypes.POINTER(Dim3)]),
     "khrt_template_launch_symbol": (_i, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
     "khrt_template_function": (_i, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "khrt_gemm_candidate_count": (_i, []),
+    "khrt_gemm_candidate_get": (_i, [_i, ctypes.POINTER(GemmCandidate)]),
+    "khrt_gemm_candidate_geometry": (_i, [ctypes.c_char_p, _i64, _i64, _i64, ctypes.POINTER(Dim3),
+                                          ctypes.POINTER(Dim3)]),
+    "khrt_gemm_candidate_function": (_i, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "khrt_set_tune_cache": (_i, [ctypes.c_char_p]),
+    "khrt_tune_cache_key": (_i, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _sz]),
+    "khrt_device_token": (_i, [ctypes.c_char_p, _sz]),
     "kh_vecadd": (_i, [_vp, _vp, _vp, _i64, _vp]),
     "kh_fused_gelu": (_i, [_vp, _vp, _vp, _i64, _vp]),
     "kh_softmax": (_i, [_vp, _vp, _i64, _i64, _vp]),
@@ -458,6 +476,48 @@ def template_function(name: str) -> int:
     f = ctypes.c_void_p()
     check(lib.khrt_template_function(name.encode(), ctypes.byref(f)))
     return f.value
+
+
+def gemm_candidates() -> list[dict]:
+    """Every GEMM candidate (launcher symbols first, then the tune space)."""
+    out = []
+    for i in range(lib.khrt_gemm_candidate_count()):
+        c = GemmCandidate()
+        check(lib.khrt_gemm_candidate_get(i, ctypes.byref(c)))
+        d = {f: getattr(c, f) for f, _ in GemmCandidate._fields_}
+        for f in ("symbol", "code_object", "pipeline"):
+            d[f] = d[f].decode()
+        out.append(d)
+    return out
+
+
+def gemm_candidate_geometry(symbol: str, m: int, n: int, k: int):
+    g, b = Dim3(), Dim3()
+    check(lib.khrt_gemm_candidate_geometry(symbol.encode(), m, n, k, ctypes.byref(g), ctypes.byref(b)))
+    return g.tuple(), b.tuple()
+
+
+def gemm_candidate_function(symbol: str) -> int:
+    f = ctypes.c_void_p()
+    check(lib.khrt_gemm_candidate_function(symbol.encode(), ctypes.byref(f)))
+    return f.value
+
+
+def set_tune_cache(path: str | None) -> None:
+    """Points the GEMM launcher at a `kernelh tune` cache file (None: off)."""
+    check(lib.khrt_set_tune_cache(path.encode() if path else None))
+
+
+def tune_cache_key(kernel: str, shape: str) -> str:
+    buf = ctypes.create_string_buffer(17)
+    check(lib.khrt_tune_cache_key(kernel.encode(), shape.encode(), buf, 17))
+    return buf.value.decode()
+
+
+def device_token() -> str:
+    buf = ctypes.create_string_buffer(512)
+    check(lib.khrt_device_token(buf, 512))
+    return buf.value.decode()
 
 
 def vecadd(a, b, c, n: int, stream=None) -> None:

@@ -15,6 +15,7 @@ import os
 import re
 import struct
 import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -388,3 +389,81 @@ def test_elf_image_size_refuses_what_is_not_a_code_object():
     far[40:48] = struct.pack("<Q", 1 << 40)  # e_shoff far beyond any code object
     rc, _ = _elf_extent(bytes(far))
     assert rc == kh.KHRT_E_INVALID and "khrt_elf_image_size" in kh.lib.khrt_last_error().decode()
+
+
+# ------------------------------------------------------------------ GEMM candidates / tune space
+
+_PRODUCT_GEMM = ["gemm", "gemm_mid", "gemm_small", "gemm_small_pf2", "gemm_ksplit", "gemm_ksplit_deep"]
+
+
+def _notes(co):
+    import json
+    return {k["name"]: k for k in json.load(open(os.path.join(kh.CO_DIR, co + ".notes.json")))}
+
+
+def test_tune_list_is_the_generators_output():
+    # gemm_tune_list.h is generated by gemm_tune_space.py (which states the
+    # prune rules); the committed header must be its current output.
+    kdir = os.path.join(REPO, "kernel.h_amd", "csrc", "kernels")
+    out = subprocess.run([sys.executable, os.path.join(kdir, "gemm_tune_space.py")], capture_output=True,
+                         text=True, check=True).stdout
+    assert out == open(os.path.join(kdir, "gemm_tune_list.h")).read()
+
+
+def test_gemm_candidate_table():
+    cands = kh.gemm_candidates()
+    assert [c["symbol"] for c in cands[:6]] == _PRODUCT_GEMM
+    assert all(c["product"] == 1 for c in cands[:6]) and not any(c["product"] for c in cands[6:])
+    assert len({c["symbol"] for c in cands}) == len(cands)
+    space = cands[6:]
+    # The reference's axes (autotuner.hpp:36-41) all vary over the space,
+    # re-pruned for MFMA tiles: both MFMA shapes, 4 and 8 waves, BM/BN in
+    # {64,128,256}, BK in {16,32}, unroll 1 and 2.
+    assert {c["mfma"] for c in space} == {16, 32}
+    assert {c["waves"] for c in space} == {4, 8}
+    assert {c["bm"] for c in space} == {64, 128, 256} and {c["bn"] for c in space} == {64, 128, 256}
+    assert {c["bk"] for c in space} == {16, 32}
+    assert {c["unroll"] for c in space} == {1, 2}
+    assert {c["pipeline"] for c in space} == {"regs", "lds-dma", "prefetch2"}
+    notes = {co: _notes(co) for co in {c["code_object"] for c in cands}}
+    for c in cands:
+        k = notes[c["code_object"]][c["symbol"]]  # the symbol is in its code object
+        assert k["max_flat_workgroup_size"] == 64 * c["waves"], c["symbol"]
+        assert k["private_segment_bytes"] == 0 and k["vgpr_spill_count"] == 0, c["symbol"]
+        # Two waves per SIMD: <= 256 registers; LDS for two 4-wave workgroups
+        # (or one 8-wave workgroup) per CU.
+        assert k["vgpr_count"] + k["agpr_count"] <= 256, c["symbol"]
+        assert k["lds_bytes"] <= (160 if c["waves"] == 8 else 80) * 1024, c["symbol"]
+        if not c["k_split"]:
+            assert c["bm"] == c["wave_grid_m"] * c["wave_tile_m"] and c["bn"] == c["wave_grid_n"] * c["wave_tile_n"]
+            assert c["wave_tile_m"] % c["mfma"] == 0 and c["wave_tile_n"] % c["mfma"] == 0
+            assert c["waves"] == c["wave_grid_m"] * c["wave_grid_n"]
+
+
+@pytest.mark.parametrize("symbol,m,n,k,grid,block", [
+    ("gemm", 8192, 8192, 8192, 512, 256),            # persistent: two per CU
+    ("gemm", 256, 512, 64, 4, 256),                  # fewer tiles than slots
+    ("gemm_mid", 1000, 1000, 8, 64, 256),
+    ("gemm_ksplit", 512, 512, 512, 256, 512),
+    ("gemm_m16_w2x4_t4x2_k16_p1_dma", 1000, 1000, 64, 64, 512),   # 128 x 128 tiles, 8 waves
+])
+def test_gemm_candidate_geometry(symbol, m, n, k, grid, block):
+    assert kh.gemm_candidate_geometry(symbol, m, n, k) == ((grid, 1, 1), (block, 1, 1))
+
+
+def test_gemm_candidate_errors_and_tune_cache_without_device(tmp_path):
+    with pytest.raises(kh.KhrtError, match="unknown GEMM candidate"):
+        kh.gemm_candidate_geometry("gemm_nope", 8, 8, 8)
+    c = kh.GemmCandidate()
+    assert kh.lib.khrt_gemm_candidate_get(kh.lib.khrt_gemm_candidate_count(), ctypes.byref(c)) == kh.KHRT_E_INVALID
+    assert "outside" in kh.last_error()
+    # A cache naming a candidate changes nothing where no device gives the
+    # key its device part: the built-in choice stays.
+    if kh.device_count() == 0:
+        p = tmp_path / "cache.json"
+        p.write_text('{"key": "0000000000000000", "best": "gemm_small", "csv": ""}\n')
+        kh.set_tune_cache(str(p))
+        try:
+            assert kh.launch_symbol("gemm", "m=8192,n=8192,k=8192") == "gemm"
+        finally:
+            kh.set_tune_cache(None)

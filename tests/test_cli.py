@@ -184,21 +184,50 @@ def test_tune_usage_and_refusals(tmp_path):
 
 @pytest.mark.gpu
 def test_tune_evaluates_candidates_and_caches(dev, tmp_path):
-    print("[gpu-case] kernelh tune gemm m=n=k=512, 6 candidates", flush=True)
+    print("[gpu-case] kernelh tune gemm m=n=k=512, 10 candidates", flush=True)
     cache = str(tmp_path / "cache.json")
-    args = ("tune", "--shape", "m=512,n=512,k=512", "--out", str(tmp_path), "--max-candidates", "6",
+    shape = "m=512,n=512,k=512"
+    args = ("tune", "--shape", shape, "--out", str(tmp_path), "--max-candidates", "10",
             "--timeout", "60", "--cache", cache)
     r = run(*args)
     assert r.returncode == 0, r.stdout
-    assert "best config: gemm_t" in r.stdout and "tune ok" in r.stdout
+    assert "best config: gemm" in r.stdout and "tune ok" in r.stdout
     rows = list(csv.DictReader(open(tmp_path / "tune-results.csv")))
-    assert len(rows) == 6
+    assert len(rows) == 10
     assert list(rows[0].keys())[:11] == ["kernel", "shape", "bm", "bn", "bk", "waves", "unroll", "vec", "ms_median",
                                           "accepted", "reason"]
     assert all(row["accepted"] == "true" and row["reason"] == "ok" for row in rows), rows
     assert all(float(row["ms_median"]) > 0 for row in rows)
+    # The launcher's own symbols come first, with their real axes: the
+    # persistent 128x256 `gemm` (4 waves, two slabs ahead), the K-split
+    # symbols (8 waves; the deep one three batches ahead).
+    by = {row["symbol"]: row for row in rows}
+    assert (by["gemm"]["bm"], by["gemm"]["bn"], by["gemm"]["waves"], by["gemm"]["unroll"]) == ("128", "256", "4", "2")
+    assert (by["gemm_mid"]["unroll"], by["gemm_ksplit"]["waves"], by["gemm_ksplit_deep"]["unroll"]) == ("1", "8", "3")
+    assert {row["vec"] for row in rows} == {"4"}  # k, n multiples of 4: dwordx4 loads
+    assert all(row["product"] == ("1" if i < 6 else "0") for i, row in enumerate(rows))
+    best = min(rows, key=lambda row: float(row["ms_median"]))["symbol"]
+    assert f"best config: {best} " in r.stdout
     r2 = run(*args)
     assert r2.returncode == 0 and "cache-hit" in r2.stdout and "served from cache" in r2.stdout
+    # The runtime's launcher reads the same cache: kh_gemm then runs `best`.
+    kh.set_tune_cache(cache)
+    try:
+        assert kh.launch_symbol("gemm", shape) == best
+    finally:
+        kh.set_tune_cache(None)
+
+
+@pytest.mark.gpu
+def test_tune_vec_column_follows_the_shape(dev, tmp_path):
+    # k not a multiple of 4: every candidate takes its guarded scalar loads.
+    print("[gpu-case] kernelh tune gemm m=100,n=100,k=33, 2 candidates", flush=True)
+    r = run("tune", "--shape", "m=100,n=100,k=33", "--out", str(tmp_path), "--max-candidates", "2",
+            "--cache", str(tmp_path / "c.json"))
+    assert r.returncode == 0, r.stdout
+    rows = list(csv.DictReader(open(tmp_path / "tune-results.csv")))
+    assert [row["vec"] for row in rows] == ["1", "1"]
+    assert all(row["accepted"] == "true" for row in rows), rows
 
 
 @pytest.mark.gpu

@@ -16,6 +16,8 @@
   launcher's own grid (one workgroup per tile, or at most two per CU for
   `gemm`; XCD-remapped) is checked at a shape it sends to each symbol.
 """
+import json
+
 import numpy as np
 import pytest
 
@@ -195,3 +197,67 @@ def test_gemm_launcher_choice_at_scale(dev, m, n, k, grid):
         err = O.rel_frobenius(C[rows], A[rows].astype(np.float64) @ B.astype(np.float64))
         print(f"gemm {m}x{n}x{k} rel-frobenius (rows sampled)={err:.3e}")
         assert err <= 1e-5
+
+
+# ------------------------------------------------------------------ tune candidates
+
+@pytest.mark.parametrize("m,n,k", [(200, 264, 72), (67, 45, 33), (129, 520, 260)])
+def test_every_gemm_candidate_exact(dev, m, n, k):
+    """Every GEMM candidate (the launcher's six symbols and the whole gfx950
+    tune space: MFMA 32x32 and 16x16 tiles, 4 and 8 waves, every pipeline)
+    at its own launch geometry, integer fill: bit-exact. (200, 264, 72) and
+    (129, 520, 260) take the float4 paths with tails in m, n and k; (67, 45,
+    33) the guarded generic path."""
+    A, B = O.gemm_int_inputs(m, n, k)
+    want = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    dA, dB, dC = up(A), up(B), empty(m * n)
+    args = kh.LaunchArgs().add_memref(dA, [m, k]).add_memref(dB, [k, n]).add_memref(dC, [m, n])
+    wrong = []
+    for c in kh.gemm_candidates():
+        sym = c["symbol"]
+        grid, block = kh.gemm_candidate_geometry(sym, m, n, k)
+        dC.fill(float("nan"))
+        say(f"{sym} m={m} n={n} k={k} grid={grid} block={block}")
+        kh.kernel_launch(kh.gemm_candidate_function(sym), grid, block, args)
+        if not np.array_equal(down(dC, m * n).reshape(m, n), want):
+            wrong.append(sym)
+    assert not wrong, wrong
+
+
+def test_tune_candidate_refuses_another_block_size(dev):
+    # An 8-wave candidate launched with 256 threads writes NaN, never part
+    # of the tile.
+    m = n = k = 64
+    A, B = O.gemm_int_inputs(m, n, k)
+    dA, dB, dC = up(A), up(B), empty(m * n, 0.0)
+    args = kh.LaunchArgs().add_memref(dA, [m, k]).add_memref(dB, [k, n]).add_memref(dC, [m, n])
+    sym = next(c["symbol"] for c in kh.gemm_candidates() if c["waves"] == 8 and not c["product"])
+    say(f"{sym} at 256 threads (refused)")
+    kh.kernel_launch(kh.gemm_candidate_function(sym), (4, 1, 1), (256, 1, 1), args)
+    assert np.all(np.isnan(down(dC, m * n)))
+
+
+def test_tune_cache_steers_the_launcher(dev, tmp_path):
+    """A tune cache entry for a shape makes kh_gemm (and the geometry and
+    symbol queries) run the cached candidate for that shape only; other
+    shapes keep the built-in choice; turning the cache off restores it."""
+    m, n, k = 1000, 1000, 64
+    shape = f"m={m},n={n},k={k}"
+    pick = "gemm_m16_w2x4_t4x2_k16_p1_dma"  # 128 x 128 tiles, 8 waves, 16x16 MFMA
+    default = kh.launch_symbol("gemm", shape)
+    other = kh.launch_symbol("gemm", "m=1000,n=1000,k=68")
+    assert default != pick
+    cache = tmp_path / "tune-cache.json"
+    cache.write_text(json.dumps({"key": kh.tune_cache_key("gemm", shape), "best": pick, "csv": ""}) + "\n")
+    A, B = O.gemm_int_inputs(m, n, k)
+    want = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    kh.set_tune_cache(str(cache))
+    try:
+        assert kh.launch_symbol("gemm", shape) == pick
+        assert kh.geometry("gemm", shape) == kh.gemm_candidate_geometry(pick, m, n, k)
+        assert kh.launch_symbol("gemm", "m=1000,n=1000,k=68") == other  # no entry: built-in choice
+        C = _gemm(A, B, m, n, k)
+        assert np.array_equal(C, want)
+    finally:
+        kh.set_tune_cache(None)
+    assert kh.launch_symbol("gemm", shape) == default
