@@ -1,18 +1,20 @@
 // fp32 GEMM for gfx950 on the matrix cores: C[m,n] = A[m,k] B[k,n],
-// row-major, v_mfma_f32_32x32x2f32.
+// row-major, v_mfma_f32_32x32x2f32 (and v_mfma_f32_16x16x4f32 for the
+// 64x64-tile pipelines where it measured faster).
 //
 // Symbol and memref arguments follow the reference template
 // (lib/dsl/kernels/gemm.cpp:116-296): A [m,k], B [k,n], C [m,n], rank 2,
 // 21 parameters. The reference computes one element per lane with scalar
 // FMAs out of an 8 KiB LDS tile (gemm.cpp:265-296). Here:
 //
-//   * Workgroup = 256 threads (4 wave64s, 2x2) computing a BM x BN tile of C;
-//     each wave owns a quarter as WTM x WTN MFMA 32x32 accumulators. Four
-//     such symbols, all correct for every shape; the launcher scores each by
-//     its full-occupancy rate times how busy its last round of workgroups
-//     would be (kh_tiles.h) and takes the best, unless the launch has at most
-//     256 tiles of 32x32 (then `gemm_ksplit` / `gemm_ksplit_deep`, at the
-//     end of this file, split K over 8 waves instead):
+//   * Workgroup = 256 threads (4 wave64s, 2x2; `gemm_wide`: 512, 2x4)
+//     computing a BM x BN tile of C; each wave owns its part as WTM x WTN
+//     MFMA accumulator blocks. Five such symbols, all correct for every
+//     shape; the launcher scores each by its full-occupancy rate times how
+//     busy its last round of workgroups would be (kh_tiles.h) and takes the
+//     best, unless the launch has at most 256 tiles of 32x32 (then
+//     `gemm_ksplit` / `gemm_ksplit_deep`, at the end of this file, split K
+//     over 8 waves instead); a tune cache, when set, overrides the choice:
 //       `gemm`        128x256 tiles (64x128 per wave, 128 accumulator registers
 //                     per lane), 16-deep K slabs: the least LDS and L2 traffic
 //                     per MFMA (8192^3, 4096^3, 8192x8192x256); persistent
@@ -21,9 +23,12 @@
 //                     8192x1024x8192);
 //       `gemm_small`  64x64 tiles, for grids the larger tiles would fill
 //                     unevenly (768^3, 1024^3);
-//       `gemm_small_pf2` the same tiles with two-ahead prefetch, when they
-//                     number at least KH_GEMM_SMALL_PF2_TILES (2048^3 to
-//                     3584^3, 6144x6144x1024).
+//       `gemm_small_pf2` the same tiles on 16x16 MFMAs with two-ahead
+//                     prefetch, when they number more than one per CU
+//                     (1536^3 to 3584^3, 2048x2048x8192);
+//       `gemm_wide`   64x128 tiles on eight waves of 16x16 MFMAs, one
+//                     workgroup per CU, where its tiles fill whole rounds
+//                     (2048^3, 6144x6144x1024).
 //     Registers are capped for two waves per SIMD (two workgroups per CU, as
 //     LDS allows), so one workgroup's barrier and slab hand-over overlap the
 //     other's MFMAs. `gemm` and `gemm_mid` raise their waves' priority
@@ -71,8 +76,13 @@ static_assert(Tile<2, 4, 16, true>::BM == KH_GEMM_BM && Tile<2, 4, 16, true>::BN
 static_assert(Tile<2, 2, 32, false>::BM == KH_GEMM_MID_BM && Tile<2, 2, 32, false>::BN == KH_GEMM_MID_BN,
               "launcher tile size");
 static_assert(Tile<1, 1, 32, false>::BM == KH_GEMM_SMALL_BM && Tile<1, 1, 32, false>::BN == KH_GEMM_SMALL_BN &&
-                  Tile<1, 1, 16, false>::BM == KH_GEMM_SMALL_BM && Tile<1, 1, 16, false>::BN == KH_GEMM_SMALL_BN,
+                  Tile<2, 2, 32, false, 2, 2, 16>::BM == KH_GEMM_SMALL_BM &&
+                  Tile<2, 2, 32, false, 2, 2, 16>::BN == KH_GEMM_SMALL_BN,
               "launcher tile size (gemm_small and gemm_small_pf2)");
+static_assert(Tile<2, 2, 32, false, 2, 4, 16>::BM == KH_GEMM_WIDE_BM &&
+                  Tile<2, 2, 32, false, 2, 4, 16>::BN == KH_GEMM_WIDE_BN &&
+                  Tile<2, 2, 32, false, 2, 4, 16>::NT == KH_GEMM_WIDE_THREADS,
+              "launcher tile size (gemm_wide)");
 
 // The reference symbol: 128x256 tiles, persistent. Each workgroup loops
 // over tiles bid, bid + grid, ... (the launcher gives it min(tiles, two per
@@ -102,16 +112,35 @@ gemm_small(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(fl
   gemm_entry<1, 1, 32, false, false>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
 }
 
-// Same arguments and results with 64x64 tiles, 16-deep slabs prefetched two
-// ahead through registers: more loads in flight per CU, for grids of many
-// tiles (+5-7% over `gemm_small` from six tiles per CU, 2560^3 to
-// 6144x6144x1024). With one or two tiles per CU the fewer barriers of
-// `gemm_small`'s 32-deep slabs win (1024^3: 77 vs 71 TFLOP/s). A kernel of its
-// own: compiled into `gemm_small` behind a size test, both pipelines lost 4%.
+// Same arguments and results with 64x64 tiles on v_mfma_f32_16x16x4f32 (each
+// wave 32x32 as 2x2 blocks of 16x16), 32-deep slabs prefetched two ahead
+// through registers: more loads in flight per CU, for grids of many tiles.
+// The tune space found the 16x16 form faster than the same tiles on 32x32
+// MFMAs at every shape timed (rotated U[-1,1] inputs, warm clocks): 2048^3
+// 121.5 vs 117.0, 3072^3 123.4 vs 114.2, 2048x2048x8192 127.6 vs 108.1,
+// 6144x6144x1024 125.0 vs 121.1 TFLOP/s; level at 1536^3. With one tile per
+// CU the fewer barriers of `gemm_small` still win (1024^3: 73.9 vs 68.1).
 extern "C" __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_small_pf2(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
-  khg::gemm_entry_pipe<1, 1, 16, false, khg::kPipePrefetch2>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0,
-                                                             B_s0, C_s0);
+  khg::gemm_entry_pipe<2, 2, 32, true, khg::kPipePrefetch2, 2, 2, 16>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1,
+                                                                      A_n1, A_s0, B_s0, C_s0);
+}
+
+// Same arguments and results with 64x128 tiles on eight waves (2 x 4, each
+// 32x32 as 2x2 blocks of v_mfma_f32_16x16x4f32), 32-deep register-staged
+// slabs; one workgroup per CU. From the tune space: where its tiles fill
+// whole rounds of 256 it leads the 64x64 tiles (2048^3 124.5 vs 121.5,
+// 6144x6144x1024 129.0 vs 125.0, 2048x2048x8192 125.7 vs 108.1 for the
+// previous choice). The tile split assumes 512 threads: any other launch is
+// refused by writing NaN over C.
+extern "C" __global__ void __launch_bounds__(KH_GEMM_WIDE_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
+gemm_wide(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
+  if (blockDim.x != KH_GEMM_WIDE_THREADS || blockDim.y != 1 || blockDim.z != 1) {
+    khg::refuse_launch(KH_PTR(C), C_n0, C_n1, C_s0);
+    return;
+  }
+  khg::gemm_entry_pipe<2, 2, 32, true, khg::kPipeRegs, 2, 4, 16>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1,
+                                                                 A_s0, B_s0, C_s0);
 }
 
 

@@ -493,6 +493,17 @@ __device__ __forceinline__ void store_tile(const AccOf<T> (&acc)[WTM][WTN], floa
   }
 }
 
+// Writes NaN over C (grid-strided over the whole launch): how a kernel whose
+// tile split assumes one workgroup size refuses a launch with another,
+// instead of computing part of each tile.
+__device__ __forceinline__ void refuse_launch(float *C, int64_t M, int64_t N, int64_t ldc) {
+  const int64_t threads = (int64_t)blockDim.x * blockDim.y * blockDim.z;
+  const int64_t flat = ((int64_t)threadIdx.z * blockDim.y + threadIdx.y) * blockDim.x + threadIdx.x;
+  const int64_t block = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * gridDim.y * gridDim.z * threads;
+  for (int64_t i = block * threads + flat; i < M * N; i += stride) C[(i / N) * ldc + i % N] = __builtin_nanf("");
+}
+
 // Fast-path pipelines (gemm_body's PIPE).
 constexpr int kPipeRegs = 1;       // register-staged, one slab ahead
 constexpr int kPipeDma = 2;        // direct-to-LDS, three stages

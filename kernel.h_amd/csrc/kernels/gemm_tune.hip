@@ -14,21 +14,12 @@
 #endif
 
 // A candidate's tile split assumes its own workgroup size (64 WGM WGN
-// threads, one-dimensional); any other launch is refused by writing NaN over
-// C instead of computing part of the tile.
-__device__ __forceinline__ void refuse_launch(float *C, int64_t M, int64_t N, int64_t ldc) {
-  const int64_t threads = (int64_t)blockDim.x * blockDim.y * blockDim.z;
-  const int64_t flat = ((int64_t)threadIdx.z * blockDim.y + threadIdx.y) * blockDim.x + threadIdx.x;
-  const int64_t block = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
-  const int64_t stride = (int64_t)gridDim.x * gridDim.y * gridDim.z * threads;
-  for (int64_t i = block * threads + flat; i < M * N; i += stride) C[(i / N) * ldc + i % N] = __builtin_nanf("");
-}
-
+// threads, one-dimensional); any other launch is refused (khg::refuse_launch).
 #define KH_GEMM_TUNE_KERNEL(PART, MF, WGM, WGN, WTM, WTN, BK, PRIO, PIPE, SYM)                               \
   extern "C" __global__ void __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(2)))         \
   SYM(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {                        \
     if (blockDim.x != 64 * WGM * WGN || blockDim.y != 1 || blockDim.z != 1) {                                \
-      refuse_launch(KH_PTR(C), C_n0, C_n1, C_s0);                                                              \
+      khg::refuse_launch(KH_PTR(C), C_n0, C_n1, C_s0);                                                              \
       return;                                                                                                  \
     }                                                                                                          \
     khg::gemm_entry_pipe<WTM, WTN, BK, PRIO != 0, PIPE, WGM, WGN, MF>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0,  \

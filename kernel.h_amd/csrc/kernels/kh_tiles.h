@@ -24,27 +24,34 @@
 #define KH_GEMM_MID_BN 128
 #define KH_GEMM_SMALL_BM 64
 #define KH_GEMM_SMALL_BN 64
+// `gemm_wide`: 64x128 tiles on eight waves (512 threads), one workgroup per CU.
+#define KH_GEMM_WIDE_BM 64
+#define KH_GEMM_WIDE_BN 128
+#define KH_GEMM_WIDE_THREADS 512
 
-// The launcher's tile choice (khrt_templates.cpp, gemm_symbol): for each
-// symbol, score = its measured rate at full occupancy (TFLOP/s, MI355X,
-// 8192^3-class shapes) x the fraction of the last round of workgroups that
-// is busy, and take the best. `gemm` and `gemm_mid` run two workgroups per
-// CU, so a round is 2 x KH_GEMM_CUS tiles and a half-empty last round
-// costs a full one; `gemm_small`'s workgroups are light enough that a
-// partial round costs little, so its rounds are counted per CU. Fitted on
-// 14 shapes from 2048^3 to 8192^3 (square, skinny and rectangular): the
-// choice is the measured best or within 4% of it on all of them.
+// The launcher's tile choice (khrt_templates.cpp, heuristic_gemm_symbol):
+// for each symbol, score = its measured rate at full occupancy (TFLOP/s,
+// MI355X) x the fraction of the last round of workgroups that is busy, and
+// take the best. `gemm` and `gemm_mid` run two workgroups per CU, so a round
+// is 2 x KH_GEMM_CUS tiles and a half-empty last round costs a full one;
+// `gemm_wide` runs one per CU (a round of KH_GEMM_CUS tiles); the 64x64
+// tiles are light enough that a partial round costs little, so their rounds
+// are counted per CU. Fitted on 20 shapes from 1024^3 to 8192^3 (square,
+// skinny, rectangular, deep K) timed with rotated U[-1,1] inputs and warm
+// clocks: the choice is the measured best or within 3% of it on all of them.
 #define KH_GEMM_CUS 256
 #define KH_GEMM_ROUND_BIG (2 * KH_GEMM_CUS)
 #define KH_GEMM_ROUND_MID (2 * KH_GEMM_CUS)
+#define KH_GEMM_ROUND_WIDE KH_GEMM_CUS
 #define KH_GEMM_ROUND_SMALL KH_GEMM_CUS
 #define KH_GEMM_RATE_BIG 142
 #define KH_GEMM_RATE_MID 135
-#define KH_GEMM_RATE_SMALL 125
-// Where the 64x64 tiles are chosen and number at least this many (four per
-// CU), the launcher takes `gemm_small_pf2` (two-ahead prefetch) instead of
-// `gemm_small`.
-#define KH_GEMM_SMALL_PF2_TILES 1024
+#define KH_GEMM_RATE_WIDE 129
+#define KH_GEMM_RATE_SMALL 126
+// Where the 64x64 tiles are chosen and number more than this (one per CU),
+// the launcher takes `gemm_small_pf2` (16x16 MFMAs, two-ahead prefetch)
+// instead of `gemm_small`.
+#define KH_GEMM_SMALL_PF2_TILES 256
 // `gemm_ksplit`: 32x32 tiles, K split over the 8 waves of a 512-thread
 // workgroup. The launcher takes it when its tiles fit one round (at most
 // one workgroup per CU): there the larger tiles leave three CUs in four idle.

@@ -199,13 +199,14 @@ const GemmCandidate kGemmCandidates[] = {
     {"gemm", "gemm", 32, 2, 2, 2, 4, 16, 1, kPersistent, true},
     {"gemm_mid", "gemm", 32, 2, 2, 2, 2, 32, 1, kRegs, true},
     {"gemm_small", "gemm", 32, 2, 2, 1, 1, 32, 0, kRegs, true},
-    {"gemm_small_pf2", "gemm", 32, 2, 2, 1, 1, 16, 0, kPf2, true},
+    {"gemm_small_pf2", "gemm", 16, 2, 2, 2, 2, 32, 1, kPf2, true},
+    {"gemm_wide", "gemm", 16, 2, 4, 2, 2, 32, 1, kRegs, true},
     {"gemm_ksplit", "gemm", 32, 1, 1, 1, 1, 8, 0, kKsplit, true},
     {"gemm_ksplit_deep", "gemm", 32, 1, 1, 1, 1, 8, 0, kKsplitDeep, true},
     KH_GEMM_TUNE_CONFIGS(KH_TUNE_CANDIDATE)};
 #undef KH_TUNE_CANDIDATE
 constexpr int kGemmCandidateCount = static_cast<int>(sizeof(kGemmCandidates) / sizeof(kGemmCandidates[0]));
-static_assert(kGemmCandidateCount == 6 + KH_GEMM_TUNE_COUNT, "candidate table");
+static_assert(kGemmCandidateCount == 7 + KH_GEMM_TUNE_COUNT, "candidate table");
 
 const GemmCandidate *find_gemm_candidate(const char *symbol) {
   if (symbol == nullptr) return nullptr;
@@ -328,12 +329,15 @@ const char *heuristic_gemm_symbol(int64_t m, int64_t n, int64_t k) {
                                 KH_GEMM_RATE_BIG);
   const double mid = gemm_score(ceil_div(m, KH_GEMM_MID_BM) * ceil_div(n, KH_GEMM_MID_BN), KH_GEMM_ROUND_MID,
                                 KH_GEMM_RATE_MID);
+  const double wide = gemm_score(ceil_div(m, KH_GEMM_WIDE_BM) * ceil_div(n, KH_GEMM_WIDE_BN), KH_GEMM_ROUND_WIDE,
+                                 KH_GEMM_RATE_WIDE);
   const double small = gemm_score(ceil_div(m, KH_GEMM_SMALL_BM) * ceil_div(n, KH_GEMM_SMALL_BN),
                                   KH_GEMM_ROUND_SMALL, KH_GEMM_RATE_SMALL);
-  if (big >= mid && big >= small) return "gemm";
-  if (mid > small) return "gemm_mid";
+  if (big >= mid && big >= wide && big >= small) return "gemm";
+  if (mid >= wide && mid > small) return "gemm_mid";
+  if (wide > small) return "gemm_wide";
   const int64_t tiles64 = ceil_div(m, KH_GEMM_SMALL_BM) * ceil_div(n, KH_GEMM_SMALL_BN);
-  return tiles64 >= KH_GEMM_SMALL_PF2_TILES ? "gemm_small_pf2" : "gemm_small";
+  return tiles64 > KH_GEMM_SMALL_PF2_TILES ? "gemm_small_pf2" : "gemm_small";
 }
 
 // The launcher's GEMM candidate: the tune cache's choice for this shape when

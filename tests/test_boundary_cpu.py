@@ -269,9 +269,9 @@ def test_kernarg_segment_is_2n_plus_3_slots(name, nslots):
     ("gemm", "m=4096,n=4096,k=64", (512, 1, 1), (256, 1, 1)),         # exactly one round
     ("gemm", "m=12288,n=12288,k=1024", (512, 1, 1), (256, 1, 1)),    # 4608 tiles: 9 per workgroup
     ("gemm", "m=8192,n=1024,k=8192", (512, 1, 1), (256, 1, 1)),       # 128x128 (gemm_mid): 512 tiles
-    ("gemm", "m=6144,n=6144,k=1024", (9216, 1, 1), (256, 1, 1)),      # 64x64: 128x256 would fill 2.25 rounds
+    ("gemm", "m=6144,n=6144,k=1024", (4608, 1, 1), (512, 1, 1)),      # gemm_wide: 64x128, 18 full rounds
     ("gemm", "m=3072,n=3072,k=3072", (2304, 1, 1), (256, 1, 1)),      # 64x64 (gemm_small_pf2)
-    ("gemm", "m=2048,n=2048,k=2048", (1024, 1, 1), (256, 1, 1)),      # 64x64: 128x128 would half-fill
+    ("gemm", "m=2048,n=2048,k=2048", (512, 1, 1), (512, 1, 1)),       # gemm_wide: 64x128 on 8 waves, 2 rounds
     ("gemm", "m=1024,n=1024,k=1024", (256, 1, 1), (256, 1, 1)),       # 64x64
     ("gemm", "m=512,n=512,k=512", (256, 1, 1), (512, 1, 1)),        # gemm_ksplit: 256 tiles of 32x32, 8 waves
     ("gemm", "m=768,n=768,k=768", (144, 1, 1), (256, 1, 1)),        # 576 tiles of 32x32: 64x64 instead
@@ -288,7 +288,8 @@ def test_launcher_geometry(name, shape, grid, block):
     ("gemm", "m=8192,n=1024,k=8192", "gemm_mid"),
     ("gemm", "m=1024,n=1024,k=1024", "gemm_small"),
     ("gemm", "m=3072,n=3072,k=3072", "gemm_small_pf2"),   # >= 1024 tiles of 64x64
-    ("gemm", "m=2048,n=2048,k=2048", "gemm_small_pf2"),
+    ("gemm", "m=2048,n=2048,k=2048", "gemm_wide"),
+    ("gemm", "m=1536,n=1536,k=1536", "gemm_small_pf2"),  # 576 tiles of 64x64: more than one per CU
     ("gemm", "m=512,n=512,k=2048", "gemm_ksplit_deep"),   # 256 tiles of 32x32, deep K
     ("gemm", "m=512,n=512,k=1024", "gemm_ksplit"),
     ("gemm", "m=300,n=520,k=100", "gemm_ksplit"),
@@ -393,7 +394,8 @@ def test_elf_image_size_refuses_what_is_not_a_code_object():
 
 # ------------------------------------------------------------------ GEMM candidates / tune space
 
-_PRODUCT_GEMM = ["gemm", "gemm_mid", "gemm_small", "gemm_small_pf2", "gemm_ksplit", "gemm_ksplit_deep"]
+_PRODUCT_GEMM = ["gemm", "gemm_mid", "gemm_small", "gemm_small_pf2", "gemm_wide", "gemm_ksplit",
+                 "gemm_ksplit_deep"]
 
 
 def _notes(co):
@@ -412,10 +414,11 @@ def test_tune_list_is_the_generators_output():
 
 def test_gemm_candidate_table():
     cands = kh.gemm_candidates()
-    assert [c["symbol"] for c in cands[:6]] == _PRODUCT_GEMM
-    assert all(c["product"] == 1 for c in cands[:6]) and not any(c["product"] for c in cands[6:])
+    np_ = len(_PRODUCT_GEMM)
+    assert [c["symbol"] for c in cands[:np_]] == _PRODUCT_GEMM
+    assert all(c["product"] == 1 for c in cands[:np_]) and not any(c["product"] for c in cands[np_:])
     assert len({c["symbol"] for c in cands}) == len(cands)
-    space = cands[6:]
+    space = cands[np_:]
     # The reference's axes (autotuner.hpp:36-41) all vary over the space,
     # re-pruned for MFMA tiles: both MFMA shapes, 4 and 8 waves, BM/BN in
     # {64,128,256}, BK in {16,32}, unroll 1 and 2.
@@ -445,6 +448,7 @@ def test_gemm_candidate_table():
     ("gemm", 256, 512, 64, 4, 256),                  # fewer tiles than slots
     ("gemm_mid", 1000, 1000, 8, 64, 256),
     ("gemm_ksplit", 512, 512, 512, 256, 512),
+    ("gemm_wide", 2048, 2048, 2048, 512, 512),
     ("gemm_m16_w2x4_t4x2_k16_p1_dma", 1000, 1000, 64, 64, 512),   # 128 x 128 tiles, 8 waves
 ])
 def test_gemm_candidate_geometry(symbol, m, n, k, grid, block):

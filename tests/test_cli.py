@@ -205,7 +205,7 @@ def test_tune_evaluates_candidates_and_caches(dev, tmp_path):
     assert (by["gemm"]["bm"], by["gemm"]["bn"], by["gemm"]["waves"], by["gemm"]["unroll"]) == ("128", "256", "4", "2")
     assert (by["gemm_mid"]["unroll"], by["gemm_ksplit"]["waves"], by["gemm_ksplit_deep"]["unroll"]) == ("1", "8", "3")
     assert {row["vec"] for row in rows} == {"4"}  # k, n multiples of 4: dwordx4 loads
-    assert all(row["product"] == ("1" if i < 6 else "0") for i, row in enumerate(rows))
+    assert all(row["product"] == ("1" if i < 7 else "0") for i, row in enumerate(rows))
     best = min(rows, key=lambda row: float(row["ms_median"]))["symbol"]
     assert f"best config: {best} " in r.stdout
     r2 = run(*args)

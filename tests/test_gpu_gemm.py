@@ -93,7 +93,7 @@ def test_gemm_reference_geometry_and_negative_control(dev):
     assert O.rel_frobenius(C, wrong) > 1e-5
 
 
-@pytest.mark.parametrize("symbol", ["gemm", "gemm_mid", "gemm_small", "gemm_small_pf2", "gemm_ksplit",
+@pytest.mark.parametrize("symbol", ["gemm", "gemm_mid", "gemm_small", "gemm_small_pf2", "gemm_wide", "gemm_ksplit",
                                     "gemm_ksplit_deep"])
 @pytest.mark.parametrize("m,n,k", [(256, 256, 256), (1000, 1000, 1000), (64, 192, 4097), (129, 65, 33),
                                    (3, 5, 7), (512, 2048, 96),
@@ -115,7 +115,8 @@ def test_every_gemm_symbol_at_every_shape(dev, symbol, m, n, k):
     dA, dB, dC = up(A), up(B), empty(m * n)
     args = kh.LaunchArgs().add_memref(dA, [m, k]).add_memref(dB, [k, n]).add_memref(dC, [m, n])
     say(f"{symbol} m={m} n={n} k={k}")
-    kh.kernel_launch(f, (37, 1, 1), (256, 1, 1), args)  # grid-strided: any grid
+    block = 512 if symbol == "gemm_wide" else 256  # gemm_wide's tile split is for 8 waves
+    kh.kernel_launch(f, (37, 1, 1), (block, 1, 1), args)  # grid-strided: any grid
     C = down(dC, m * n).reshape(m, n)
     if k <= 4096:
         assert np.array_equal(C, (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
@@ -130,8 +131,8 @@ def test_gemm_symbols_random_shapes_exact(dev):
     equal the fp64 product bit for bit whatever the tiling and grid."""
     rng = np.random.default_rng(20261201)
     mod = kh.GpuModule(kh.code_object("gemm"))
-    fns = {sym: mod.get_function(sym) for sym in ("gemm", "gemm_mid", "gemm_small", "gemm_small_pf2", "gemm_ksplit",
-                                                       "gemm_ksplit_deep")}
+    fns = {sym: mod.get_function(sym) for sym in ("gemm", "gemm_mid", "gemm_small", "gemm_small_pf2", "gemm_wide",
+                                                       "gemm_ksplit", "gemm_ksplit_deep")}
     for _ in range(30):
         m, n = int(rng.integers(1, 700)), int(rng.integers(1, 700))
         k = int(rng.choice([int(rng.integers(1, 60)), int(rng.integers(1, 500))]))
@@ -144,7 +145,8 @@ def test_gemm_symbols_random_shapes_exact(dev):
         args = kh.LaunchArgs().add_memref(dA, [m, k]).add_memref(dB, [k, n]).add_memref(dC, [m, n])
         for sym, f in fns.items():
             grid = int(rng.choice([1, 3, 8, 37, 512]))
-            block = int(rng.choice([64, 192, 512])) if sym.startswith("gemm_ksplit") else 256  # 1, 3 or 8 waves
+            block = (int(rng.choice([64, 192, 512])) if sym.startswith("gemm_ksplit")  # 1, 3 or 8 waves
+                     else 512 if sym == "gemm_wide" else 256)
             say(f"{sym} m={m} n={n} k={k} grid={grid} block={block}")
             kh.kernel_launch(f, (grid, 1, 1), (block, 1, 1), args)
             assert np.array_equal(down(dC, m * n).reshape(m, n), want), (sym, m, n, k, grid)
@@ -175,7 +177,8 @@ def test_gemm_padded_c_rows(dev, extra):
 
 @pytest.mark.parametrize("m,n,k,grid", [
     (8192, 8192, 256, 512),     # gemm: 2048 tiles of 128x256 over 512 persistent workgroups
-    (6144, 6144, 1024, 9216),   # gemm_small_pf2: 128x256 tiles would fill 2.25 rounds
+    (6144, 6144, 1024, 4608),   # gemm_wide: 4608 tiles of 64x128 at 512 threads, 18 full rounds
+    (2048, 2048, 8192, 512),    # gemm_wide, deep K
     (3072, 3072, 3072, 2304),   # gemm_small_pf2 (2304 tiles of 64x64)
     (8192, 1024, 8192, 512),    # gemm_mid: 512 tiles of 128x128
     (4096, 4096, 4096, 512),    # gemm: one full round of 128x256
@@ -231,10 +234,11 @@ def test_tune_candidate_refuses_another_block_size(dev):
     A, B = O.gemm_int_inputs(m, n, k)
     dA, dB, dC = up(A), up(B), empty(m * n, 0.0)
     args = kh.LaunchArgs().add_memref(dA, [m, k]).add_memref(dB, [k, n]).add_memref(dC, [m, n])
-    sym = next(c["symbol"] for c in kh.gemm_candidates() if c["waves"] == 8 and not c["product"])
-    say(f"{sym} at 256 threads (refused)")
-    kh.kernel_launch(kh.gemm_candidate_function(sym), (4, 1, 1), (256, 1, 1), args)
-    assert np.all(np.isnan(down(dC, m * n)))
+    for sym in ("gemm_wide", next(c["symbol"] for c in kh.gemm_candidates() if c["waves"] == 8 and not c["product"])):
+        dC.fill(0.0)
+        say(f"{sym} at 256 threads (refused)")
+        kh.kernel_launch(kh.gemm_candidate_function(sym), (4, 1, 1), (256, 1, 1), args)
+        assert np.all(np.isnan(down(dC, m * n))), sym
 
 
 def test_tune_cache_steers_the_launcher(dev, tmp_path):
