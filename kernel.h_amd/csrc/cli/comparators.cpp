@@ -4,6 +4,7 @@
 #include "khrt.h"
 
 #include <dlfcn.h>
+#include <hipblaslt/hipblaslt.h>
 #include <rocblas/rocblas.h>
 
 #include <algorithm>
@@ -254,6 +255,121 @@ bool prepare_rocblas_gemm(const std::map<std::string, int64_t> &s, Bufs &b, std:
                                       static_cast<rocblas_int>(k), &one, B, static_cast<rocblas_int>(n), A,
                                       static_cast<rocblas_int>(k), &zero, C, static_cast<rocblas_int>(n));
     return st == rocblas_status_success ? 0 : 1;
+  };
+  work = 2.0 * m * n * k;
+  return true;
+}
+
+namespace {
+
+// hipBLASLt through its C API, dlopen'ed like rocBLAS: one handle, and per
+// shape one matmul description, three column-major layouts, the heuristic's
+// first algorithm and its workspace (kept for the process lifetime, a few
+// shapes per run).
+struct Hipblaslt {
+  using create_t = hipblasStatus_t (*)(hipblasLtHandle_t *);
+  using desc_create_t = hipblasStatus_t (*)(hipblasLtMatmulDesc_t *, hipblasComputeType_t, hipDataType);
+  using layout_create_t = hipblasStatus_t (*)(hipblasLtMatrixLayout_t *, hipDataType, uint64_t, uint64_t, int64_t);
+  using pref_create_t = hipblasStatus_t (*)(hipblasLtMatmulPreference_t *);
+  using pref_set_t = hipblasStatus_t (*)(hipblasLtMatmulPreference_t, hipblasLtMatmulPreferenceAttributes_t,
+                                         const void *, size_t);
+  using heuristic_t = hipblasStatus_t (*)(hipblasLtHandle_t, hipblasLtMatmulDesc_t, hipblasLtMatrixLayout_t,
+                                          hipblasLtMatrixLayout_t, hipblasLtMatrixLayout_t, hipblasLtMatrixLayout_t,
+                                          hipblasLtMatmulPreference_t, int, hipblasLtMatmulHeuristicResult_t[],
+                                          int *);
+  using matmul_t = hipblasStatus_t (*)(hipblasLtHandle_t, hipblasLtMatmulDesc_t, const void *, const void *,
+                                       hipblasLtMatrixLayout_t, const void *, hipblasLtMatrixLayout_t, const void *,
+                                       const void *, hipblasLtMatrixLayout_t, void *, hipblasLtMatrixLayout_t,
+                                       const hipblasLtMatmulAlgo_t *, void *, size_t, hipStream_t);
+  void *lib = nullptr;
+  create_t create = nullptr;
+  desc_create_t desc_create = nullptr;
+  layout_create_t layout_create = nullptr;
+  pref_create_t pref_create = nullptr;
+  pref_set_t pref_set = nullptr;
+  heuristic_t heuristic = nullptr;
+  matmul_t matmul = nullptr;
+  hipblasLtHandle_t handle = nullptr;
+  std::string error;
+
+  template <class F>
+  bool sym(F &f, const char *name) {
+    f = reinterpret_cast<F>(dlsym(lib, name));
+    if (!f) error = std::string("libhipblaslt lacks ") + name;
+    return f != nullptr;
+  }
+
+  Hipblaslt() {
+    for (const char *name : {"libhipblaslt.so.1", "libhipblaslt.so", "/opt/rocm/lib/libhipblaslt.so"}) {
+      lib = dlopen(name, RTLD_NOW | RTLD_LOCAL);
+      if (lib) break;
+    }
+    if (!lib) {
+      error = "libhipblaslt not found";
+      return;
+    }
+    if (!sym(create, "hipblasLtCreate") || !sym(desc_create, "hipblasLtMatmulDescCreate") ||
+        !sym(layout_create, "hipblasLtMatrixLayoutCreate") || !sym(pref_create, "hipblasLtMatmulPreferenceCreate") ||
+        !sym(pref_set, "hipblasLtMatmulPreferenceSetAttribute") ||
+        !sym(heuristic, "hipblasLtMatmulAlgoGetHeuristic") || !sym(matmul, "hipblasLtMatmul")) {
+      return;
+    }
+    if (create(&handle) != HIPBLAS_STATUS_SUCCESS) error = "hipblasLtCreate failed";
+  }
+};
+
+Hipblaslt &hipblaslt() {
+  static Hipblaslt h;
+  return h;
+}
+
+}  // namespace
+
+bool prepare_hipblaslt_gemm(const std::map<std::string, int64_t> &s, Bufs &b, std::function<int()> &launch,
+                            double &work, std::string &error) {
+  Hipblaslt &h = hipblaslt();
+  if (!h.error.empty()) {
+    error = h.error;
+    return false;
+  }
+  const int64_t m = get(s, "m"), n = get(s, "n"), k = get(s, "k");
+  float *A = b.alloc(m * k, 1.0f), *B = b.alloc(k * n, 1.0f), *C = b.alloc(m * n, 0.0f);
+  if (!A || !B || !C) {
+    error = "hipblaslt buffer allocation failed";
+    return false;
+  }
+  // Row-major C = A B as column-major C^T (n x m) = B^T (n x k) A^T (k x m),
+  // fp32 data, fp32 compute, no transposes.
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t lx = nullptr, ly = nullptr, lc = nullptr;
+  hipblasLtMatmulPreference_t pref = nullptr;
+  if (h.desc_create(&desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS ||
+      h.layout_create(&lx, HIP_R_32F, n, k, n) != HIPBLAS_STATUS_SUCCESS ||
+      h.layout_create(&ly, HIP_R_32F, k, m, k) != HIPBLAS_STATUS_SUCCESS ||
+      h.layout_create(&lc, HIP_R_32F, n, m, n) != HIPBLAS_STATUS_SUCCESS ||
+      h.pref_create(&pref) != HIPBLAS_STATUS_SUCCESS) {
+    error = "hipblaslt descriptor creation failed";
+    return false;
+  }
+  const uint64_t ws_bytes = 64ull << 20;
+  h.pref_set(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws_bytes, sizeof ws_bytes);
+  auto result = std::make_shared<hipblasLtMatmulHeuristicResult_t>();
+  int found = 0;
+  if (h.heuristic(h.handle, desc, lx, ly, lc, lc, pref, 1, result.get(), &found) != HIPBLAS_STATUS_SUCCESS ||
+      found < 1) {
+    error = "hipblaslt has no fp32 algorithm for this shape";
+    return false;
+  }
+  float *ws = result->workspaceSize > 0 ? b.alloc(static_cast<int64_t>((result->workspaceSize + 3) / 4), 0.0f) : nullptr;
+  if (result->workspaceSize > 0 && ws == nullptr) {
+    error = "hipblaslt workspace allocation failed";
+    return false;
+  }
+  launch = [=, &h] {
+    const float one = 1.0f, zero = 0.0f;
+    const hipblasStatus_t st = h.matmul(h.handle, desc, &one, B, lx, A, ly, &zero, C, lc, C, lc, &result->algo, ws,
+                                        result->workspaceSize, nullptr);
+    return st == HIPBLAS_STATUS_SUCCESS ? 0 : 1;
   };
   work = 2.0 * m * n * k;
   return true;

@@ -1,6 +1,6 @@
 // Comparator rows for `kernelh bench`: the hand-written HIP baselines
 // (hipref-naive / hipref-vec, roofline_fma) from the code object embedded in
-// the CLI, and rocBLAS fp32 GEMM as the vendor comparator.
+// the CLI, and rocBLAS and hipBLASLt fp32 GEMM as the vendor comparators.
 //
 // Mirrors the reference's bench backends (bench/harness/hipref_backend.cpp,
 // rocblas_backend.cpp, roofline.cpp:100-145): same symbols, launch geometry
@@ -35,5 +35,11 @@ bool prepare_roofline_fma(Bufs &b, std::function<int()> &launch, double &work, s
 // error, not a crash, when librocblas is absent).
 bool prepare_rocblas_gemm(const std::map<std::string, int64_t> &shape, Bufs &b, std::function<int()> &launch,
                           double &work, std::string &error);
+
+// hipBLASLt fp32 GEMM (hipblasLtMatmul with the heuristic's first algorithm
+// and up to 64 MiB of workspace), the same product and layout as the
+// rocBLAS row; dlopen'ed, an error when absent or without an fp32 algorithm.
+bool prepare_hipblaslt_gemm(const std::map<std::string, int64_t> &shape, Bufs &b, std::function<int()> &launch,
+                            double &work, std::string &error);
 
 }  // namespace khcli

@@ -5,7 +5,7 @@
 //                   [--resources]                          (main.cpp:435-646)
 //   kernelh tune    --kernel gemm --shape m=..,n=..,k=.. --out <dir> [...]
 //                                                          (main.cpp:649-1420)
-//   kernelh bench   --suite <roofline|kernelh|rocblas|hipref|all> --out <path>
+//   kernelh bench   --suite <roofline|kernelh|rocblas|hipblaslt|hipref|all> --out <path>
 //                   [--occupancy] [--kernel <name> --shape ... [--backend <b>]]
 //                                                          (main.cpp:2154-2228)
 // Exit codes as in the reference (main.cpp:125-127, run_bench.hpp:9-10):
@@ -19,7 +19,7 @@
 // one object serves every shape.
 //
 // bench backends (bench/harness/run_bench.cpp:48-66): kernelh (the gfx950
-// templates), rocblas (vendor fp32 GEMM), hipref-naive / hipref-vec
+// templates), rocblas and hipblaslt (vendor fp32 GEMM), hipref-naive / hipref-vec
 // (hand-written HIP comparators embedded in this executable) and roofline
 // (triad bandwidth, vector FMA ceiling).
 // bench times each row with the reference's method: 5 warmup launches, then
@@ -72,9 +72,9 @@ void usage(std::ostream &os) {
      << "  --shape m=..,n=..,k=.. --out <dir> [--max-candidates n] [--timeout s]\n"
      << "  [--cache path]; writes <dir>/tune-results.csv, prints the best config\n\n"
      << "bench options:\n"
-     << "  --suite <name>        roofline, kernelh, rocblas, hipref, all (default: all)\n"
-     << "  --backend <name>      with --kernel: kernelh (default), rocblas, hipref-naive,\n"
-     << "                        hipref-vec, roofline\n"
+     << "  --suite <name>        roofline, kernelh, rocblas, hipblaslt, hipref, all (default: all)\n"
+     << "  --backend <name>      with --kernel: kernelh (default), rocblas, hipblaslt,\n"
+     << "                        hipref-naive, hipref-vec, roofline\n"
      << "  --kernel <name>       single-row mode: time one template ...\n"
      << "  --shape k=v,...       ... at this shape\n"
      << "  --out <path>          results.csv path or directory (required)\n"
@@ -271,7 +271,7 @@ int run_compile(int argc, char **argv) {
 
 struct Row {
   std::string kernel, shape;
-  std::string backend = "kernelh";  // kernelh, rocblas, hipref-naive, hipref-vec, roofline
+  std::string backend = "kernelh";  // kernelh, rocblas, hipblaslt, hipref-naive, hipref-vec, roofline
 };
 
 using khcli::Bufs;
@@ -302,6 +302,14 @@ bool prepare(const Row &row, Bufs &b, std::function<int()> &launch, double &work
     }
     flops = true;
     return khcli::prepare_rocblas_gemm(s, b, launch, work, error);
+  }
+  if (row.backend == "hipblaslt") {
+    if (k != "gemm") {
+      error = "hipblaslt backend only benchmarks gemm (got '" + k + "')";
+      return false;
+    }
+    flops = true;
+    return khcli::prepare_hipblaslt_gemm(s, b, launch, work, error);
   }
   if (k == "roofline_fma") {
     flops = true;
@@ -448,12 +456,13 @@ std::vector<Row> suite_rows(const std::string &suite) {
   }
   if (suite == "kernelh" || suite == "all") add(kernelh_rows());
   if (suite == "rocblas" || suite == "all") add(gemm_rows("rocblas"));
+  if (suite == "hipblaslt" || suite == "all") add(gemm_rows("hipblaslt"));
   if (suite == "hipref" || suite == "all") add(hipref_rows());
   return rows;
 }
 
 bool known_suite(const std::string &s) {
-  return s == "all" || s == "roofline" || s == "kernelh" || s == "rocblas" || s == "hipref";
+  return s == "all" || s == "roofline" || s == "kernelh" || s == "rocblas" || s == "hipblaslt" || s == "hipref";
 }
 
 int write_occupancy(const fs::path &dir, const std::vector<std::string> &kernels) {
@@ -529,12 +538,12 @@ int run_bench(int argc, char **argv) {
       return kExitUsage;
     }
   }
-  const bool known_backend = backend == "kernelh" || backend == "rocblas" || backend == "hipref-naive" ||
-                             backend == "hipref-vec" || backend == "roofline";
+  const bool known_backend = backend == "kernelh" || backend == "rocblas" || backend == "hipblaslt" ||
+                             backend == "hipref-naive" || backend == "hipref-vec" || backend == "roofline";
   if (out.empty() || !known_suite(suite) || !known_backend || iters < 1 || warmup < 0 ||
       (!kernel.empty() && shape.empty())) {
-    std::cerr << "error: bench needs --out, a suite of roofline|kernelh|rocblas|hipref|all, a backend of "
-                 "kernelh|rocblas|hipref-naive|hipref-vec|roofline, and --shape with --kernel\n";
+    std::cerr << "error: bench needs --out, a suite of roofline|kernelh|rocblas|hipblaslt|hipref|all, a backend of "
+                 "kernelh|rocblas|hipblaslt|hipref-naive|hipref-vec|roofline, and --shape with --kernel\n";
     return kExitUsage;
   }
   fs::path csv = out;

@@ -152,6 +152,7 @@ def test_bench_single_row_results_csv(dev, tmp_path):
 @pytest.mark.gpu
 @pytest.mark.parametrize("kernel,shape,backend", [
     ("gemm", "m=512,n=512,k=512", "rocblas"),
+    ("gemm", "m=512,n=512,k=512", "hipblaslt"),
     ("gemm", "m=512,n=512,k=512", "hipref-naive"),
     ("softmax", "rows=4096,cols=1024", "hipref-vec"),
     ("scan", "n=100000", "hipref-naive"),

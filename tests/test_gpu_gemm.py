@@ -103,7 +103,10 @@ def test_gemm_reference_geometry_and_negative_control(dev):
                                    (2048, 2048, 260), (2112, 2048, 36), (2049, 2048, 33),
                                    # gemm's persistent cases: two slabs per tile (k = 20), one
                                    # slab (k = 16, its per-tile fallback), edge tiles in m and n.
-                                   (300, 520, 20), (256, 512, 16), (1000, 1028, 100)])
+                                   (300, 520, 20), (256, 512, 16), (1000, 1028, 100),
+                                   # gemm's tail-free slab loads (K a multiple of 16, N of 256)
+                                   # with edge tiles in m, and the smallest such K.
+                                   (1000, 512, 64), (77, 256, 48), (520, 768, 32)])
 def test_every_gemm_symbol_at_every_shape(dev, symbol, m, n, k):
     # Integer fill: exact in fp32, so both tilings must agree bit for bit.
     A, B = O.gemm_int_inputs(m, n, k) if k <= 4096 else (None, None)
