@@ -44,14 +44,16 @@ ROTATE_BYTES = 1 << 30  # rotate buffer sets until the working set exceeds 1 GiB
 
 METRIC = "GEMM-8192 fp32 TFLOPS + softmax/scan HBM GB/s, % of MI355X roofline"
 
-# HBM bytes per launch of the headline kernels, taken from two rocprofv3
-# --pmc passes (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000: the factors a copy
-# kernel of known size reads) over `bench.py --kernels <name>` with its
-# buffer rotation, recorded in profiles/templates_baseline_sizes_hbm_traffic.md.
-# Constants of that profile, not measured by the run that reports them.
+# HBM bytes per launch of every configuration, from two rocprofv3 --pmc passes
+# (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000: the factors a copy kernel of known
+# size reads) over `bench.py --steps 2 --warmup 1 --no-cpu --no-ceilings` with
+# its buffer rotation (working sets past 1 GiB), recorded in
+# profiles/templates_baseline_sizes_hbm_traffic.md. Constants of that profile
+# (median dispatch), not measured by the run that reports them.
 PMC_TRAFFIC_BYTES = {
-    "vecadd": 201374080, "softmax": 33634176, "layernorm": 33737882, "scan": 539377210,
-    "fused_gelu": 537017626, "gemm": 4281652941, "attention": 1208230925,
+    "vecadd": 201381888, "softmax": 33636224, "layernorm": 33738880, "scan": 539398176, "scan_1e6": 8324160,
+    "fused_gelu": 537011456, "fused_gelu_2^22": 33635840, "gemm": 4282522112, "gemm_8192x8192x256": 375275904,
+    "gemm_2048": 117561856, "gemm_512": 10656640, "attention": 1208265984, "attention_s1024": 302283008,
 }
 PMC_TRAFFIC_SOURCE = "profiles/templates_baseline_sizes_hbm_traffic.md (constant, not measured by this run)"
 
