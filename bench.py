@@ -30,6 +30,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import struct
 import sys
 import time
 
@@ -204,9 +205,10 @@ def measure_ceilings(kh, stream, hbm_cases, prime, steps):
     256) and 32 grid-strided workgroups per CU. A kernel's ceiling is the
     best of the 3 GiB streams and its own-size streams.
 
-    fp32 MFMA: 8 independent v_mfma_f32_32x32x2f32 chains per wave, two waves
-    per SIMD, ~2 ms per launch (shorter launches under-measure it, as the
-    clock has not settled and launch gaps count)."""
+    fp32 MFMA: independent chains of each fp32 MFMA shape (8 of 32x32x2 or
+    16 of 16x16x4 per wave), two waves per SIMD, ~3.5 ms per launch (shorter
+    launches under-measure it, as the clock has not settled and launch gaps
+    count); the best of three sequences of ten launches, the faster shape."""
     co = os.path.join(REPO, "kernel.h_amd", "build", "co", "roofline.hsaco")
     with open(co, "rb") as f:
         mod = kh.GpuModule(f.read())
@@ -255,15 +257,26 @@ def measure_ceilings(kh, stream, hbm_cases, prime, steps):
         best, rows = streams({"copy": int(c.work // 8), "triad": int(c.work // 12)}, steps, rotate=True)
         per_case[c.name] = {"gbps": max(big_best, best), "own_size_best": best, "streams": rows}
 
-    blocks, iters = cu * 2, 4096
+    # Both fp32 MFMA shapes, ~3.5 ms launches, ten per sequence; the best of
+    # three sequences each (clocks settle over the first launches).
+    blocks, iters = cu * 2, 8192
     out = kh.Buffer(4 * blocks * 256)
-    flops = float(blocks) * 4 * iters * 8 * 4096
-    kh.roofline_mfma(out, blocks, iters, stream)
-    t_mfma = time_queued(kh, stream, [lambda: kh.roofline_mfma(out, blocks, iters, stream)] * 5, prime)
+    args16 = kh.LaunchArgs().add_memref(out, [blocks * 256]).add_scalar_bytes(struct.pack("<q", iters))
+    mfma16 = mod.get_function("roofline_mfma16")
+    runs = {"v_mfma_f32_32x32x2f32": (float(blocks) * 4 * iters * 8 * 32 * 32 * 2 * 2,
+                                      lambda: kh.roofline_mfma(out, blocks, iters, stream)),
+            "v_mfma_f32_16x16x4f32": (float(blocks) * 4 * iters * 16 * 16 * 16 * 4 * 2,
+                                      lambda: kh.launch_raw(mfma16, (blocks, 1, 1), (256, 1, 1), args16, stream))}
+    mfma_rates = {}
+    for name, (flops, call) in runs.items():
+        call()
+        best = min(time_queued(kh, stream, [call] * 10, prime) for _ in range(3))
+        mfma_rates[name] = flops / (best * 1e-3) / 1e12
     out.free()
     return {"hbm_3GiB_best_gbps": big_best, "hbm_3GiB_streams": big_rows, "hbm_per_kernel": per_case,
-            "fp32_mfma_tflops": flops / (t_mfma * 1e-3) / 1e12,
-            "mfma_config": f"{blocks} workgroups x 4 waves x {iters} x 8 v_mfma_f32_32x32x2f32"}
+            "fp32_mfma_tflops": max(mfma_rates.values()), "fp32_mfma_by_instruction": mfma_rates,
+            "mfma_config": f"{blocks} workgroups x 4 waves x {iters} rounds of independent chains "
+                           "(8 of 32x32x2 or 16 of 16x16x4 per wave), best of 3 sequences of 10 launches"}
 
 
 def _median_runs(fn, runs=3, long_s=10.0):

@@ -8,6 +8,7 @@
 //   roofline_copy   dst = src: a kernel of exactly known traffic, used to
 //                   calibrate the FETCH_SIZE / WRITE_SIZE counters.
 //   roofline_mfma   back-to-back independent v_mfma_f32_32x32x2f32 chains
+//   roofline_mfma16 the same with v_mfma_f32_16x16x4f32
 //                   per wave (4096 FLOP each), no memory traffic in the
 //                   loop: the attainable fp32 matrix rate.
 //
@@ -87,6 +88,29 @@ roofline_mfma(KH_MEMREF1(float, out), int64_t iters) {
   for (int j = 0; j < 8; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) s += acc[j][r];
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid < out_n0) KH_PTR(out)[gid] = s;
+}
+
+// The same with v_mfma_f32_16x16x4f32 (the same rate per CU, a quarter of the
+// work per instruction): 16 independent chains per wave.
+typedef float v4f __attribute__((ext_vector_type(4)));
+extern "C" __global__ void __launch_bounds__(256)
+roofline_mfma16(KH_MEMREF1(float, out), int64_t iters) {
+  const int lane = kh::lane_id();
+  const float a = 1.0f + 1e-7f * (float)lane, b = 1.0f - 1e-7f * (float)lane;
+  v4f acc[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = v4f{};
+  for (int64_t it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[j], 0, 0, 0);
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s += acc[j][r];
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid < out_n0) KH_PTR(out)[gid] = s;
 }
