@@ -251,7 +251,8 @@ __device__ __forceinline__ void dma_slab(const float *__restrict__ A, const floa
 // asm after it (both memory clobbers) keep every LDS access on its side.
 template <int N>
 __device__ __forceinline__ void vm_barrier() {
-  static_assert(N >= 0 && N < 64, "vmcnt field");
+  // 63 is the field's "do not wait" encoding, so the largest real wait is 62.
+  static_assert(N >= 0 && N < 63, "vmcnt field");
   // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14].
   constexpr int kImm = (N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14);
   asm volatile("" ::: "memory");
@@ -518,6 +519,45 @@ __device__ __forceinline__ void refuse_launch(float *C, int64_t M, int64_t N, in
   for (int64_t i = block * threads + flat; i < M * N; i += stride) C[(i / N) * ldc + i % N] = __builtin_nanf("");
 }
 
+// store_tile for the persistent pipeline (32x32 MFMAs): buffer stores over a
+// resource spanning the tile's rows inside C, so rows past M are dropped by
+// the hardware range check and columns past N go to an offset outside it.
+// Every lane issues exactly WTM x WTN x 16 store instructions, no branches,
+// so a later wait can count them (gemm_tiles_flat waits for the next
+// tile's slab loads while the most recent 63 of these stores stay in
+// flight). Needs BM x ldc x 4 < 2^31.
+template <int WTM, int WTN, class T>
+__device__ __forceinline__ void store_tile_buf(const AccOf<T> (&acc)[WTM][WTN], float *__restrict__ Cp, int64_t M,
+                                               int64_t N, int64_t ldc, int64_t m0, int64_t n0, int wm, int wn,
+                                               int lane) {
+  static_assert(T::kMF == 32, "32x32 accumulator layout");
+  const int64_t rows = (M - m0) < T::BM ? (M - m0) : T::BM;
+  const __amdgpu_buffer_rsrc_t rc =
+      __builtin_amdgcn_make_buffer_rsrc(Cp + m0 * ldc, (short)0, (int)(rows * ldc * 4), kRsrcWord3);
+  const int col = lane & 31, h = lane >> 5;
+  const uint32_t ld4 = (uint32_t)ldc * 4u;
+  // Per lane: one offset per column block (kOutside past N), plus each
+  // store's row displacement. The displacement goes into the vector offset,
+  // not the scalar one: the range check that drops rows past M covers the
+  // vector offset (kOutside + a displacement below 2^31 stays out of range).
+  uint32_t base[WTN];
+#pragma unroll
+  for (int j = 0; j < WTN; ++j) {
+    const int gc = wn * 32 * WTN + j * 32 + col;
+    base[j] = (n0 + gc < N) ? (uint32_t)((wm * 32 * WTM + 4 * h) * ld4 + (uint32_t)(n0 + gc) * 4u) : kOutside;
+  }
+#pragma unroll
+  for (int i = 0; i < WTM; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const uint32_t rowoff = (uint32_t)(i * 32 + 8 * (r >> 2) + (r & 3)) * ld4;
+#pragma unroll
+      for (int j = 0; j < WTN; ++j)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][r]), rc, base[j] + rowoff, 0, 0);
+    }
+  }
+}
+
 // Fast-path pipelines (gemm_body's PIPE).
 constexpr int kPipeRegs = 1;       // register-staged, one slab ahead
 constexpr int kPipeDma = 2;        // direct-to-LDS, three stages
@@ -580,7 +620,7 @@ __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const f
 // One slab of the persistent ring: chunk 0's MFMAs, the barrier (slab q+1
 // has landed and stage fut is free), the fetch of a later slab into stage
 // fut, slab q+1's first fragments, then this slab's remaining chunks.
-template <int WTM, int WTN, class T, bool PRIO, bool ALN>
+template <int WTM, int WTN, class T, bool PRIO, bool ALN, int WAIT = 0>
 __device__ __forceinline__ void flat_step(AccOf<T> (&acc)[WTM][WTN], Frag<WTM, WTN> &f0, Frag<WTM, WTN> &f1, int &cur,
                                           const float *__restrict__ Ap, const float *__restrict__ Bp, int64_t M,
                                           int64_t N, int64_t K, int64_t lda, int64_t ldb, bool dma, int64_t dm0,
@@ -594,7 +634,7 @@ __device__ __forceinline__ void flat_step(AccOf<T> (&acc)[WTM][WTN], Frag<WTM, W
   if (PRIO) __builtin_amdgcn_s_setprio(1);
   mfma_frag<WTM, WTN>(acc, f0);
   if (PRIO) __builtin_amdgcn_s_setprio(0);
-  vm_barrier<0>();
+  vm_barrier<WAIT>();
   if (dma)
     dma_slab<T, ALN>(Ap, Bp, M, N, K, lda, ldb, dm0, dn0, dk0, As + fut * T::A_STAGE, Bs + fut * T::B_STAGE, wv,
                      lane);
@@ -621,6 +661,8 @@ __device__ __forceinline__ void gemm_tiles_flat(const float *__restrict__ Ap, co
                                                 int64_t lda, int64_t ldb, int64_t ldc, float *As, float *Bs) {
   using T = Tile<WTM, WTN, BKT, true, WGM, WGN, MF>;
   constexpr int BK = T::BK;
+  constexpr int kStores = WTM * WTN * 16;  // store_tile_buf's stores per lane
+  constexpr int kStoreSlack = kStores < 62 ? kStores : 62;
   const int tid = threadIdx.x;
   const int lane = kh::lane_id();
   const int wave = tid >> 6;
@@ -676,9 +718,14 @@ __device__ __forceinline__ void gemm_tiles_flat(const float *__restrict__ Ap, co
       // shared copy the kernel measured 0.6% slower at 8192^3 and its L2
       // misses doubled (FETCH_SIZE), with the same instructions in the
       // steady-state loop.
+      // In later tiles the previous tile's C stores (exactly kStores per
+      // lane, issued after slab 1's loads) are still in flight. Vector
+      // memory operations retire in issue order, so waiting until at most
+      // min(kStores, 62) are outstanding completes the loads and lets the
+      // newest stores drain behind this tile's MFMAs.
       if (t > 0)
-        flat_step<WTM, WTN, T, PRIO, ALN>(acc, f0, f1, cur, Ap, Bp, M, N, K, lda, ldb, dma, dm0, dn0, dk0, true, As, Bs,
-                                     wv, wm, wn, lane);
+        flat_step<WTM, WTN, T, PRIO, ALN, kStoreSlack>(acc, f0, f1, cur, Ap, Bp, M, N, K, lda, ldb, dma, dm0, dn0,
+                                                       dk0, true, As, Bs, wv, wm, wn, lane);
       else
         flat_step<WTM, WTN, T, PRIO, ALN>(acc, f0, f1, cur, Ap, Bp, M, N, K, lda, ldb, dma, dm0, dn0, dk0, true, As, Bs,
                                      wv, wm, wn, lane);
@@ -691,7 +738,7 @@ __device__ __forceinline__ void gemm_tiles_flat(const float *__restrict__ Ap, co
     for (int64_t ks = ns > 2 ? ns - 2 : 1; ks < ns; ++ks)
       flat_step<WTM, WTN, T, PRIO, ALN>(acc, f0, f1, cur, Ap, Bp, M, N, K, lda, ldb, has_next, nm0, nn0,
                                       (ks + 2 - ns) * BK, ks + 1 < ns || has_next, As, Bs, wv, wm, wn, lane);
-    store_tile<WTM, WTN, T>(acc, Cp, M, N, ldc, cm0, cn0, wm, wn, lane);
+    store_tile_buf<WTM, WTN, T>(acc, Cp, M, N, ldc, cm0, cn0, wm, wn, lane);
     cm0 = nm0;
     cn0 = nn0;
   }
@@ -752,7 +799,8 @@ __device__ __forceinline__ void gemm_entry_flat(const float *__restrict__ Ap, co
   __shared__ __attribute__((aligned(16))) float Bs[L::B];
   const bool vec = ((K & 3) == 0) && ((lda & 3) == 0) && kh::aligned16(Ap) && ((N & 3) == 0) &&
                    ((ldb & 3) == 0) && kh::aligned16(Bp);
-  const bool fits32 = (int64_t)T::BM * lda * 4 < (1ll << 31) && (int64_t)T::BK * ldb * 4 < (1ll << 31);
+  const bool fits32 = (int64_t)T::BM * lda * 4 < (1ll << 31) && (int64_t)T::BK * ldb * 4 < (1ll << 31) &&
+                      (int64_t)T::BM * ldc * 4 < (1ll << 31);
   const int64_t tiles = ((M + T::BM - 1) / T::BM) * ((N + T::BN - 1) / T::BN);
   if (vec && fits32 && K > T::BK && tiles < (1ll << 31)) {
     // Tail-free slab loads where no slab reaches past K or N: +2-3% at
