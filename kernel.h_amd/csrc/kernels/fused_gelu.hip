@@ -48,33 +48,41 @@ extern "C" __global__ void __launch_bounds__(256)
 fused_gelu(KH_MEMREF1(const float, x), KH_MEMREF1(float, tmp), KH_MEMREF1(float, out)) {
   (void)tmp_alloc;
   (void)tmp_base;
+  const uint32_t gw = kh::group_size_word(), blocks = kh::grid_blocks_x();
+  KH_ARGS_READY(x_base, x_off, out_base, out_off, out_n0, gw, blocks);
   const float *__restrict__ X = KH_PTR(x);
   float *__restrict__ O = KH_PTR(out);
   const int64_t n = out_n0;
+  const int64_t bd = kh::threads_x_of(gw);
+  const int64_t nb = blocks;
   const int64_t tid = threadIdx.x;
-  const int64_t nthreads = (int64_t)blockDim.x * gridDim.x;
+  const int64_t gid = (int64_t)blockIdx.x * bd + tid;
 
   if (kh::aligned16(X) && kh::aligned16(O)) {
-    // Streamed once: nontemporal dwordx4 loads/stores, KH_UNROLL in flight.
+    // Streamed once, nontemporal, KH_UNROLL float4 per thread: the
+    // launcher's grid covers n in one step of the (scalar) loop; smaller
+    // grids take more steps. Each step moves through buffer resources over
+    // exactly the workgroup's float4s inside n, so the ragged end needs no
+    // branches, and its loads go out in two halves, the second once the
+    // first has landed (kh::kFirstBurst).
     const int64_t n4 = n >> 2;
-    const int64_t bd = blockDim.x;
-    const int64_t step = nthreads * KH_UNROLL;
-    int64_t i = (int64_t)blockIdx.x * bd * KH_UNROLL + tid;
-    for (; i + (KH_UNROLL - 1) * bd < n4; i += step) {
+    const int64_t per_step = bd * KH_UNROLL;
+    for (int64_t b0 = (int64_t)blockIdx.x * per_step; b0 < n4; b0 += nb * per_step) {
+      const uint32_t bytes = (uint32_t)((n4 - b0 < per_step ? n4 - b0 : per_step) * 16);
+      const __amdgpu_buffer_rsrc_t rx = kh::span_rsrc(X + 4 * b0, bytes);
+      const __amdgpu_buffer_rsrc_t ro = kh::span_rsrc(O + 4 * b0, bytes);
       float4 v[KH_UNROLL];
 #pragma unroll
-      for (int u = 0; u < KH_UNROLL; ++u) v[u] = kh::load_nt(X + 4 * (i + u * bd));
+      for (int u = 0; u < KH_UNROLL; ++u) {
+        v[u] = kh::buf_load4_nt(rx, (uint32_t)(tid + u * bd) * 16u);
+        if (u + 1 == kh::kFirstBurst && kh::kFirstBurst < KH_UNROLL) kh::vm_wait<0>();
+      }
 #pragma unroll
-      for (int u = 0; u < KH_UNROLL; ++u) kh::store_nt(O + 4 * (i + u * bd), gelu4(v[u]));
+      for (int u = 0; u < KH_UNROLL; ++u) kh::buf_store4_nt(ro, (uint32_t)(tid + u * bd) * 16u, gelu4(v[u]));
     }
-    for (int u = 0; u < KH_UNROLL; ++u) {
-      const int64_t j = i + u * bd;
-      if (j < n4) kh::store_nt(O + 4 * j, gelu4(kh::load_nt(X + 4 * j)));
-    }
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + tid;
     const int64_t t = (n4 << 2) + gid;
     if (t < n) O[t] = gelu_affine(X[t]);
   } else {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + tid; i < n; i += nthreads) O[i] = gelu_affine(X[i]);
+    for (int64_t i = gid; i < n; i += bd * nb) O[i] = gelu_affine(X[i]);
   }
 }

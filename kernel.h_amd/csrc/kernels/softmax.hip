@@ -25,23 +25,30 @@
 
 namespace {
 
+// The row moves through buffer resources spanning exactly its cols floats:
+// columns past the end read 0 (replaced by -inf before the max) and their
+// stores are dropped, so the path has no per-lane branches. For rows of four
+// or more float4 per lane the loads go out in two halves, the second once the
+// first has landed (kh::kFirstBurst).
 template <int V>
 __device__ __forceinline__ void softmax_row_regs(const float *__restrict__ xr, float *__restrict__ yr,
                                                  int64_t cols, int lane) {
+  const __amdgpu_buffer_rsrc_t rx = kh::span_rsrc(xr, (uint32_t)cols * 4u);
+  const __amdgpu_buffer_rsrc_t ry = kh::span_rsrc(yr, (uint32_t)cols * 4u);
+  constexpr int kHalf = V >= 4 ? V / 2 : V;
   float4 v[V];
-  const float ninf = -__builtin_inff();
 #pragma unroll
   for (int j = 0; j < V; ++j) {
-    const int64_t c = (int64_t)(lane + j * kh::kWave) * 4;
-    if (c < cols) {
-      v[j] = kh::load_nt(xr + c);
-    } else {
-      v[j] = make_float4(ninf, ninf, ninf, ninf);
-    }
+    v[j] = kh::buf_load4_nt(rx, (uint32_t)(lane + j * kh::kWave) * 16u);
+    if (j + 1 == kHalf && kHalf < V) kh::vm_wait<0>();
   }
+  const float ninf = -__builtin_inff();
   float m = ninf;
 #pragma unroll
-  for (int j = 0; j < V; ++j) m = fmaxf(m, fmaxf(fmaxf(v[j].x, v[j].y), fmaxf(v[j].z, v[j].w)));
+  for (int j = 0; j < V; ++j) {
+    if ((int64_t)(lane + j * kh::kWave) * 4 >= cols) v[j] = make_float4(ninf, ninf, ninf, ninf);
+    m = fmaxf(m, fmaxf(fmaxf(v[j].x, v[j].y), fmaxf(v[j].z, v[j].w)));
+  }
   m = kh::wave_max(m);
   const float mb = -m * kh::kLog2e;
   float s = 0.0f;
@@ -56,17 +63,9 @@ __device__ __forceinline__ void softmax_row_regs(const float *__restrict__ xr, f
   s = kh::wave_sum(s);
   const float inv = 1.0f / s;
 #pragma unroll
-  for (int j = 0; j < V; ++j) {
-    const int64_t c = (int64_t)(lane + j * kh::kWave) * 4;
-    if (c < cols) {
-      float4 o;
-      o.x = v[j].x * inv;
-      o.y = v[j].y * inv;
-      o.z = v[j].z * inv;
-      o.w = v[j].w * inv;
-      kh::store_nt(yr + c, o);
-    }
-  }
+  for (int j = 0; j < V; ++j)
+    kh::buf_store4_nt(ry, (uint32_t)(lane + j * kh::kWave) * 16u,
+                      make_float4(v[j].x * inv, v[j].y * inv, v[j].z * inv, v[j].w * inv));
 }
 
 // Any cols, any alignment: per-lane online (max, sum) over a strided sweep,
@@ -94,11 +93,11 @@ __device__ __forceinline__ void softmax_row_stream(const float *__restrict__ xr,
 // path, so the narrow symbol stays lean (more rows in flight per CU).
 template <bool WIDE>
 __device__ __forceinline__ void softmax_rows(const float *__restrict__ X, float *__restrict__ Y, int64_t rows,
-                                             int64_t cols, int64_t xs, int64_t ys) {
+                                             int64_t cols, int64_t xs, int64_t ys, int64_t bd, int64_t nb) {
   const int lane = kh::lane_id();
-  const int64_t waves_per_block = blockDim.x / kh::kWave;
-  const int64_t wave = threadIdx.x / kh::kWave;
-  const int64_t nwaves = waves_per_block * gridDim.x;
+  const int64_t waves_per_block = bd / kh::kWave;
+  const int64_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kh::kWave);  // uniform: scalar row loop
+  const int64_t nwaves = waves_per_block * nb;
   const bool vec = ((cols & 3) == 0) && ((xs & 3) == 0) && ((ys & 3) == 0) && kh::aligned16(X) &&
                    kh::aligned16(Y);
   const int64_t v4 = (cols + 255) / 256;  // float4 per lane needed
@@ -127,12 +126,16 @@ __device__ __forceinline__ void softmax_rows(const float *__restrict__ X, float 
 // shape through the streaming path.
 extern "C" __global__ void __launch_bounds__(256)
 softmax(KH_MEMREF2(const float, x), KH_MEMREF2(float, y)) {
-  softmax_rows<false>(KH_PTR(x), KH_PTR(y), x_n0, x_n1, x_s0, y_s0);
+  const uint32_t gw = kh::group_size_word(), nb = kh::grid_blocks_x();
+  KH_ARGS_READY(x_base, x_off, x_n0, x_n1, x_s0, y_base, y_off, y_s0, gw, nb);
+  softmax_rows<false>(KH_PTR(x), KH_PTR(y), x_n0, x_n1, x_s0, y_s0, kh::threads_x_of(gw), nb);
 }
 
 // Same arguments and results; register path for rows of 1025..4096 floats
 // (the launcher picks it for those widths).
 extern "C" __global__ void __launch_bounds__(256)
 softmax_wide(KH_MEMREF2(const float, x), KH_MEMREF2(float, y)) {
-  softmax_rows<true>(KH_PTR(x), KH_PTR(y), x_n0, x_n1, x_s0, y_s0);
+  const uint32_t gw = kh::group_size_word(), nb = kh::grid_blocks_x();
+  KH_ARGS_READY(x_base, x_off, x_n0, x_n1, x_s0, y_base, y_off, y_s0, gw, nb);
+  softmax_rows<true>(KH_PTR(x), KH_PTR(y), x_n0, x_n1, x_s0, y_s0, kh::threads_x_of(gw), nb);
 }
