@@ -97,18 +97,21 @@ static_assert(Tile<2, 2, 32, false, 2, 4, 16>::BM == KH_GEMM_WIDE_BM &&
 // per-tile pipeline (or the generic path).
 extern "C" __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 gemm(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
+  KH_GEMM_ARGS_READY();
   khg::gemm_entry_flat<2, 4, 16, true>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
 }
 
 // Same arguments and results with 128x128 tiles.
 extern "C" __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_mid(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
+  KH_GEMM_ARGS_READY();
   gemm_entry<2, 2, 32, true, false>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
 }
 
 // Same arguments and results with 64x64 tiles.
 extern "C" __global__ void __launch_bounds__(kThreads)
 gemm_small(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
+  KH_GEMM_ARGS_READY();
   gemm_entry<1, 1, 32, false, false>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
 }
 
@@ -122,6 +125,7 @@ gemm_small(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(fl
 // CU the fewer barriers of `gemm_small` still win (1024^3: 73.9 vs 68.1).
 extern "C" __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_small_pf2(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
+  KH_GEMM_ARGS_READY();
   khg::gemm_entry_pipe<2, 2, 32, true, khg::kPipePrefetch2, 2, 2, 16>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1,
                                                                       A_n1, A_s0, B_s0, C_s0);
 }
@@ -135,7 +139,9 @@ gemm_small_pf2(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF
 // refused by writing NaN over C.
 extern "C" __global__ void __launch_bounds__(KH_GEMM_WIDE_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_wide(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
-  if (blockDim.x != KH_GEMM_WIDE_THREADS || blockDim.y != 1 || blockDim.z != 1) {
+  const uint32_t gxy = kh::group_size_word(), gz = kh::group_size_z_word();
+  KH_GEMM_ARGS_READY(gxy, gz);
+  if (kh::threads_x_of(gxy) != KH_GEMM_WIDE_THREADS || kh::threads_y_of(gxy) != 1 || kh::threads_z_of(gz) != 1) {
     khg::refuse_launch(KH_PTR(C), C_n0, C_n1, C_s0);
     return;
   }
@@ -211,9 +217,10 @@ __device__ __forceinline__ void ks_mfma(v16f &acc, const float4 &a, const float 
 template <bool VEC, int NWC, bool DEEP>
 __device__ __forceinline__ void gemm_ksplit_body(const float *__restrict__ A, const float *__restrict__ B,
                                                  float *__restrict__ C, int64_t M, int64_t N, int64_t K,
-                                                 int64_t lda, int64_t ldb, int64_t ldc, float *red) {
-  const int lane = kh::lane_id(), wave = threadIdx.x / kh::kWave;
-  const int nw = NWC > 0 ? NWC : blockDim.x / kh::kWave;  // whole waves; a partial last wave takes no k, no output
+                                                 int64_t lda, int64_t ldb, int64_t ldc, int bd, int64_t nblocks,
+                                                 float *red) {
+  const int lane = kh::lane_id(), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kh::kWave);
+  const int nw = NWC > 0 ? NWC : bd / kh::kWave;  // whole waves; a partial last wave takes no k, no output
   const int r = lane & 31, h = lane >> 5;
   const int64_t tiles_m = (M + kKsTile - 1) / kKsTile, tiles_n = (N + kKsTile - 1) / kKsTile;
   const int64_t total = tiles_m * tiles_n;
@@ -221,7 +228,7 @@ __device__ __forceinline__ void gemm_ksplit_body(const float *__restrict__ A, co
   const int64_t kc = DEEP ? 32 * ((K + 32 * nw - 1) / (32 * nw)) : 8 * ((K + 8 * nw - 1) / (8 * nw));
   const int64_t kb = wave * kc, ke = kb + kc < K ? kb + kc : K;
   const int64_t groups = ke > kb ? (ke - kb + 7) / 8 : 0;
-  for (int64_t t = blockIdx.x; t < total; t += gridDim.x) {
+  for (int64_t t = blockIdx.x; t < total; t += nblocks) {
     const int64_t m0 = (t / tiles_n) * kKsTile, n0 = (t % tiles_n) * kKsTile;
     const bool arow_ok = m0 + r < M, bcol_ok = n0 + r < N;
     const int64_t arow = arow_ok ? m0 + r : M - 1, bcol = bcol_ok ? n0 + r : N - 1;
@@ -307,25 +314,35 @@ __device__ __forceinline__ void gemm_ksplit_body(const float *__restrict__ A, co
 
 template <bool DEEP>
 __device__ __forceinline__ void gemm_ksplit_entry(const float *Ap, const float *Bp, float *Cp, int64_t M, int64_t N,
-                                                  int64_t K, int64_t lda, int64_t ldb, int64_t ldc, float *red) {
+                                                  int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int bd,
+                                                  int64_t nb, float *red) {
   const bool vec = ((K & 3) == 0) && ((lda & 3) == 0) && kh::aligned16(Ap);
-  if (blockDim.x == KH_GEMM_KSPLIT_THREADS) {
+  if (bd == KH_GEMM_KSPLIT_THREADS) {
     if (vec) {
-      gemm_ksplit_body<true, kKsMaxWaves, DEEP>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, red);
+      gemm_ksplit_body<true, kKsMaxWaves, DEEP>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, bd, nb, red);
     } else {
-      gemm_ksplit_body<false, kKsMaxWaves, DEEP>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, red);
+      gemm_ksplit_body<false, kKsMaxWaves, DEEP>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, bd, nb, red);
     }
   } else if (vec) {
-    gemm_ksplit_body<true, 0, DEEP>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, red);
+    gemm_ksplit_body<true, 0, DEEP>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, bd, nb, red);
   } else {
-    gemm_ksplit_body<false, 0, DEEP>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, red);
+    gemm_ksplit_body<false, 0, DEEP>(Ap, Bp, Cp, M, N, K, lda, ldb, ldc, bd, nb, red);
   }
 }
+
+// The arguments the K-split kernels use, loaded in one round (KH_ARGS_READY):
+// at 512^3 the launch is ~10 us, and every serial round trip to
+// kernel-argument memory before the first operand load is part of it.
+#define KH_KSPLIT_ENTRY(DEEP)                                                                                  \
+  const uint32_t gw = kh::group_size_word(), nb = kh::grid_blocks_x();                                       \
+  KH_ARGS_READY(A_base, A_off, A_n0, A_n1, A_s0, B_base, B_off, B_n1, B_s0, C_base, C_off, C_s0, gw, nb);    \
+  gemm_ksplit_entry<DEEP>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0,                \
+                          (int)kh::threads_x_of(gw), nb, red)
 
 extern "C" __global__ void __launch_bounds__(KH_GEMM_KSPLIT_THREADS)
 gemm_ksplit(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
   __shared__ float red[kKsMaxWaves * 16 * 64];
-  gemm_ksplit_entry<false>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0, red);
+  KH_KSPLIT_ENTRY(false);
 }
 
 // Same tiles and split with the deep-chunk path compiled in: the launcher
@@ -337,5 +354,5 @@ gemm_ksplit(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(f
 extern "C" __global__ void __launch_bounds__(KH_GEMM_KSPLIT_THREADS)
 gemm_ksplit_deep(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
   __shared__ float red[kKsMaxWaves * 16 * 64];
-  gemm_ksplit_entry<true>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0, red);
+  KH_KSPLIT_ENTRY(true);
 }

@@ -508,14 +508,24 @@ __device__ __forceinline__ void store_tile(const AccOf<T> (&acc)[WTM][WTN], floa
   }
 }
 
+// Every kernel argument a GEMM entry uses, with the launch's block counts,
+// loaded in one round before anything else (KH_ARGS_READY): the tile loops
+// read the same words again, and those loads fold into these.
+#define KH_GEMM_ARGS_READY(...)                                                                               \
+  KH_ARGS_READY(A_base, A_off, A_n0, A_n1, A_s0, B_base, B_off, B_n1, B_s0, C_base, C_off, C_n0, C_n1, C_s0,  \
+                kh::grid_blocks_x(), kh::grid_blocks_y(), kh::grid_blocks_z(), ##__VA_ARGS__)
+
 // Writes NaN over C (grid-strided over the whole launch): how a kernel whose
 // tile split assumes one workgroup size refuses a launch with another,
 // instead of computing part of each tile.
 __device__ __forceinline__ void refuse_launch(float *C, int64_t M, int64_t N, int64_t ldc) {
-  const int64_t threads = (int64_t)blockDim.x * blockDim.y * blockDim.z;
-  const int64_t flat = ((int64_t)threadIdx.z * blockDim.y + threadIdx.y) * blockDim.x + threadIdx.x;
-  const int64_t block = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
-  const int64_t stride = (int64_t)gridDim.x * gridDim.y * gridDim.z * threads;
+  const uint32_t gxy = kh::group_size_word();
+  const int64_t tx = kh::threads_x_of(gxy), ty = kh::threads_y_of(gxy), tz = kh::threads_z_of(kh::group_size_z_word());
+  const int64_t gx = kh::grid_blocks_x(), gy = kh::grid_blocks_y(), gz = kh::grid_blocks_z();
+  const int64_t threads = tx * ty * tz;
+  const int64_t flat = ((int64_t)threadIdx.z * ty + threadIdx.y) * tx + threadIdx.x;
+  const int64_t block = ((int64_t)blockIdx.z * gy + blockIdx.y) * gx + blockIdx.x;
+  const int64_t stride = gx * gy * gz * threads;
   for (int64_t i = block * threads + flat; i < M * N; i += stride) C[(i / N) * ldc + i % N] = __builtin_nanf("");
 }
 
@@ -580,8 +590,9 @@ __device__ __forceinline__ void gemm_tiles(const float *__restrict__ Ap, const f
   const int64_t tiles_m = (M + T::BM - 1) / T::BM, tiles_n = (N + T::BN - 1) / T::BN;
   const int64_t total = tiles_m * tiles_n;
   const int64_t nslabs = (K + T::BK - 1) / T::BK;
-  const int64_t nblocks = (int64_t)gridDim.x * gridDim.y * gridDim.z;
-  const int64_t bid = blockIdx.x + (int64_t)gridDim.x * (blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
+  const int64_t gx = kh::grid_blocks_x(), gy = kh::grid_blocks_y(), gz = kh::grid_blocks_z();
+  const int64_t nblocks = gx * gy * gz;
+  const int64_t bid = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
   const bool xcd_remap = (nblocks == total) && ((total & 7) == 0);
 
   for (int64_t pid = bid; pid < total; pid += nblocks) {
@@ -672,8 +683,9 @@ __device__ __forceinline__ void gemm_tiles_flat(const float *__restrict__ Ap, co
   const int64_t tiles_m = (M + T::BM - 1) / T::BM, tiles_n = (N + T::BN - 1) / T::BN;
   const int64_t total = tiles_m * tiles_n;
   const int64_t ns = (K + BK - 1) / BK;
-  const int64_t nblocks = (int64_t)gridDim.x * gridDim.y * gridDim.z;
-  const int64_t bid = blockIdx.x + (int64_t)gridDim.x * (blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
+  const int64_t gx = kh::grid_blocks_x(), gy = kh::grid_blocks_y(), gz = kh::grid_blocks_z();
+  const int64_t nblocks = gx * gy * gz;
+  const int64_t bid = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
   if (bid >= total) return;
   const bool xcd_remap = ((total & 7) == 0) && ((nblocks & 7) == 0);
   const int64_t mine = (total - bid + nblocks - 1) / nblocks;  // tiles of this workgroup

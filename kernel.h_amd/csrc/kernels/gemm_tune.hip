@@ -18,7 +18,9 @@
 #define KH_GEMM_TUNE_KERNEL(PART, MF, WGM, WGN, WTM, WTN, BK, PRIO, PIPE, SYM)                               \
   extern "C" __global__ void __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(2)))         \
   SYM(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {                        \
-    if (blockDim.x != 64 * WGM * WGN || blockDim.y != 1 || blockDim.z != 1) {                                \
+    const uint32_t gxy = kh::group_size_word(), gz = kh::group_size_z_word();                                \
+    KH_GEMM_ARGS_READY(gxy, gz);                                                                               \
+    if (kh::threads_x_of(gxy) != 64 * WGM * WGN || kh::threads_y_of(gxy) != 1 || kh::threads_z_of(gz) != 1) { \
       khg::refuse_launch(KH_PTR(C), C_n0, C_n1, C_s0);                                                              \
       return;                                                                                                  \
     }                                                                                                          \

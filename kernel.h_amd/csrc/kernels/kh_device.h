@@ -50,11 +50,17 @@ __device__ __forceinline__ uint32_t implicit_arg_u32(int index) {
       (const uint32_t __attribute__((address_space(4))) *)__builtin_amdgcn_implicitarg_ptr();
   return p[index];
 }
-// Raw words: the block count, and the word whose low 16 bits are the
-// workgroup size (threads_x_of).
+// Raw words: the block counts, the word holding the workgroup's x and y
+// sizes (16 bits each: threads_x_of, threads_y_of) and the one whose low 16
+// bits are its z size (threads_z_of).
 __device__ __forceinline__ uint32_t grid_blocks_x() { return implicit_arg_u32(0); }
+__device__ __forceinline__ uint32_t grid_blocks_y() { return implicit_arg_u32(1); }
+__device__ __forceinline__ uint32_t grid_blocks_z() { return implicit_arg_u32(2); }
 __device__ __forceinline__ uint32_t group_size_word() { return implicit_arg_u32(3); }
+__device__ __forceinline__ uint32_t group_size_z_word() { return implicit_arg_u32(4); }
 __device__ __forceinline__ uint32_t threads_x_of(uint32_t word) { return word & 0xffffu; }
+__device__ __forceinline__ uint32_t threads_y_of(uint32_t word) { return word >> 16; }
+__device__ __forceinline__ uint32_t threads_z_of(uint32_t word) { return word & 0xffffu; }
 __device__ __forceinline__ uint32_t block_threads_x() { return threads_x_of(group_size_word()); }
 
 }  // namespace kh
@@ -86,10 +92,17 @@ __device__ __forceinline__ uint32_t block_threads_x() { return threads_x_of(grou
 #define KH_FE_14(M, a, ...) M(a), KH_FE_13(M, __VA_ARGS__)
 #define KH_FE_15(M, a, ...) M(a), KH_FE_14(M, __VA_ARGS__)
 #define KH_FE_16(M, a, ...) M(a), KH_FE_15(M, __VA_ARGS__)
-#define KH_FE_PICK(_1, _2, _3, _4, _5, _6, _7, _8, _9, _10, _11, _12, _13, _14, _15, _16, NAME, ...) NAME
+#define KH_FE_17(M, a, ...) M(a), KH_FE_16(M, __VA_ARGS__)
+#define KH_FE_18(M, a, ...) M(a), KH_FE_17(M, __VA_ARGS__)
+#define KH_FE_19(M, a, ...) M(a), KH_FE_18(M, __VA_ARGS__)
+#define KH_FE_20(M, a, ...) M(a), KH_FE_19(M, __VA_ARGS__)
+#define KH_FE_PICK(_1, _2, _3, _4, _5, _6, _7, _8, _9, _10, _11, _12, _13, _14, _15, _16, _17, _18, _19, _20, NAME, \
+                   ...)                                                                                        \
+  NAME
 #define KH_FOR_EACH(M, ...)                                                                                    \
-  KH_FE_PICK(__VA_ARGS__, KH_FE_16, KH_FE_15, KH_FE_14, KH_FE_13, KH_FE_12, KH_FE_11, KH_FE_10, KH_FE_9,       \
-             KH_FE_8, KH_FE_7, KH_FE_6, KH_FE_5, KH_FE_4, KH_FE_3, KH_FE_2, KH_FE_1)(M, __VA_ARGS__)
+  KH_FE_PICK(__VA_ARGS__, KH_FE_20, KH_FE_19, KH_FE_18, KH_FE_17, KH_FE_16, KH_FE_15, KH_FE_14, KH_FE_13,      \
+             KH_FE_12, KH_FE_11, KH_FE_10, KH_FE_9, KH_FE_8, KH_FE_7, KH_FE_6, KH_FE_5, KH_FE_4, KH_FE_3,       \
+             KH_FE_2, KH_FE_1)(M, __VA_ARGS__)
 #define KH_ARGS_READY(...) asm volatile("" ::KH_FOR_EACH(KH_S_OP, __VA_ARGS__))
 
 namespace kh {
