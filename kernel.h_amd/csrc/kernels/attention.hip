@@ -64,8 +64,8 @@ constexpr float kNegBig = -1e30f;  // finite "minus infinity" seed for m
 // Any workgroup size: synchronous strided staging of one tile.
 __device__ __forceinline__ void stage_kv_generic(float *__restrict__ Ks, float *__restrict__ Vt,
                                                  const float *__restrict__ Kg, const float *__restrict__ Vg,
-                                                 int64_t ks, int64_t vs, int64_t key0, int64_t seq) {
-  for (int e = threadIdx.x; e < TK * D; e += blockDim.x) {
+                                                 int64_t ks, int64_t vs, int64_t key0, int64_t seq, int bd) {
+  for (int e = threadIdx.x; e < TK * D; e += bd) {
     const int key = e / D, d = e % D;
     const int64_t kk = key0 + key;
     Ks[key * LDK + d] = kk < seq ? Kg[kk * ks + d] : 0.0f;
@@ -190,12 +190,12 @@ __device__ __forceinline__ void store_v(const float4 (&v)[4], float *__restrict_
 template <bool VEC4>
 __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, const float *__restrict__ Kg,
                                                 const float *__restrict__ Vg, float *__restrict__ Og, int64_t qs,
-                                                int64_t ks, int64_t vs, int64_t os, int64_t seq, float *Ks,
-                                                float *Vt) {
+                                                int64_t ks, int64_t vs, int64_t os, int64_t seq, int bd,
+                                                int64_t nblocks, float *Ks, float *Vt) {
   const int tid = threadIdx.x;
   const int lane = kh::lane_id();
   const int wave = tid / kh::kWave;
-  const int nwaves = blockDim.x / kh::kWave;
+  const int nwaves = bd / kh::kWave;
   const int r = lane & 31, h = lane >> 5;
   const int64_t rows_per_block = (int64_t)QW * nwaves;
   const int64_t nqt = (seq + rows_per_block - 1) / rows_per_block;
@@ -203,12 +203,12 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
   // The fast path's buffer loads address the slices with 32-bit offsets and
   // bound K by seq rows of ks floats and V by seq rows of vs floats, so every
   // row must hold its D floats.
-  const bool fast = VEC4 && blockDim.x == kFastThreads && ks >= D && vs >= D &&
+  const bool fast = VEC4 && bd == kFastThreads && ks >= D && vs >= D &&
                     (seq + 2 * TK) * (ks > vs ? ks : vs) * 4 < (1ll << 31);
   // log2(e)/sqrt(d): S^T comes out in log2 units, so exp(S - m) = 2^(S' - m').
   const float qscale = kh::kLog2e * 0.125f;
 
-  for (int64_t qt = blockIdx.x; qt < nqt; qt += gridDim.x) {
+  for (int64_t qt = blockIdx.x; qt < nqt; qt += nblocks) {
     const int64_t q_row = qt * rows_per_block + (int64_t)wave * QW + r;
     float4 q[8];
 #pragma unroll
@@ -270,7 +270,7 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
       softmax_pv<true>(o, m, l, sa, Vt + (t & 1) * D * LDV, t * TK, seq, lane);
     } else {
       for (int64_t t = 0; t < ntiles; ++t) {
-        stage_kv_generic(Ks, Vt, Kg, Vg, ks, vs, t * TK, seq);
+        stage_kv_generic(Ks, Vt, Kg, Vg, ks, vs, t * TK, seq, bd);
         __syncthreads();
         v16f sg[2];
         qk_tile(sg, q, Ks, lane);
@@ -320,17 +320,26 @@ attention(KH_MEMREF4(const float, Q), KH_MEMREF4(const float, K), KH_MEMREF4(con
   // four [batch, heads, seq, 64] tensors with contiguous head_dim rows.
   // Anything else is refused by filling O (as its descriptor describes it)
   // with NaN, never by computing from memory the descriptors do not cover.
-  const bool same = K_n0 == Q_n0 && V_n0 == Q_n0 && O_n0 == Q_n0 && K_n1 == heads && V_n1 == heads &&
-                    O_n1 == heads && K_n2 == seq && V_n2 == seq && O_n2 == seq;
-  const bool d64 = Q_n3 == D && K_n3 == D && V_n3 == D && O_n3 == D;
-  const bool rows = (Q_s3 == 1 || Q_n3 <= 1) && (K_s3 == 1 || K_n3 <= 1) && (V_s3 == 1 || V_n3 <= 1) &&
-                    (O_s3 == 1 || O_n3 <= 1);
-  if (!(same && d64 && rows)) {
+  // Evaluated without short-circuit branches (& and |, not && and ||): the
+  // compiler then issues every descriptor load in one round at the start
+  // instead of one round per branch.
+  const bool same = (K_n0 == Q_n0) & (V_n0 == Q_n0) & (O_n0 == Q_n0) & (K_n1 == heads) & (V_n1 == heads) &
+                    (O_n1 == heads) & (K_n2 == seq) & (V_n2 == seq) & (O_n2 == seq);
+  const bool d64 = (Q_n3 == D) & (K_n3 == D) & (V_n3 == D) & (O_n3 == D);
+  const bool rows = ((Q_s3 == 1) | (Q_n3 <= 1)) & ((K_s3 == 1) | (K_n3 <= 1)) & ((V_s3 == 1) | (V_n3 <= 1)) &
+                    ((O_s3 == 1) | (O_n3 <= 1));
+  const int ok = same & d64 & rows;
+  // The check's loads, the base pointers and the launch geometry in one round.
+  const uint32_t gxy = kh::group_size_word(), bcx = kh::grid_blocks_x();
+  KH_ARGS_READY(ok, Q_base, Q_off, K_base, K_off, V_base, V_off, O_base, O_off, gxy, bcx);
+  if (!ok) {
     const int64_t total = O_n0 * O_n1 * O_n2 * O_n3;
-    const int64_t threads = (int64_t)blockDim.x * blockDim.y * blockDim.z;
-    const int64_t flat = ((int64_t)threadIdx.z * blockDim.y + threadIdx.y) * blockDim.x + threadIdx.x;
-    const int64_t block = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
-    const int64_t step = threads * gridDim.x * gridDim.y * gridDim.z;
+    const int64_t tx = kh::threads_x_of(gxy), ty = kh::threads_y_of(gxy), tz = kh::threads_z_of(kh::group_size_z_word());
+    const int64_t gy = kh::grid_blocks_y(), gz = kh::grid_blocks_z();
+    const int64_t threads = tx * ty * tz;
+    const int64_t flat = ((int64_t)threadIdx.z * ty + threadIdx.y) * tx + threadIdx.x;
+    const int64_t block = ((int64_t)blockIdx.z * gy + blockIdx.y) * bcx + blockIdx.x;
+    const int64_t step = threads * bcx * gy * gz;
     for (int64_t e = block * threads + flat; e < total; e += step) {
       int64_t r = e;
       const int64_t i3 = r % O_n3;
@@ -355,10 +364,10 @@ attention(KH_MEMREF4(const float, Q), KH_MEMREF4(const float, K), KH_MEMREF4(con
   __shared__ __attribute__((aligned(16))) float Vt[2 * D * LDV];
 
   // float4 access to Q, K, V and O needs 16-byte aligned rows.
-  const bool vec4 = kh::aligned16(Qp) && kh::aligned16(Kp) && kh::aligned16(Vp) && kh::aligned16(Op) &&
-                    ((Q_s0 | Q_s1 | Q_s2 | K_s0 | K_s1 | K_s2 | V_s0 | V_s1 | V_s2 | O_s0 | O_s1 | O_s2) & 3) == 0;
+  const bool vec4 = kh::aligned16(Qp) & kh::aligned16(Kp) & kh::aligned16(Vp) & kh::aligned16(Op) &
+                    (((Q_s0 | Q_s1 | Q_s2 | K_s0 | K_s1 | K_s2 | V_s0 | V_s1 | V_s2 | O_s0 | O_s1 | O_s2) & 3) == 0);
   if (vec4)
-    attention_slice<true>(Qg, Kg, Vg, Og, Q_s2, K_s2, V_s2, O_s2, seq, Ks, Vt);
+    attention_slice<true>(Qg, Kg, Vg, Og, Q_s2, K_s2, V_s2, O_s2, seq, (int)kh::threads_x_of(gxy), bcx, Ks, Vt);
   else
-    attention_slice<false>(Qg, Kg, Vg, Og, Q_s2, K_s2, V_s2, O_s2, seq, Ks, Vt);
+    attention_slice<false>(Qg, Kg, Vg, Og, Q_s2, K_s2, V_s2, O_s2, seq, (int)kh::threads_x_of(gxy), bcx, Ks, Vt);
 }

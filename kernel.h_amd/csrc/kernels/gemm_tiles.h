@@ -73,7 +73,7 @@ struct Tile {
   static constexpr int SWZ_SHIFT = QP == 2 ? 2 : QP == 4 ? 1 : 0;
   static_assert(NA * NT * 4 == BM * BK && NB * NT * 4 == BK * BN,
                 "a slab must split into whole float4s over the workgroup's threads");
-  static_assert(BK % Mfma<MF>::CK == 0 && QP <= 8, "slabs are consumed in whole chunks");
+  static_assert(BK % Mfma<MF>::CK == 0 && (!DMA || QP <= 8), "slabs are consumed in whole chunks");
   static_assert(BROW <= 64 || BROW % 64 == 0, "a wave's B load covers whole rows");
   static_assert(BK % RPI == 0, "B row groups split the slab");
   __device__ static constexpr int aswz(int row) { return DMA ? ((row >> SWZ_SHIFT) ^ (row >> 3)) & (QP - 1) : 0; }
