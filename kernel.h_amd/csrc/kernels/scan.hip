@@ -236,7 +236,7 @@ struct Opened {
   bool ok;
 };
 
-__device__ __forceinline__ Opened open_session(Header *h, Counters *c, int64_t ntiles) {
+__device__ __forceinline__ Opened open_session(Header *h, Counters *c, int64_t ntiles, uint64_t nblocks) {
   Opened o;
   o.ok = true;
   o.base = ld(&h->base);
@@ -248,7 +248,7 @@ __device__ __forceinline__ Opened open_session(Header *h, Counters *c, int64_t n
   // workgroup, all >= base: a ticket outside that range means the counter
   // was changed behind the header's back (another kernel wrote it), and the
   // header is not taken as valid even though its check matches.
-  const uint64_t span = (uint64_t)ntiles + 2ull * gridDim.x * gridDim.y * gridDim.z + 4;
+  const uint64_t span = (uint64_t)ntiles + 2ull * nblocks + 4;
   const bool signed0 = seen0 == header_check(h, o.base, o.nonce);
   const bool in_range = (uint32_t)(o.t1 - first_ticket(o.base)) < span;
   // Valid: the header is stable for the whole call (only the last workgroup
@@ -318,9 +318,8 @@ __device__ __forceinline__ uint64_t count_done(Counters *c, uint32_t tickets) {
 // plus all the tickets of this call (the counter's value), its generation
 // one more.
 __device__ __forceinline__ void close_session(Header *h, Counters *c, uint64_t base, uint64_t nonce,
-                                              uint64_t done_before,
-                                              uint32_t tickets) {
-  if ((uint32_t)done_before != gridDim.x * gridDim.y * gridDim.z - 1) return;
+                                              uint64_t done_before, uint32_t tickets, uint32_t nblocks) {
+  if ((uint32_t)done_before != nblocks - 1) return;
   const uint32_t next_ticket = first_ticket(base) + (uint32_t)(done_before >> 32) + tickets;
   const uint64_t next = ((base & 0xffffffff00000000ull) + (1ull << 32)) | next_ticket;
   st(&c->counter, next_ticket);  // already its value, unless something else wrote it
@@ -555,11 +554,11 @@ template <bool VEC>
 __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *__restrict__ Y, const Session &ses,
                                            int64_t n, int64_t tr, int64_t tn, bool single, uint64_t *s_raw,
                                            double *s_wave_total, double *s_prefix, double *s_off,
-                                           uint64_t *s_done) {
+                                           uint64_t *s_done, int bd) {
   const int tid = threadIdx.x;
   const int lane = kh::lane_id();
   const int wave = tid / kh::kWave;
-  const int ndata = blockDim.x / kh::kWave - 1;
+  const int ndata = bd / kh::kWave - 1;
   const bool ctrl = wave == ndata;
   const int64_t tile_elems = (int64_t)ndata * kh::kWave * kPerThread;
   const int64_t ntiles = (n + tile_elems - 1) / tile_elems;
@@ -732,13 +731,20 @@ scan(KH_MEMREF1(const float, x), KH_MEMREF1(float, y), KH_MEMREF1(float, y_lo),
   __shared__ double s_prefix;
 
   if (n <= 0) return;
+  // Every argument and the launch geometry in one round of scalar loads.
+  const uint32_t gxy = kh::group_size_word(), gzw = kh::group_size_z_word();
+  const uint32_t bx = kh::grid_blocks_x(), by = kh::grid_blocks_y(), bz = kh::grid_blocks_z();
+  KH_ARGS_READY(x_base, x_off, y_base, y_off, totals_hi_base, totals_hi_off, totals_hi_n0, totals_hi_s0,
+                totals_lo_base, totals_lo_off, totals_lo_n0, totals_lo_s0, gxy, gzw, bx, by, bz);
+  const uint32_t nblocks = bx * by * bz;
   // Refusals, decided identically by every workgroup before any state is
   // touched: the launch shape the tile loop assumes (one-dimensional
   // workgroups of whole waves, at least three data waves) and room for the
   // header and the records. y := NaN, never a hang or a stray write.
-  const bool shape_ok = blockDim.x >= kMinThreads && blockDim.x % kh::kWave == 0 && blockDim.y == 1 &&
-                        blockDim.z == 1;
-  const int64_t tile_elems = (int64_t)((int)blockDim.x - kh::kWave) * kPerThread;
+  const int bdx = (int)kh::threads_x_of(gxy);
+  const bool shape_ok = (bdx >= kMinThreads) & (bdx % kh::kWave == 0) & (kh::threads_y_of(gxy) == 1) &
+                        (kh::threads_z_of(gzw) == 1);
+  const int64_t tile_elems = (int64_t)(bdx - kh::kWave) * kPerThread;
   const int64_t ntiles = shape_ok ? (n + tile_elems - 1) / tile_elems : 0;
   const int64_t lo_bytes = bytes_from_align8(KH_PTR(totals_lo), totals_lo_n0, totals_lo_s0);
   // (Tickets and tile indices are 32-bit: ntiles < 2^31 always holds for a
@@ -755,7 +761,7 @@ scan(KH_MEMREF1(const float, x), KH_MEMREF1(float, y), KH_MEMREF1(float, y_lo),
   Opened o{0, 0, 0, 0, true};
   if (!refuse && !single) {
     if (tid == 0) {
-      o = open_session(ses.h, ses.c, ntiles);
+      o = open_session(ses.h, ses.c, ntiles, nblocks);
       s_session[0] = o.base;
       s_session[1] = session_key(ses.h, o.nonce);
       s_ticket[0] = tile_of(o.t0, o.base, ntiles);
@@ -766,10 +772,11 @@ scan(KH_MEMREF1(const float, x), KH_MEMREF1(float, y), KH_MEMREF1(float, y_lo),
     refuse = s_refuse;
   }
   if (refuse) {
-    const int64_t threads = (int64_t)blockDim.x * blockDim.y * blockDim.z;
-    const int64_t flat = ((int64_t)threadIdx.z * blockDim.y + threadIdx.y) * blockDim.x + tid;
-    const int64_t block = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
-    const int64_t blocks = (int64_t)gridDim.x * gridDim.y * gridDim.z;
+    const int64_t ty = kh::threads_y_of(gxy), tz = kh::threads_z_of(gzw);
+    const int64_t threads = (int64_t)bdx * ty * tz;
+    const int64_t flat = ((int64_t)threadIdx.z * ty + threadIdx.y) * bdx + tid;
+    const int64_t block = ((int64_t)blockIdx.z * by + blockIdx.y) * bx + blockIdx.x;
+    const int64_t blocks = nblocks;
     for (int64_t i = block * threads + flat; i < n; i += blocks * threads) Y[i] = __builtin_nanf("");
     return;
   }
@@ -787,17 +794,18 @@ scan(KH_MEMREF1(const float, x), KH_MEMREF1(float, y), KH_MEMREF1(float, y_lo),
   ses.keys = record_keys(s_session[1]);
   if (first >= ntiles) {
     // No tile for this workgroup: both its tickets are past the end.
-    if (tid == 0) close_session(ses.h, ses.c, ses.base, o.nonce, count_done(ses.c, 2), 2);
+    if (tid == 0) close_session(ses.h, ses.c, ses.base, o.nonce, count_done(ses.c, 2), 2, nblocks);
     return;
   }
   __shared__ uint64_t s_done[2];
   if (kh::aligned16(X) && kh::aligned16(Y) && (n & 3) == 0)
-    scan_tiles<true>(X, Y, ses, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off, s_done);
+    scan_tiles<true>(X, Y, ses, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off, s_done, bdx);
   else
-    scan_tiles<false>(X, Y, ses, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off, s_done);
+    scan_tiles<false>(X, Y, ses, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off, s_done, bdx);
   // s_done was written before the last barrier B; the nonce is in thread 0's
   // registers.
-  if (!single && tid == 0) close_session(ses.h, ses.c, ses.base, o.nonce, s_done[0], (uint32_t)s_done[1]);
+  if (!single && tid == 0)
+    close_session(ses.h, ses.c, ses.base, o.nonce, s_done[0], (uint32_t)s_done[1], nblocks);
 }
 
 // The reference's second pass (scan.cpp:350-453). With the single-pass
