@@ -17,6 +17,8 @@
 // gives exactly 0, so the formula is finite for every finite input. The
 // absolute error of out is a few fp32 ulps of |t|, far inside the 1e-4
 // fp64-reference tolerance (e2e_fused_gelu_test.cpp:63).
+#include <type_traits>
+
 #include "kh_device.h"
 #include "kh_tiles.h"
 
@@ -63,11 +65,13 @@ fused_gelu(KH_MEMREF1(const float, x), KH_MEMREF1(float, tmp), KH_MEMREF1(float,
     // launcher's grid covers n in one step of the (scalar) loop; smaller
     // grids take more steps. Each step moves through buffer resources over
     // exactly the workgroup's float4s inside n, so the ragged end needs no
-    // branches, and its loads go out in two halves, the second once the
-    // first has landed (kh::kFirstBurst).
+    // branches. In a launch that fits one round, the first step's loads go
+    // out in two halves, the second once the first has landed, and its
+    // stores once all have (kh::kFirstBurst).
     const int64_t n4 = n >> 2;
     const int64_t per_step = bd * KH_UNROLL;
-    for (int64_t b0 = (int64_t)blockIdx.x * per_step; b0 < n4; b0 += nb * per_step) {
+    auto step = [&](auto split_tag, int64_t b0) __attribute__((always_inline)) {
+      constexpr bool kSplit = decltype(split_tag)::value;
       const uint32_t bytes = (uint32_t)((n4 - b0 < per_step ? n4 - b0 : per_step) * 16);
       const __amdgpu_buffer_rsrc_t rx = kh::span_rsrc(X + 4 * b0, bytes);
       const __amdgpu_buffer_rsrc_t ro = kh::span_rsrc(O + 4 * b0, bytes);
@@ -75,11 +79,20 @@ fused_gelu(KH_MEMREF1(const float, x), KH_MEMREF1(float, tmp), KH_MEMREF1(float,
 #pragma unroll
       for (int u = 0; u < KH_UNROLL; ++u) {
         v[u] = kh::buf_load4_nt(rx, (uint32_t)(tid + u * bd) * 16u);
-        if (u + 1 == kh::kFirstBurst && kh::kFirstBurst < KH_UNROLL) kh::vm_wait<0>();
+        if (kSplit && u + 1 == kh::kFirstBurst) kh::vm_wait<0>();
       }
+      if (kSplit) kh::vm_wait<0>();
 #pragma unroll
       for (int u = 0; u < KH_UNROLL; ++u) kh::buf_store4_nt(ro, (uint32_t)(tid + u * bd) * 16u, gelu4(v[u]));
+    };
+    int64_t b0 = (int64_t)blockIdx.x * per_step;
+    if (b0 < n4) {
+      if (kh::split_first_burst(bd * nb))
+        step(std::true_type{}, b0);
+      else
+        step(std::false_type{}, b0);
     }
+    for (b0 += nb * per_step; b0 < n4; b0 += nb * per_step) step(std::false_type{}, b0);
     const int64_t t = (n4 << 2) + gid;
     if (t < n) O[t] = gelu_affine(X[t]);
   } else {

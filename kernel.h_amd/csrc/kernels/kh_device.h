@@ -185,8 +185,17 @@ __device__ __forceinline__ void vm_wait() {
 // launch, MI355X): issuing each wave's loads in two halves, the second once
 // the first has landed, ran 6.05-6.13 us against 6.9-7.1 us with all four
 // in flight at once and 6.7-6.9 us one at a time (copy and softmax alike,
-// same bits). The smaller first burst over the whole chip is what helps.
+// same bits). The smaller first burst over the whole chip is what helps, so
+// the split applies to the first step of launches that fit one round of the
+// chip (256 CUs x 2048 resident threads): in longer launches every wave
+// keeping all its loads in flight moves more bytes, and in a later step of a
+// loop the wait would also hold for the previous step's stores (vector
+// memory operations retire in issue order).
 constexpr int kFirstBurst = 2;
+constexpr int64_t kFirstBurstMaxThreads = 256 * 2048;
+__device__ __forceinline__ bool split_first_burst(int64_t launch_threads) {
+  return launch_threads <= kFirstBurstMaxThreads;
+}
 
 // 2^x on the hardware transcendental unit (v_exp_f32).
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }

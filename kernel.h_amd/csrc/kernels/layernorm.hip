@@ -16,6 +16,8 @@
 // cache for the variance and the output). Rows are grid-strided over
 // wavefronts; any block that is a multiple of 64 threads is correct,
 // including the reference's rows x 256 geometry (kernelh_backend.cpp:290).
+#include <type_traits>
+
 #include "kh_device.h"
 
 #ifndef KH_LN_MAXV
@@ -43,9 +45,10 @@ constexpr int kStageCols = 1024;
 // re-read took 8.0-8.4 us.
 // Rows move through buffer resources spanning exactly cols floats: columns
 // past the end read 0 (kept out of the variance by a select) and their
-// stores are dropped, so the path has no per-lane branches. For rows of four
-// or more float4 per lane the loads go out in two halves, the second once the
-// first has landed (kh::kFirstBurst). Without STAGED, gamma and beta are read
+// stores are dropped, so the path has no per-lane branches. For a wave's first
+// staged row, in a launch that fits one round, and four or more float4 per
+// lane, the loads go out in two halves, the second once the first has landed
+// (kh::kFirstBurst). Without STAGED, gamma and beta are read
 // the same way; with it, from LDS (a lane past cols reads a staged slot it
 // does not use: every path that stages has 4 V float4 <= kStageCols).
 template <int V, bool STAGED>
@@ -59,18 +62,25 @@ __device__ __forceinline__ void layernorm_rows_regs(const float *__restrict__ X,
   const uint32_t row_bytes = (uint32_t)cols * 4u;
   constexpr int kHalf = V >= 4 ? V / 2 : V;
   float4 v[V];
-  auto load_row = [&](int64_t r) {
+  auto load_row = [&](int64_t r, auto split_tag) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rx = kh::span_rsrc(X + r * xs, row_bytes);
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       v[j] = kh::buf_load4_nt(rx, (uint32_t)(lane + j * kh::kWave) * 16u);
-      if (j + 1 == kHalf && kHalf < V) kh::vm_wait<0>();
+      if (decltype(split_tag)::value && j + 1 == kHalf && kHalf < V) kh::vm_wait<0>();
     }
   };
   if constexpr (STAGED) {
     // Every thread of the block reaches the barrier: the staging sits
     // outside the row loop, and the path choice is uniform over the launch.
-    if (r0 < rows) load_row(r0);
+    // The first row's loads go out before the gamma/beta copy, whose LDS
+    // writes wait for them as well (issue order).
+    if (r0 < rows) {
+      if (kh::split_first_burst(rstep * kh::kWave))  // launch threads
+        load_row(r0, std::true_type{});
+      else
+        load_row(r0, std::false_type{});
+    }
     for (int64_t i = threadIdx.x; 4 * i < cols; i += bd) {
       reinterpret_cast<float4 *>(Gs)[i] = reinterpret_cast<const float4 *>(G)[i];
       reinterpret_cast<float4 *>(Bs)[i] = reinterpret_cast<const float4 *>(B)[i];
@@ -80,7 +90,7 @@ __device__ __forceinline__ void layernorm_rows_regs(const float *__restrict__ X,
   const __amdgpu_buffer_rsrc_t rg = kh::span_rsrc(G, row_bytes), rb = kh::span_rsrc(B, row_bytes);
   for (int64_t r = r0; r < rows; r += rstep) {
     const __amdgpu_buffer_rsrc_t ry = kh::span_rsrc(Y + r * ys, row_bytes);
-    if (!STAGED || r != r0) load_row(r);
+    if (!STAGED || r != r0) load_row(r, std::false_type{});
     float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < V; ++j) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);

@@ -12,9 +12,10 @@
 //                   per wave (4096 FLOP each), no memory traffic in the
 //                   loop: the attainable fp32 matrix rate.
 //
-// The streaming pair uses the fastest pattern a sweep over unroll depth,
-// cache hints and grid size found on MI355X: four nontemporal dwordx4 loads
-// in flight per thread before the stores, 32 workgroups per CU.
+// The streaming pair uses the fastest pattern found on MI355X: four
+// nontemporal dwordx4 accesses per thread and operand, the loads issued in two
+// halves (the second once the first has landed), then the stores; bench.py
+// runs it at one step per workgroup and at 32 grid-strided workgroups per CU.
 #include "kh_device.h"
 
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -23,51 +24,70 @@ namespace {
 constexpr int kU = 4;
 }
 
+// One unrolled step per workgroup: bd x kU float4s through buffer spans over
+// exactly the step's elements (the ragged end needs no branches), nontemporal,
+// the first step's loads in two halves when the launch fits one round
+// (kh::kFirstBurst), as in the product streaming kernels; smaller grids loop
+// over steps.
+namespace {
+// One step of the stream over the float4s [s0, s0 + bd kU) within n4, for
+// N = 1 (copy) or 2 (triad) source operands.
+template <int N, bool SPLIT>
+__device__ __forceinline__ void stream_step(const float *__restrict__ A, const float *__restrict__ B,
+                                            float *__restrict__ C, int64_t n4, int64_t s0, int64_t per,
+                                            uint32_t bd, uint32_t tid) {
+  const uint32_t bytes = (uint32_t)((n4 - s0 < per ? n4 - s0 : per) * 16);
+  const __amdgpu_buffer_rsrc_t ra = kh::span_rsrc(A + 4 * s0, bytes), rc = kh::span_rsrc(C + 4 * s0, bytes);
+  const __amdgpu_buffer_rsrc_t rb = kh::span_rsrc(N == 2 ? B + 4 * s0 : A, N == 2 ? bytes : 0);
+  float4 x[kU], y[kU];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    x[u] = kh::buf_load4_nt(ra, (tid + u * bd) * 16u);
+    if (N == 2) y[u] = kh::buf_load4_nt(rb, (tid + u * bd) * 16u);
+    if (SPLIT && u + 1 == kU / 2) kh::vm_wait<0>();
+  }
+  if (SPLIT) kh::vm_wait<0>();
+#pragma unroll
+  for (int u = 0; u < kU; ++u)
+    kh::buf_store4_nt(rc, (tid + u * bd) * 16u,
+                      N == 2 ? make_float4(x[u].x + y[u].x, x[u].y + y[u].y, x[u].z + y[u].z, x[u].w + y[u].w)
+                             : x[u]);
+}
+
+template <int N>
+__device__ __forceinline__ void stream(const float *__restrict__ A, const float *__restrict__ B,
+                                       float *__restrict__ C, int64_t n, uint32_t gw, uint32_t nb) {
+  const int64_t n4 = n >> 2, bd = kh::threads_x_of(gw), per = bd * kU;
+  const uint32_t tid = threadIdx.x;
+  int64_t s0 = (int64_t)blockIdx.x * per;
+  if (s0 < n4) {
+    if (kh::split_first_burst(bd * (int64_t)nb))
+      stream_step<N, true>(A, B, C, n4, s0, per, (uint32_t)bd, tid);
+    else
+      stream_step<N, false>(A, B, C, n4, s0, per, (uint32_t)bd, tid);
+  }
+  for (s0 += (int64_t)nb * per; s0 < n4; s0 += (int64_t)nb * per)
+    stream_step<N, false>(A, B, C, n4, s0, per, (uint32_t)bd, tid);
+}
+}  // namespace
+
+// One unrolled step per workgroup: bd x kU float4s through buffer spans over
+// exactly the step's elements (the ragged end needs no branches), nontemporal.
+// In a launch that fits one round the first step's loads go out in two
+// halves and its stores once all have landed (kh::kFirstBurst), as in the
+// product streaming kernels; smaller grids loop over steps.
 extern "C" __global__ void __launch_bounds__(256)
 roofline_triad(KH_MEMREF1(const float, a), KH_MEMREF1(const float, b), KH_MEMREF1(float, c)) {
-  const float *__restrict__ A = KH_PTR(a);
-  const float *__restrict__ B = KH_PTR(b);
-  float *__restrict__ C = KH_PTR(c);
-  const int64_t n4 = c_n0 >> 2;
-  const int64_t bd = blockDim.x;
-  const int64_t step = bd * gridDim.x * kU;
-  for (int64_t i = (int64_t)blockIdx.x * bd * kU + threadIdx.x; i + (kU - 1) * bd < n4; i += step) {
-    float4 x[kU], y[kU];
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      x[u] = kh::load_nt(A + 4 * (i + u * bd));
-      y[u] = kh::load_nt(B + 4 * (i + u * bd));
-    }
-#pragma unroll
-    for (int u = 0; u < kU; ++u)
-      kh::store_nt(C + 4 * (i + u * bd), make_float4(x[u].x + y[u].x, x[u].y + y[u].y, x[u].z + y[u].z, x[u].w + y[u].w));
-  }
-  // Vectors past the last full unrolled step.
-  const int64_t done = (n4 / (bd * kU)) * (bd * kU);
-  for (int64_t i = done + (int64_t)blockIdx.x * bd + threadIdx.x; i < n4; i += bd * gridDim.x) {
-    const float4 x = kh::load_nt(A + 4 * i), y = kh::load_nt(B + 4 * i);
-    kh::store_nt(C + 4 * i, make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w));
-  }
+  const uint32_t gw = kh::group_size_word(), nb = kh::grid_blocks_x();
+  KH_ARGS_READY(a_base, a_off, b_base, b_off, c_base, c_off, c_n0, gw, nb);
+  stream<2>(KH_PTR(a), KH_PTR(b), KH_PTR(c), c_n0, gw, nb);
 }
 
 extern "C" __global__ void __launch_bounds__(256)
 roofline_copy(KH_MEMREF1(const float, src), KH_MEMREF1(float, dst)) {
-  const float *__restrict__ S = KH_PTR(src);
-  float *__restrict__ T = KH_PTR(dst);
-  const int64_t n4 = dst_n0 >> 2;
-  const int64_t bd = blockDim.x;
-  const int64_t step = bd * gridDim.x * kU;
-  for (int64_t i = (int64_t)blockIdx.x * bd * kU + threadIdx.x; i + (kU - 1) * bd < n4; i += step) {
-    float4 v[kU];
-#pragma unroll
-    for (int u = 0; u < kU; ++u) v[u] = kh::load_nt(S + 4 * (i + u * bd));
-#pragma unroll
-    for (int u = 0; u < kU; ++u) kh::store_nt(T + 4 * (i + u * bd), v[u]);
-  }
-  // Vectors past the last full unrolled step.
-  const int64_t done = (n4 / (bd * kU)) * (bd * kU);
-  for (int64_t i = done + (int64_t)blockIdx.x * bd + threadIdx.x; i < n4; i += bd * gridDim.x)
-    kh::store_nt(T + 4 * i, kh::load_nt(S + 4 * i));
+  const uint32_t gw = kh::group_size_word(), nb = kh::grid_blocks_x();
+  KH_ARGS_READY(src_base, src_off, dst_base, dst_off, dst_n0, gw, nb);
+  stream<1>(KH_PTR(src), nullptr, KH_PTR(dst), dst_n0, gw, nb);
 }
 
 // out[n0 >= blocks*threads]: one value per thread keeps the chains live.

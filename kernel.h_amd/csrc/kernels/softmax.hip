@@ -27,10 +27,11 @@ namespace {
 
 // The row moves through buffer resources spanning exactly its cols floats:
 // columns past the end read 0 (replaced by -inf before the max) and their
-// stores are dropped, so the path has no per-lane branches. For rows of four
-// or more float4 per lane the loads go out in two halves, the second once the
-// first has landed (kh::kFirstBurst).
-template <int V>
+// stores are dropped, so the path has no per-lane branches. With SPLIT (a
+// wave's first row in a launch that fits one round, four or more float4 per
+// lane) the loads go out in two halves, the second once the first has
+// landed, and nothing else is issued until all have (kh::kFirstBurst).
+template <int V, bool SPLIT = false>
 __device__ __forceinline__ void softmax_row_regs(const float *__restrict__ xr, float *__restrict__ yr,
                                                  int64_t cols, int lane) {
   const __amdgpu_buffer_rsrc_t rx = kh::span_rsrc(xr, (uint32_t)cols * 4u);
@@ -40,8 +41,9 @@ __device__ __forceinline__ void softmax_row_regs(const float *__restrict__ xr, f
 #pragma unroll
   for (int j = 0; j < V; ++j) {
     v[j] = kh::buf_load4_nt(rx, (uint32_t)(lane + j * kh::kWave) * 16u);
-    if (j + 1 == kHalf && kHalf < V) kh::vm_wait<0>();
+    if (SPLIT && j + 1 == kHalf && kHalf < V) kh::vm_wait<0>();
   }
+  if (SPLIT) kh::vm_wait<0>();
   const float ninf = -__builtin_inff();
   float m = ninf;
 #pragma unroll
@@ -101,6 +103,7 @@ __device__ __forceinline__ void softmax_rows(const float *__restrict__ X, float 
   const bool vec = ((cols & 3) == 0) && ((xs & 3) == 0) && ((ys & 3) == 0) && kh::aligned16(X) &&
                    kh::aligned16(Y);
   const int64_t v4 = (cols + 255) / 256;  // float4 per lane needed
+  bool split = kh::split_first_burst(bd * nb);  // each wave's first row only
   for (int64_t r = blockIdx.x * waves_per_block + wave; r < rows; r += nwaves) {
     const float *xr = X + r * xs;
     float *yr = Y + r * ys;
@@ -109,14 +112,15 @@ __device__ __forceinline__ void softmax_rows(const float *__restrict__ X, float 
     } else if (!WIDE && vec && v4 <= 2) {
       softmax_row_regs<2>(xr, yr, cols, lane);
     } else if (!WIDE && vec && v4 <= 4) {
-      softmax_row_regs<4>(xr, yr, cols, lane);
+      split ? softmax_row_regs<4, true>(xr, yr, cols, lane) : softmax_row_regs<4>(xr, yr, cols, lane);
     } else if (WIDE && vec && v4 <= 8) {
-      softmax_row_regs<8>(xr, yr, cols, lane);
+      split ? softmax_row_regs<8, true>(xr, yr, cols, lane) : softmax_row_regs<8>(xr, yr, cols, lane);
     } else if (WIDE && vec && v4 <= KH_SM_MAXV) {
-      softmax_row_regs<KH_SM_MAXV>(xr, yr, cols, lane);
+      split ? softmax_row_regs<KH_SM_MAXV, true>(xr, yr, cols, lane) : softmax_row_regs<KH_SM_MAXV>(xr, yr, cols, lane);
     } else {
       softmax_row_stream(xr, yr, cols, lane);
     }
+    split = false;
   }
 }
 
