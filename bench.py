@@ -78,9 +78,10 @@ class Case:
     input arrays once; every buffer set gets its own device copies of them
     (plus its own outputs), so rotated launches read distinct memory."""
 
-    def __init__(self, name, config, work, unit, bound, host, device, launch, note=""):
+    def __init__(self, name, config, work, unit, bound, host, device, launch, note="", gemm_shape=None):
         self.name, self.config, self.work, self.unit, self.bound = name, config, work, unit, bound
         self.host, self.device, self.launch, self.note = host, device, launch, note
+        self.gemm_shape = gemm_shape  # (m, n, k) for the vendor comparison leg
         self.sets = []
         self.ms = []
 
@@ -137,7 +138,7 @@ def make_cases(kh, rng, only):
                     "TFLOP/s", "mfma",
                     lambda: (u24(rng, m * k, -1, 1), u24(rng, k * nn, -1, 1)),
                     lambda h: (up(h[0]), up(h[1]), out(m * nn)),
-                    lambda s, st: kh.gemm(s[0], s[1], s[2], m, nn, k, st))
+                    lambda s, st: kh.gemm(s[0], s[1], s[2], m, nn, k, st), gemm_shape=(m, nn, k))
 
     add(gemm_case("gemm", 8192, 8192, 8192))
     add(gemm_case("gemm_512", 512, 512, 512))
@@ -350,6 +351,45 @@ def cpu_baseline(budget_s: float):
             "isa": isa}
 
 
+def measure_vendor_gemm(torch, gemm_cases, steps):
+    """The vendor fp32 GEMM (torch.mm: hipBLASLt or rocBLAS, TF32 off) on each
+    GEMM case's shape, under this bench's own conditions: as many rotated
+    buffer sets as the case, U[-1,1] inputs, K back-to-back launches between
+    two events on torch's stream, queued behind a ~0.35 ms copy. A reference
+    point for the same shapes, not part of this build's result."""
+    dev = torch.device("cuda:0")
+    torch.backends.cuda.matmul.allow_tf32 = False
+    prime = (torch.empty(1 << 27, device=dev), torch.empty(1 << 27, device=dev))
+    res = {}
+    for c in gemm_cases:
+        m, n, k = c.gemm_shape
+        gen = torch.Generator(device=dev).manual_seed(20261201)
+        sets = [(torch.rand(m, k, device=dev, generator=gen) * 2 - 1, torch.rand(k, n, device=dev, generator=gen) * 2 - 1,
+                 torch.empty(m, n, device=dev)) for _ in range(len(c.sets))]
+        st = torch.cuda.current_stream()
+        for i in range(3):
+            x, y, z = sets[i % len(sets)]
+            torch.mm(x, y, out=z)
+        best = None
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            prime[1].copy_(prime[0])
+            e0.record(st)
+            for i in range(steps):
+                x, y, z = sets[i % len(sets)]
+                torch.mm(x, y, out=z)
+            e1.record(st)
+            e1.synchronize()
+            ms = e0.elapsed_time(e1) / steps
+            best = ms if best is None else min(best, ms)
+        res[c.name] = {"ms": best, "rate": 2.0 * m * n * k / (best * 1e-3) / 1e12, "unit": "TFLOP/s",
+                       "buffer_sets": len(sets), "library": "torch.mm (hipBLASLt/rocBLAS), tf32 off",
+                       "timing": "best of 3 sequences of K launches"}
+        del sets
+        torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -360,12 +400,21 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-rotate", action="store_true", help="reuse one buffer set (cache-warm)")
     ap.add_argument("--no-ceilings", action="store_true", help="skip the measured roofline microbenchmarks")
+    ap.add_argument("--no-vendor", action="store_true", help="skip the vendor GEMM comparison (torch.mm)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {a.gpus}); "
               "multi-GPU runs are out of scope", file=sys.stderr)
         return 2
 
+    torch = None
+    if not a.no_vendor:
+        try:
+            import torch  # noqa: F811  (vendor GEMM comparison only)
+            if not torch.cuda.is_available():
+                torch = None
+        except Exception:
+            torch = None
     import kernelh as kh
     kh.init_device(0)
     info = kh.device_info()
@@ -427,6 +476,11 @@ def main() -> int:
             f"fp32 MFMA {ceilings['fp32_mfma_tflops']:.1f} TFLOP/s")
     prime[0].free()
     prime[1].free()
+    vendor = {}
+    gemm_cases = [c for c in cases if c.gemm_shape]
+    if torch is not None and gemm_cases:
+        vendor = measure_vendor_gemm(torch, gemm_cases, a.steps)
+        log("[bench] vendor fp32 GEMM: " + ", ".join(f"{k} {v['rate']:.1f}" for k, v in vendor.items()))
 
     kernels = {}
     for c in cases:
@@ -453,6 +507,8 @@ def main() -> int:
             k["traffic_source"] = PMC_TRAFFIC_SOURCE
         if c.note:
             k["note"] = c.note
+        if c.name in vendor:
+            k["vendor"] = dict(vendor[c.name], ratio=rate / vendor[c.name]["rate"])
         kernels[c.name] = k
         log(f"[bench] {c.name:20s} {ms:9.4f} ms  {rate:9.1f} {c.unit}  ({100 * rate / peak:5.1f}% of peak"
             + (f", {100 * k['frac_of_measured']:5.1f}% of measured)" if ceilings else ")"))
