@@ -52,9 +52,9 @@ METRIC = "GEMM-8192 fp32 TFLOPS + softmax/scan HBM GB/s, % of MI355X roofline"
 # profiles/templates_baseline_sizes_hbm_traffic.md. Constants of that profile
 # (median dispatch), not measured by the run that reports them.
 PMC_TRAFFIC_BYTES = {
-    "vecadd": 201381888, "softmax": 33636224, "layernorm": 33738880, "scan": 539398176, "scan_1e6": 8324160,
-    "fused_gelu": 537011456, "fused_gelu_2^22": 33635840, "gemm": 4282522112, "gemm_8192x8192x256": 375275904,
-    "gemm_2048": 117561856, "gemm_512": 10656640, "attention": 1208265984, "attention_s1024": 302283008,
+    "vecadd": 201379840, "softmax": 33652736, "layernorm": 33726464, "scan": 539358208, "scan_1e6": 8348672,
+    "fused_gelu": 536952832, "fused_gelu_2^22": 33637376, "gemm": 3747041280, "gemm_8192x8192x256": 380571648,
+    "gemm_2048": 117557248, "gemm_512": 10651648, "attention": 1208264704, "attention_s1024": 302288896,
 }
 PMC_TRAFFIC_SOURCE = "profiles/templates_baseline_sizes_hbm_traffic.md (constant, not measured by this run)"
 

@@ -45,10 +45,11 @@ def test_compile_writes_artifacts(tmp_path, kernel, shape):
 # way the reference's degraded-mode e2e tests probe theirs for ds_ / exp_f32
 # / rsq (e2e_gemm_test.cpp:211-231, e2e_layernorm_test.cpp:274-292).
 DESIGN_INSTRUCTIONS = {
-    "vecadd": ("n=16777216", ["global_load_dwordx4", "global_store_dwordx4"]),
-    "fused_gelu": ("n=67108864", ["v_exp_f32", "v_rcp_f32", "global_load_dwordx4"]),
-    "softmax": ("rows=4096,cols=1024", ["v_exp_f32", "row_ror:8", "global_load_dwordx4"]),
-    "layernorm": ("rows=4096,cols=1024", ["v_rsq_f32", "row_ror:8", "global_load_dwordx4"]),
+    # Streaming kernels: nontemporal dwordx4 buffer accesses over row / step spans.
+    "vecadd": ("n=16777216", ["buffer_load_dwordx4", "buffer_store_dwordx4", "offen nt"]),
+    "fused_gelu": ("n=67108864", ["v_exp_f32", "v_rcp_f32", "buffer_load_dwordx4", "offen nt"]),
+    "softmax": ("rows=4096,cols=1024", ["v_exp_f32", "row_ror:8", "buffer_load_dwordx4", "offen nt"]),
+    "layernorm": ("rows=4096,cols=1024", ["v_rsq_f32", "row_ror:8", "buffer_load_dwordx4", "offen nt"]),
     "scan": ("n=67108864", ["row_shr:8", "row_bcast:31", "global_atomic_add", "buffer_load_dwordx4"]),
     "gemm": ("m=8192,n=8192,k=8192", ["v_mfma_f32_32x32x2_f32", "offen lds", "ds_read_b128", "s_setprio"]),
     "attention": ("batch=4,heads=16,seq=4096,head_dim=64", ["v_mfma_f32_32x32x2_f32", "v_exp_f32", "ds_read_b128"]),
