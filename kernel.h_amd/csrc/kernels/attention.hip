@@ -234,12 +234,17 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
       const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(Vg), (short)0,
                                                                           (int)(seq * vs * 4), 0x00020000);
       float4 kr[4], vr[4];
-      load_k(kr, rk, ks, 0, tid);
-      load_v(vr, rv, vs, 0, tid);
-      store_k(kr, Ks, tid);
-      store_v(vr, Vt, tid);
-      load_k(kr, rk, ks, TK, tid);
-      store_k(kr, Ks + TK * LDK, tid);
+      {
+        // K0, V0 and K1 go out together (one memory latency before the
+        // first MFMA, not two); the score registers are not live yet.
+        float4 k1[4];
+        load_k(kr, rk, ks, 0, tid);
+        load_v(vr, rv, vs, 0, tid);
+        load_k(k1, rk, ks, TK, tid);
+        store_k(kr, Ks, tid);
+        store_v(vr, Vt, tid);
+        store_k(k1, Ks + TK * LDK, tid);
+      }
       __syncthreads();
       // One pipeline step: S^T of tile t+1 into sn while tile t's softmax
       // and PV consume sc. The loop is unrolled by two so sc and sn swap

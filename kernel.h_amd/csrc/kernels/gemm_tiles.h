@@ -529,22 +529,27 @@ __device__ __forceinline__ void refuse_launch(float *C, int64_t M, int64_t N, in
   for (int64_t i = block * threads + flat; i < M * N; i += stride) C[(i / N) * ldc + i % N] = __builtin_nanf("");
 }
 
-// store_tile for the persistent pipeline (32x32 MFMAs): buffer stores over a
-// resource spanning the tile's rows inside C, so rows past M are dropped by
-// the hardware range check and columns past N go to an offset outside it.
-// Every lane issues exactly WTM x WTN x 16 store instructions, no branches,
+// store_tile for the persistent pipeline: buffer stores over a resource
+// spanning the tile's rows inside C, so rows past M are dropped by the
+// hardware range check and columns past N go to an offset outside it. Every
+// lane issues exactly WTM x WTN x (16 or 4: the accumulator registers of one
+// 32x32 or 16x16 block) store instructions, no branches,
 // so a later wait can count them (gemm_tiles_flat waits for the next
-// tile's slab loads while the most recent 63 of these stores stay in
+// tile's slab loads while the most recent 62 of these stores stay in
 // flight). Needs BM x ldc x 4 < 2^31.
 template <int WTM, int WTN, class T>
 __device__ __forceinline__ void store_tile_buf(const AccOf<T> (&acc)[WTM][WTN], float *__restrict__ Cp, int64_t M,
                                                int64_t N, int64_t ldc, int64_t m0, int64_t n0, int wm, int wn,
                                                int lane) {
-  static_assert(T::kMF == 32, "32x32 accumulator layout");
+  // Accumulator layouts: MF = 32, lane l, register r holds row
+  // 8(r/4) + 4(l/32) + r%4 of its block; MF = 16, row 4(l/16) + r; column
+  // l % MF in both.
+  constexpr int MF = T::kMF;
+  constexpr int kRegs = MF == 32 ? 16 : 4;
   const int64_t rows = (M - m0) < T::BM ? (M - m0) : T::BM;
   const __amdgpu_buffer_rsrc_t rc =
       __builtin_amdgcn_make_buffer_rsrc(Cp + m0 * ldc, (short)0, (int)(rows * ldc * 4), kRsrcWord3);
-  const int col = lane & 31, h = lane >> 5;
+  const int col = lane & (MF - 1), h = lane / MF;
   const uint32_t ld4 = (uint32_t)ldc * 4u;
   // Per lane: one offset per column block (kOutside past N), plus each
   // store's row displacement. The displacement goes into the vector offset,
@@ -553,14 +558,15 @@ __device__ __forceinline__ void store_tile_buf(const AccOf<T> (&acc)[WTM][WTN], 
   uint32_t base[WTN];
 #pragma unroll
   for (int j = 0; j < WTN; ++j) {
-    const int gc = wn * 32 * WTN + j * 32 + col;
-    base[j] = (n0 + gc < N) ? (uint32_t)((wm * 32 * WTM + 4 * h) * ld4 + (uint32_t)(n0 + gc) * 4u) : kOutside;
+    const int gc = wn * MF * WTN + j * MF + col;
+    base[j] = (n0 + gc < N) ? (uint32_t)((wm * MF * WTM + 4 * h) * ld4 + (uint32_t)(n0 + gc) * 4u) : kOutside;
   }
 #pragma unroll
   for (int i = 0; i < WTM; ++i) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const uint32_t rowoff = (uint32_t)(i * 32 + 8 * (r >> 2) + (r & 3)) * ld4;
+    for (int r = 0; r < kRegs; ++r) {
+      const int row = MF == 32 ? i * 32 + 8 * (r >> 2) + (r & 3) : i * 16 + r;
+      const uint32_t rowoff = (uint32_t)row * ld4;
 #pragma unroll
       for (int j = 0; j < WTN; ++j)
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][r]), rc, base[j] + rowoff, 0, 0);
@@ -672,7 +678,7 @@ __device__ __forceinline__ void gemm_tiles_flat(const float *__restrict__ Ap, co
                                                 int64_t lda, int64_t ldb, int64_t ldc, float *As, float *Bs) {
   using T = Tile<WTM, WTN, BKT, true, WGM, WGN, MF>;
   constexpr int BK = T::BK;
-  constexpr int kStores = WTM * WTN * 16;  // store_tile_buf's stores per lane
+  constexpr int kStores = WTM * WTN * (MF == 32 ? 16 : 4);  // store_tile_buf's stores per lane
   constexpr int kStoreSlack = kStores < 62 ? kStores : 62;
   const int tid = threadIdx.x;
   const int lane = kh::lane_id();
