@@ -178,11 +178,11 @@ def rotation_count(bytes_per_set, cap=1024):
 
 def time_queued(kh, stream, launches, prime):
     """Average GPU duration of `launches` (callables, issued back to back)
-    queued behind a ~0.35 ms copy, so the host has enqueued them all before
-    the first starts: microsecond kernels are timed at the GPU's rate, not
-    the host's submission rate."""
+    queued behind `prime(stream)`, a ~0.35 ms copy, so the host has enqueued
+    them all before the first starts: microsecond kernels are timed at the
+    GPU's rate, not the host's submission rate."""
     e0, e1 = kh.Event(), kh.Event()
-    kh.roofline_copy(prime[0], prime[1], prime[2], stream)
+    prime(stream)
     e0.record(stream)
     for f in launches:
         f()
@@ -203,8 +203,9 @@ def measure_ceilings(kh, stream, hbm_cases, prime, steps):
     of exactly each HBM kernel's bytes per launch, rotated like that
     kernel's buffers. Each runs under two geometries: the product streaming
     kernels' (one unrolled step per thread, ceil(n/4/1024) workgroups of
-    256) and 32 grid-strided workgroups per CU. A kernel's ceiling is the
-    best of the 3 GiB streams and its own-size streams.
+    256) and 32 grid-strided workgroups per CU, each the best of five
+    sequences. A kernel's ceiling is the best of the 3 GiB streams and its
+    own-size streams.
 
     fp32 MFMA: independent chains of each fp32 MFMA shape (8 of 32x32x2 or
     16 of 16x16x4 per wave), two waves per SIMD, ~3.5 ms per launch (shorter
@@ -227,7 +228,9 @@ def measure_ceilings(kh, stream, hbm_cases, prime, steps):
             return lambda: kh.launch_raw(fn[kind], (grid, 1, 1), (256, 1, 1), args, stream)
         calls = [launch(sets[i % len(sets)]) for i in range(reps)]
         calls[0]()
-        ms = time_queued(kh, stream, calls, prime)
+        # Best of five sequences: a ceiling is the most the pattern reached,
+        # not one sample of it (the kernels' own rates are means).
+        ms = min(time_queued(kh, stream, calls, prime) for _ in range(5))
         return (12.0 if kind == "triad" else 8.0) * n / (ms * 1e-3) / 1e9
 
     def streams(n, reps, rotate):
@@ -255,7 +258,9 @@ def measure_ceilings(kh, stream, hbm_cases, prime, steps):
     big_best, big_rows = streams(1 << 28, 5, rotate=False)
     per_case = {}
     for c in hbm_cases:
-        best, rows = streams({"copy": int(c.work // 8), "triad": int(c.work // 12)}, steps, rotate=True)
+        # As many launches per sequence as the kernel's own measurement.
+        best, rows = streams({"copy": int(c.work // 8), "triad": int(c.work // 12)},
+                             getattr(c, "gpu_launches", steps), rotate=True)
         per_case[c.name] = {"gbps": max(big_best, best), "own_size_best": best, "streams": rows}
 
     # Both fp32 MFMA shapes, ~3.5 ms launches, ten per sequence; the best of
@@ -351,15 +356,15 @@ def cpu_baseline(budget_s: float):
             "isa": isa}
 
 
-def measure_vendor_gemm(torch, gemm_cases, steps):
+def measure_vendor_gemm(torch, gemm_cases, steps, prime):
     """The vendor fp32 GEMM (torch.mm: hipBLASLt or rocBLAS, TF32 off) on each
     GEMM case's shape, under this bench's own conditions: as many rotated
     buffer sets as the case, U[-1,1] inputs, K back-to-back launches between
-    two events on torch's stream, queued behind a ~0.35 ms copy. A reference
+    two events on torch's stream (as many as this build's own measurement of
+    the case), queued behind the same ~0.35 ms copy. A reference
     point for the same shapes, not part of this build's result."""
     dev = torch.device("cuda:0")
     torch.backends.cuda.matmul.allow_tf32 = False
-    prime = (torch.empty(1 << 27, device=dev), torch.empty(1 << 27, device=dev))
     res = {}
     for c in gemm_cases:
         m, n, k = c.gemm_shape
@@ -371,20 +376,21 @@ def measure_vendor_gemm(torch, gemm_cases, steps):
             x, y, z = sets[i % len(sets)]
             torch.mm(x, y, out=z)
         best = None
+        count = c.gpu_launches  # the same number of launches as this build's measurement
         for _ in range(3):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            prime[1].copy_(prime[0])
+            prime(st.cuda_stream)
             e0.record(st)
-            for i in range(steps):
+            for i in range(count):
                 x, y, z = sets[i % len(sets)]
                 torch.mm(x, y, out=z)
             e1.record(st)
             e1.synchronize()
-            ms = e0.elapsed_time(e1) / steps
+            ms = e0.elapsed_time(e1) / count
             best = ms if best is None else min(best, ms)
         res[c.name] = {"ms": best, "rate": 2.0 * m * n * k / (best * 1e-3) / 1e12, "unit": "TFLOP/s",
                        "buffer_sets": len(sets), "library": "torch.mm (hipBLASLt/rocBLAS), tf32 off",
-                       "timing": "best of 3 sequences of K launches"}
+                       "launches_averaged": count, "timing": "best of 3 sequences"}
         del sets
         torch.cuda.empty_cache()
     return res
@@ -460,27 +466,33 @@ def main() -> int:
         c.ms_host = e0.elapsed_ms(e1) / a.steps
     log(f"[bench] timed {a.steps} steps in {wall:.3f} s")
 
-    # GPU-side launch duration: the same K back-to-back launches, queued
-    # behind a ~0.35 ms copy so that the host has enqueued them all before
-    # the first one starts.
+    # GPU-side launch duration: back-to-back launches over the same buffer
+    # sets, queued behind a ~0.35 ms copy so that the host has enqueued them
+    # all before the first one starts (time_queued).
     prime_n = 1 << 27
-    prime = (kh.Buffer(4 * prime_n), kh.Buffer(4 * prime_n), prime_n)
+    prime_bufs = (kh.Buffer(4 * prime_n), kh.Buffer(4 * prime_n))
+    prime = lambda st: kh.roofline_copy(prime_bufs[0], prime_bufs[1], prime_n, st)
+    # At least ~0.4 ms of launches per kernel (from the timed region's
+    # duration), so the first launches after the primer do not dominate a
+    # microsecond kernel's average: ~57 launches of a 7 us kernel.
     for c in cases:
+        count = max(a.steps, min(256, int(0.4 / max(c.ms_host, 1e-4)) + 1))
+        c.gpu_launches = count
         c.ms = [time_queued(kh, stream, [lambda c=c, i=i: c.launch(c.sets[(a.warmup + i) % len(c.sets)], stream)
-                                         for i in range(a.steps)], prime)]
+                                         for i in range(count)], prime)]
 
     ceilings = None
     if not a.no_ceilings:
         ceilings = measure_ceilings(kh, stream, [c for c in cases if c.bound == "hbm"], prime, a.steps)
         log(f"[bench] measured ceilings: HBM streams at 3 GiB {ceilings['hbm_3GiB_best_gbps']:.0f} GB/s, "
             f"fp32 MFMA {ceilings['fp32_mfma_tflops']:.1f} TFLOP/s")
-    prime[0].free()
-    prime[1].free()
     vendor = {}
     gemm_cases = [c for c in cases if c.gemm_shape]
     if torch is not None and gemm_cases:
-        vendor = measure_vendor_gemm(torch, gemm_cases, a.steps)
+        vendor = measure_vendor_gemm(torch, gemm_cases, a.steps, prime)
         log("[bench] vendor fp32 GEMM: " + ", ".join(f"{k} {v['rate']:.1f}" for k, v in vendor.items()))
+    prime_bufs[0].free()
+    prime_bufs[1].free()
 
     kernels = {}
     for c in cases:
@@ -491,7 +503,7 @@ def main() -> int:
         k = {"config": c.config, "ms_mean": ms, "ms_host_paced": c.ms_host,
              "rate": rate, "rate_host_paced": rate_host, "unit": c.unit,
              "bound": c.bound, "peak": peak, "frac": rate / peak,
-             "algorithmic_work_per_launch": c.work, "buffer_sets": len(c.sets)}
+             "algorithmic_work_per_launch": c.work, "buffer_sets": len(c.sets), "gpu_launches_averaged": c.gpu_launches}
         if ceilings:
             if c.bound == "mfma":
                 k["measured_ceiling"] = ceilings["fp32_mfma_tflops"]
