@@ -143,6 +143,25 @@ __device__ __forceinline__ void layernorm_row_stream(const float *__restrict__ x
   for (int64_t c = lane; c < cols; c += kh::kWave) yr[c] = fmaf((xr[c] - mean) * inv, G[c], B[c]);
 }
 
+// Blocks that are not whole wavefronts (the reference's own layernorm
+// launches use 256 threads, but any block size is accepted): the wave
+// reductions need 64 active lanes, so each thread takes whole rows,
+// serially, with the same two-pass statistics.
+__device__ __forceinline__ void layernorm_row_serial(const float *__restrict__ xr, const float *__restrict__ G,
+                                                     const float *__restrict__ B, float *__restrict__ yr,
+                                                     int64_t cols) {
+  float s = 0.0f;
+  for (int64_t c = 0; c < cols; ++c) s += xr[c];
+  const float mean = s / (float)cols;
+  float q = 0.0f;
+  for (int64_t c = 0; c < cols; ++c) {
+    const float d = xr[c] - mean;
+    q += d * d;
+  }
+  const float inv = __builtin_amdgcn_rsqf(q / (float)cols + kEps);
+  for (int64_t c = 0; c < cols; ++c) yr[c] = fmaf((xr[c] - mean) * inv, G[c], B[c]);
+}
+
 // Shared by both symbols; WIDE selects the register-path widths compiled in
 // (the kernel's register allocation is that of its widest path). Gs and Bs
 // hold kStageCols floats each in the narrow symbol and are unused (null) in
@@ -152,6 +171,11 @@ __device__ __forceinline__ void layernorm_all(const float *__restrict__ X, const
                                               const float *__restrict__ B, float *__restrict__ Y, int64_t rows,
                                               int64_t cols, int64_t xs, int64_t ys, int64_t bd, int64_t nb,
                                               float *Gs, float *Bs) {
+  if (bd % kh::kWave != 0) {  // uniform over the block: no thread reaches a barrier below
+    for (int64_t r = (int64_t)blockIdx.x * bd + threadIdx.x; r < rows; r += bd * nb)
+      layernorm_row_serial(X + r * xs, G, B, Y + r * ys, cols);
+    return;
+  }
   const int lane = kh::lane_id();
   const int64_t waves_per_block = bd / kh::kWave;
   // Uniform per wave (readfirstlane): the row loop and its buffer resources stay scalar.

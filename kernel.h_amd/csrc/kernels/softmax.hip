@@ -11,9 +11,10 @@
 //
 // Rows wider than the register path fall back to a two-sweep form (an online
 // per-lane (max, sum) pass, then a write pass that re-reads the row). Rows
-// are grid-strided over wavefronts, so any launch with a multiple of 64
-// threads per block is correct, including the reference's
-// rows x min(cols, 256) geometry (kernelh_backend.cpp:256-257).
+// are grid-strided over wavefronts; blocks that are not whole wavefronts
+// give each thread whole rows instead, so every launch is correct, including
+// the reference's rows x min(cols, 256) geometry (kernelh_backend.cpp:
+// 256-257) at any cols.
 //
 // exp(x - m) is evaluated as 2^(x*log2e - m*log2e) with one fma on
 // v_exp_f32; y = e * (1/s) with an IEEE reciprocal of s.
@@ -90,12 +91,32 @@ __device__ __forceinline__ void softmax_row_stream(const float *__restrict__ xr,
   for (int64_t c = lane; c < cols; c += kh::kWave) yr[c] = kh::exp2_hw(fmaf(xr[c], kh::kLog2e, mb)) * inv;
 }
 
+// Blocks that are not whole wavefronts (the reference's rows x
+// min(cols, 256) geometry, kernelh_backend.cpp:256-257, when cols < 256 is
+// not a multiple of 64): the wave reductions need 64 active lanes, so each
+// thread takes whole rows, serially.
+__device__ __forceinline__ void softmax_row_serial(const float *__restrict__ xr, float *__restrict__ yr,
+                                                   int64_t cols) {
+  float m = -__builtin_inff();
+  for (int64_t c = 0; c < cols; ++c) m = fmaxf(m, xr[c]);
+  const float mb = -m * kh::kLog2e;
+  float s = 0.0f;
+  for (int64_t c = 0; c < cols; ++c) s += kh::exp2_hw(fmaf(xr[c], kh::kLog2e, mb));
+  const float inv = 1.0f / s;
+  for (int64_t c = 0; c < cols; ++c) yr[c] = kh::exp2_hw(fmaf(xr[c], kh::kLog2e, mb)) * inv;
+}
+
 // Row loop shared by both symbols. WIDE selects which register-path widths
 // are compiled in: the kernel's register allocation is that of its widest
 // path, so the narrow symbol stays lean (more rows in flight per CU).
 template <bool WIDE>
 __device__ __forceinline__ void softmax_rows(const float *__restrict__ X, float *__restrict__ Y, int64_t rows,
                                              int64_t cols, int64_t xs, int64_t ys, int64_t bd, int64_t nb) {
+  if (bd % kh::kWave != 0) {
+    for (int64_t r = (int64_t)blockIdx.x * bd + threadIdx.x; r < rows; r += bd * nb)
+      softmax_row_serial(X + r * xs, Y + r * ys, cols);
+    return;
+  }
   const int lane = kh::lane_id();
   const int64_t waves_per_block = bd / kh::kWave;
   const int64_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kh::kWave);  // uniform: scalar row loop

@@ -157,3 +157,35 @@ def test_layernorm_constant_rows_and_eps0_control(dev):
     # is NaN everywhere, the kernel's eps = 1e-5 output is finite beta.
     ref0 = O.ref_layernorm(x, g, b, rows, cols, eps=0.0)
     assert np.all(np.isnan(ref0)) and not np.any(np.abs(got - ref0) <= 1e-4)
+
+
+@pytest.mark.parametrize("template", ["softmax", "layernorm"])
+@pytest.mark.parametrize("cols", [100, 40, 200])
+def test_rows_blocks_of_partial_waves(dev, template, cols):
+    # The reference's rows x min(cols, 256) geometry (kernelh_backend.cpp:
+    # 256-257) with cols < 256 not a multiple of 64: blocks of `cols`
+    # threads. The verified launch refuses them, as the reference's launch
+    # verifier does; a raw launch (plain hipModuleLaunchKernel) is still
+    # correct: the kernels give each thread whole rows when the block is not
+    # whole wavefronts.
+    rows = 70
+    x, seed = O.lcg_fill(rows * cols, 0x51ED27)
+    g, seed = O.lcg_fill(cols, seed)
+    b, seed = O.lcg_fill(cols, seed)
+    dx, dy = up(x), empty(rows * cols)
+    args = kh.LaunchArgs().add_memref(dx, [rows, cols])
+    if template == "layernorm":
+        dg, db = up(g), up(b)
+        args.add_memref(dg, [cols]).add_memref(db, [cols])
+        ref = O.ref_layernorm(x, g, b, rows, cols)
+    else:
+        ref = O.ref_softmax(x, rows, cols)
+    args.add_memref(dy, [rows, cols])
+    say(f"{template} partial-wave blocks rows={rows} cols={cols} block={min(cols, 256)}")
+    f = kh.template_function(template)
+    with pytest.raises(kh.KhrtError, match="multiple of the wavefront size"):
+        kh.kernel_launch(f, (rows, 1, 1), (min(cols, 256), 1, 1), args)
+    kh.launch_raw(f, (rows, 1, 1), (min(cols, 256), 1, 1), args)
+    kh.synchronize()
+    got = down(dy, rows * cols).reshape(rows, cols)
+    assert np.max(np.abs(got - ref)) <= 1e-4
