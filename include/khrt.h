@@ -158,7 +158,9 @@ typedef struct khrt_launch_config {
 } khrt_launch_config;
 
 /* LaunchVerifier::verify (launch_verifier.cpp:109-172): the five rules (LDS,
- * max threads, wave multiple, grid extents, occupancy > 0). Returns 0 when
+ * max threads, wave multiple, grid extents, occupancy > 0), plus, for a loaded
+ * kernel, its own workgroup-size bound (__launch_bounds__; the reference's
+ * kernels carry none). Returns 0 when
  * launchable, KHRT_E_REFUSED otherwise with every violation, one per line,
  * copied into diag (NUL-terminated, truncated to cap). `function` may be NULL
  * (analytic occupancy) or a loaded kernel (vendor occupancy API). */

@@ -55,7 +55,9 @@ std::string check_elf_image(const unsigned char *b, size_t size);
 // khrt_init_device with the device current.
 int noalloc_setup(int device);
 
-// Drops cached occupancy answers (called when a module is unloaded).
+// Drops the cached occupancy answers and kernel workgroup-size bounds
+// (called when a module is unloaded: a later module's functions can reuse
+// the handles).
 void clear_occupancy_cache();
 
 }  // namespace khrt

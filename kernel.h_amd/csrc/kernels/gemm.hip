@@ -84,6 +84,18 @@ static_assert(Tile<2, 2, 32, false, 2, 4, 16>::BM == KH_GEMM_WIDE_BM &&
                   Tile<2, 2, 32, false, 2, 4, 16>::NT == KH_GEMM_WIDE_THREADS,
               "launcher tile size (gemm_wide)");
 
+// Entry of a symbol whose tile split assumes THREADS one-dimensional
+// threads per workgroup: the arguments in one round, then any other launch
+// shape refused by writing NaN over C (khg::refuse_launch) instead of
+// computing part of each tile.
+#define KH_GEMM_ENTRY_CHECK(THREADS)                                                                            \
+  const uint32_t gxy = kh::group_size_word(), gz = kh::group_size_z_word();                                   \
+  KH_GEMM_ARGS_READY(gxy, gz);                                                                                 \
+  if (kh::threads_x_of(gxy) != (THREADS) || kh::threads_y_of(gxy) != 1 || kh::threads_z_of(gz) != 1) {       \
+    khg::refuse_launch(KH_PTR(C), C_n0, C_n1, C_s0);                                                           \
+    return;                                                                                                    \
+  }
+
 // The reference symbol: 128x256 tiles, persistent. Each workgroup loops
 // over tiles bid, bid + grid, ... (the launcher gives it min(tiles, two per
 // CU) workgroups; any grid is correct) and the three-stage slab ring runs on
@@ -97,21 +109,21 @@ static_assert(Tile<2, 2, 32, false, 2, 4, 16>::BM == KH_GEMM_WIDE_BM &&
 // per-tile pipeline (or the generic path).
 extern "C" __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 gemm(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
-  KH_GEMM_ARGS_READY();
+  KH_GEMM_ENTRY_CHECK(kThreads);
   khg::gemm_entry_flat<2, 4, 16, true>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
 }
 
 // Same arguments and results with 128x128 tiles.
 extern "C" __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_mid(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
-  KH_GEMM_ARGS_READY();
+  KH_GEMM_ENTRY_CHECK(kThreads);
   gemm_entry<2, 2, 32, true, false>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
 }
 
 // Same arguments and results with 64x64 tiles.
 extern "C" __global__ void __launch_bounds__(kThreads)
 gemm_small(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
-  KH_GEMM_ARGS_READY();
+  KH_GEMM_ENTRY_CHECK(kThreads);
   gemm_entry<1, 1, 32, false, false>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
 }
 
@@ -125,7 +137,7 @@ gemm_small(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(fl
 // CU the fewer barriers of `gemm_small` still win (1024^3: 73.9 vs 68.1).
 extern "C" __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_small_pf2(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
-  KH_GEMM_ARGS_READY();
+  KH_GEMM_ENTRY_CHECK(kThreads);
   khg::gemm_entry_pipe<2, 2, 32, true, khg::kPipePrefetch2, 2, 2, 16>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1,
                                                                       A_n1, A_s0, B_s0, C_s0);
 }
@@ -139,12 +151,7 @@ gemm_small_pf2(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF
 // refused by writing NaN over C.
 extern "C" __global__ void __launch_bounds__(KH_GEMM_WIDE_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_wide(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
-  const uint32_t gxy = kh::group_size_word(), gz = kh::group_size_z_word();
-  KH_GEMM_ARGS_READY(gxy, gz);
-  if (kh::threads_x_of(gxy) != KH_GEMM_WIDE_THREADS || kh::threads_y_of(gxy) != 1 || kh::threads_z_of(gz) != 1) {
-    khg::refuse_launch(KH_PTR(C), C_n0, C_n1, C_s0);
-    return;
-  }
+  KH_GEMM_ENTRY_CHECK(KH_GEMM_WIDE_THREADS);
   khg::gemm_entry_pipe<2, 2, 32, true, khg::kPipeRegs, 2, 4, 16>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1,
                                                                  A_s0, B_s0, C_s0);
 }

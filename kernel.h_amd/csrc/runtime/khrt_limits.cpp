@@ -114,6 +114,31 @@ int occupancy_blocks(void *function, int block, size_t shared) {
   return blocks;
 }
 
+// The kernel's own workgroup-size bound (its __launch_bounds__ /
+// max_flat_workgroup_size), cached per function handle until a module is
+// unloaded (a later module's function can reuse the address; see
+// clear_occupancy_cache); -1 when unknown. A launch above it is undefined for
+// the compiled code (register allocation, wave indexing), not merely slow.
+std::mutex g_fmax_mu;
+std::unordered_map<void *, int> g_fmax;
+
+int function_max_threads(void *function) {
+  {
+    std::lock_guard<std::mutex> lock(g_fmax_mu);
+    auto it = g_fmax.find(function);
+    if (it != g_fmax.end()) return it->second;
+  }
+  int v = -1;
+  if (hipFuncGetAttribute(&v, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, static_cast<hipFunction_t>(function)) !=
+      hipSuccess) {
+    (void)hipGetLastError();
+    v = -1;
+  }
+  std::lock_guard<std::mutex> lock(g_fmax_mu);
+  g_fmax[function] = v;
+  return v;
+}
+
 std::string analytic_occupancy_violation(const khrt_launch_config &c, const khrt_device_limits &l) {
   if (l.waves_per_cu <= 0 || l.wavefront_size <= 0 || c.threads_per_workgroup <= 0) return "";
   const long need = (static_cast<long>(c.threads_per_workgroup) + l.wavefront_size - 1) / l.wavefront_size;
@@ -153,6 +178,14 @@ std::string verify(const khrt_launch_config &c, const khrt_device_limits &l, voi
   if (l.max_threads_per_workgroup > 0 && c.threads_per_workgroup > l.max_threads_per_workgroup) {
     v.push_back("threads per workgroup " + std::to_string(c.threads_per_workgroup) + " exceeds the max " +
                 std::to_string(l.max_threads_per_workgroup));
+  }
+  if (function != nullptr && c.threads_per_workgroup > 0) {
+    const int fmax = function_max_threads(function);
+    if (fmax > 0 && c.threads_per_workgroup > fmax) {
+      v.push_back("threads per workgroup " + std::to_string(c.threads_per_workgroup) +
+                  " exceeds the kernel's own maximum " + std::to_string(fmax) +
+                  " (its declared workgroup size bound)");
+    }
   }
   if (l.wavefront_size > 1 && c.threads_per_workgroup > 0 && c.threads_per_workgroup % l.wavefront_size != 0) {
     v.push_back("threads per workgroup " + std::to_string(c.threads_per_workgroup) +
@@ -203,8 +236,12 @@ int resolve_live(khrt_device_limits *out) {
 namespace khrt {
 
 void clear_occupancy_cache() {
-  std::lock_guard<std::mutex> lock(g_occ_mu);
-  g_occ.clear();
+  {
+    std::lock_guard<std::mutex> lock(g_occ_mu);
+    g_occ.clear();
+  }
+  std::lock_guard<std::mutex> lock(g_fmax_mu);
+  g_fmax.clear();
 }
 
 int verified_launch(void *function, khrt_dim3 grid, khrt_dim3 block, size_t shared, void *stream, void **params,

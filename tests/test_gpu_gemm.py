@@ -244,6 +244,37 @@ def test_tune_candidate_refuses_another_block_size(dev):
         assert np.all(np.isnan(down(dC, m * n))), sym
 
 
+@pytest.mark.parametrize("sym,block", [("gemm", 128), ("gemm_mid", 192), ("gemm_small", 64), ("gemm_small_pf2", 128)])
+def test_product_symbols_refuse_another_block_size(dev, sym, block):
+    # The 256-thread symbols' tile split assumes four waves: a smaller
+    # workgroup writes NaN over C, never part of each tile. (A larger one is
+    # refused by the launch itself: test_launch_above_the_kernel_bound_is_refused.)
+    m = n = k = 64
+    A, B = O.gemm_int_inputs(m, n, k)
+    dA, dB, dC = up(A), up(B), empty(m * n, 0.0)
+    args = kh.LaunchArgs().add_memref(dA, [m, k]).add_memref(dB, [k, n]).add_memref(dC, [m, n])
+    say(f"{sym} at {block} threads (refused)")
+    kh.kernel_launch(kh.gemm_candidate_function(sym), (4, 1, 1), (block, 1, 1), args)
+    assert np.all(np.isnan(down(dC, m * n))), sym
+
+
+def test_launch_above_the_kernel_bound_is_refused(dev):
+    # A workgroup above the kernel's own bound (__launch_bounds__(256)) is
+    # refused before it reaches the GPU, with the bound in the message.
+    m = n = k = 64
+    A, B = O.gemm_int_inputs(m, n, k)
+    dA, dB, dC = up(A), up(B), empty(m * n, 0.0)
+    args = kh.LaunchArgs().add_memref(dA, [m, k]).add_memref(dB, [k, n]).add_memref(dC, [m, n])
+    f = kh.gemm_candidate_function("gemm")
+    # The verifier alone first (nothing launched): only if it refuses is the
+    # verified launch tried, which then refuses on the host the same way.
+    diag = kh.verify_launch(512, grid=(4, 1, 1), function=f)
+    assert "exceeds the kernel's own maximum 256" in diag, diag
+    with pytest.raises(kh.KhrtError, match="exceeds the kernel's own maximum 256"):
+        kh.kernel_launch(f, (4, 1, 1), (512, 1, 1), args)
+    assert np.all(down(dC, m * n) == 0.0)
+
+
 def test_tune_cache_steers_the_launcher(dev, tmp_path):
     """A tune cache entry for a shape makes kh_gemm (and the geometry and
     symbol queries) run the cached candidate for that shape only; other
