@@ -114,7 +114,8 @@ struct Header {
   uint32_t failed, pad;
 };
 struct Counters {
-  uint32_t counter, pad;  // tickets, mod 2^32 (a call takes far fewer)
+  uint32_t counter, pad;  // tickets, mod 2^32 (a call takes far fewer); pad takes
+                          // the carries of 64-bit ticket adds and is never read
   uint64_t done;          // low 32 bits: workgroups done; high 32: their tickets
 };
 static_assert(sizeof(Header) == 32 && sizeof(Counters) == 16, "header layout");
@@ -200,12 +201,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t record_rsrc(const Record *r) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<Record *>(r), (short)0, 0x7fffffff, 0x00020000);
 }
 
-// Publishes one value of tile t (absolute ticket): its aggregate (key
-// keys.agg) or its inclusive prefix (key keys.inc, replacing the aggregate).
-__device__ __forceinline__ void publish(Record *r, uint64_t key, uint64_t t, double v) {
+// Publishes one value of tile `tile` when `on`, from lane 0: its aggregate
+// (key keys.agg) or its inclusive prefix (key keys.inc, replacing the
+// aggregate); t is the tile's tag input. (One store from the whole wave, its
+// other lanes addressing past the resource's range, keeps the compiler's
+// wait counts exact on every path, but measured slower: 117 against 103 us
+// for the scan at n = 2^26.)
+__device__ __forceinline__ void publish(Record *rec, bool on, int64_t tile, uint64_t key, uint64_t t, double v,
+                                        int lane) {
   const uint64_t b = bits(v), c = b ^ tag(key, t);
   const u32x4 w = {(unsigned)b, (unsigned)(b >> 32), (unsigned)c, (unsigned)(c >> 32)};
-  __builtin_amdgcn_raw_buffer_store_b128(w, record_rsrc(r), 0, 0, kSc1);
+  if (on && lane == 0)
+    __builtin_amdgcn_raw_buffer_store_b128(w, record_rsrc(rec), (uint32_t)tile * (uint32_t)sizeof(Record), 0, kSc1);
 }
 
 // The call's view of the state: where it is, the ticket of tile 0 (low 32
@@ -435,8 +442,8 @@ struct Window {
 };
 
 __device__ __forceinline__ void poll_window(Window &w, const Session &s, int64_t end, int lane) {
-  // Byte offsets of the records from the (wave-uniform) record base: 32-bit,
-  // as no device holds 2^32 B of records (that would be 2^28 tiles).
+  // Byte offsets of the records from the (wave-uniform) record base: 32-bit
+  // and below 2^31 (tile indices are below 2^27).
 #pragma unroll
   for (int j = 0; j < kWindow; ++j) {
     const int64_t idx = end - lane - kh::kWave * j;
@@ -448,6 +455,18 @@ __device__ __forceinline__ void poll_window(Window &w, const Session &s, int64_t
     w.value[j] = ((uint64_t)q.y << 32) | q.x;
     w.chk[j] = ((uint64_t)q.w << 32) | q.z;
   }
+}
+
+// Waits, right here, until a polled window has landed. The look-back's
+// polls are needed at once anyway; waiting for them where they are issued
+// (not only where they are decoded) leaves no poll in flight on any path of
+// the compiler's structured control flow. Such a path (one the look-back
+// never takes) would otherwise carry the poll's registers "pending" into the
+// next step, where their reuse waits for every memory operation in flight,
+// the previous step's record stores included.
+__device__ __forceinline__ void settle(const Window &w) {
+#pragma unroll
+  for (int j = 0; j < kWindow; ++j) asm volatile("" ::"v"(w.value[j]), "v"(w.chk[j]));
 }
 
 // Published values of a polled window, kEmpty where unpublished (never an
@@ -502,6 +521,7 @@ __device__ __forceinline__ double look_back(const Session &s, int64_t tile, int 
       }
       __builtin_amdgcn_s_sleep(1);
       poll_window(w, s, end, lane);
+      settle(w);
       continue;
     }
     double contrib = 0.0;
@@ -518,6 +538,7 @@ __device__ __forceinline__ double look_back(const Session &s, int64_t tile, int 
     if (first < kWindow * kh::kWave) return excl;
     end -= kWindow * kh::kWave;
     poll_window(w, s, end, lane);
+    settle(w);
   }
 }
 
@@ -539,9 +560,16 @@ __device__ __forceinline__ int64_t tile_of(uint32_t ticket, uint64_t base, int64
 // the publication latency of tiles handed out just before it.
 // The last wave is the control wave: it takes tickets and does the
 // look-back and never touches tile data; the other (data) waves load,
-// reduce and store. Vector-memory waits are in issue order per wave, so the
-// look-back's polls never wait on tile loads or stores. Each iteration takes
-// one ticket; its value is first needed at barrier B.
+// reduce and store. The two kinds of wave run loops of their own that meet
+// at the same two barriers per iteration (A and B, the same count on both
+// sides, from the same shared ticket sequence), so the compiler's wait counts
+// for one never cover the other's memory operations. The data waves issue
+// their tile loads and stores on every path (a tile that is not there has an
+// empty range), so a data wave waits for its tile loads only, with its stores
+// left in flight; the control wave waits for its ticket and polls only.
+// (One loop for both kinds, with the waits the compiler then has to assume,
+// ran 107-108 us at n = 2^26 and 13.4 us at 10^6 against 103 and 12.7 us.)
+// Each iteration takes one ticket; its value is first needed at barrier B.
 // Deadlock-free: the lowest tile in look-back only needs aggregates of lower
 // tiles, and each of those is either finished or in the reduce stage of a
 // workgroup that publishes it without waiting on anything.
@@ -557,52 +585,114 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
                                            uint64_t *s_done, int bd) {
   const int tid = threadIdx.x;
   const int lane = kh::lane_id();
-  const int wave = tid / kh::kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kh::kWave);
   const int ndata = bd / kh::kWave - 1;
-  const bool ctrl = wave == ndata;
   const int64_t tile_elems = (int64_t)ndata * kh::kWave * kPerThread;
   const int64_t ntiles = (n + tile_elems - 1) / tile_elems;
-  const int seg = wave * kh::kWave * kPerThread;  // data waves: offset in the tile
-  // Per-thread row offsets of a reduced tile wait in LDS for its output
-  // stage (two buffers: reduce stage and output stage, alternating).
-  double *my_off = s_off + tid;
-  auto elems = [&](int64_t t) { return n - t * tile_elems < tile_elems ? n - t * tile_elems : tile_elems; };
 
-  int64_t tc = -1;       // no tile to finish in the first iteration
+  int64_t tc = -1;  // no tile to finish in the first iteration
   // Tickets are taken until one comes back at or past the last tile (the
   // starting pair included); uniform across the workgroup.
   bool taking = !single && tn < ntiles;
   bool counting = !single && !taking;  // count_done due in the next step
-  uint32_t tickets = 2;  // control wave, lane 0
-  double agg_c = 0.0;    // control wave: aggregate of tile tc
-  double wexcl_c = 0.0;  // data waves: sum of earlier waves' totals in tile tc
   int slot = 0;
+  // After barrier B, for every wave: the tile of the ticket taken in this
+  // step (when one was), the ticket state, and the tiles of the next step.
+  // False once tc was the workgroup's last tile.
+  auto advance = [&](bool take) __attribute__((always_inline)) -> bool {
+    const int64_t after =
+        take ? tile_of((uint32_t)__builtin_amdgcn_readfirstlane((int)s_raw[slot]), ses.base, ntiles) : ntiles;
+    if (take && after >= ntiles) {
+      taking = false;  // the workgroup's last ticket is back
+      counting = true;
+    }
+    if (tr >= ntiles) return false;
+    tc = tr;
+    tr = tn;
+    tn = after;
+    // s_raw[slot] was read above, after barrier B, and is next written two
+    // iterations later. s_wave_total and s_prefix are rewritten only after
+    // every wave has passed the next barrier A, past all their reads. A
+    // thread's row offsets are its own: buffer `slot` holds tile tr's (read
+    // as tile tc's in the next iteration, where slot has flipped).
+    slot ^= 1;
+    return true;
+  };
+
+  if (wave == ndata) {
+    // ---- control wave -------------------------------------------------------
+    uint32_t tickets = 2;  // lane 0
+    double agg_c = 0.0;    // aggregate of tile tc
+    // The ticket counter as a 64-bit word (its low half is the counter), so
+    // that a ticket and the done count are one atomic instruction of one
+    // width, whose result needs no merge of two values (which would wait
+    // for it where it is issued).
+    uint64_t *const counter64 = reinterpret_cast<uint64_t *>(&ses.c->counter);
+    for (;;) {
+      const bool take = taking, count = counting;
+      counting = false;
+      const bool looks_back = tc > 0;
+      // The one atomic of the step: the next ticket, or the done count.
+      // Defined only on lane 0, where it is used.
+      uint64_t raw;
+      if (lane == 0 && (take || count)) {
+        raw = fetch_add(take ? counter64 : &ses.c->done, take ? uint64_t(1) : ((uint64_t)tickets << 32) | 1u);
+        tickets += take;
+      }
+      // The first look-back poll for tile tc goes out now, before barrier
+      // A: tc was reduced (and its predecessors' aggregates published) in
+      // earlier iterations, so its round trip overlaps the data waves'
+      // reduction. Always issued; waited for before any branch below.
+      Window w;
+      poll_window(w, ses, looks_back ? tc - 1 : 0, lane);
+      kh::lds_barrier();  // barrier A
+      // ---- publish tile tr's aggregate (tile 0: it is its inclusive) -------
+      double agg_r = 0.0;
+      if (tr < ntiles) agg_r = wave_sum_f64(lane < ndata ? s_wave_total[lane] : 0.0);
+      publish(ses.rec, !single && tr < ntiles - 1, tr, tr == 0 ? ses.keys.inc : ses.keys.agg, tag_of(ses.base, tr),
+              agg_r, lane);
+      // ---- decoupled look-back for tile tc -----------------------------------
+      settle(w);
+      double excl = 0.0;
+      if (looks_back) excl = look_back(ses, tc, lane, w);
+      // The atomic went out before the polls just waited for.
+      if (lane == 0) {
+        *s_prefix = excl;
+        s_raw[slot] = take ? raw : 0ull;
+        if (count) {
+          s_done[0] = raw;
+          s_done[1] = tickets;
+        }
+      }
+      publish(ses.rec, looks_back && tc < ntiles - 1, tc, ses.keys.inc, tag_of(ses.base, tc), excl + agg_c, lane);
+      agg_c = agg_r;
+      kh::lds_barrier();  // barrier B
+      if (!advance(take)) return;
+    }
+  }
+
+  // ---- data waves -------------------------------------------------------------
+  const int seg = wave * kh::kWave * kPerThread;  // offset in the tile
+  // Per-thread row offsets of a reduced tile wait in LDS for its output
+  // stage (two buffers: reduce stage and output stage, alternating).
+  double *my_off = s_off + tid;
+  // Buffer resource over tile t's elements; empty for a tile that is not there.
+  auto span = [&](const float *base, int64_t t) {
+    const bool in = t >= 0 && t < ntiles;
+    const int64_t at = in ? t * tile_elems : 0;
+    return tile_rsrc(base + at, in ? (n - at < tile_elems ? n - at : tile_elems) : 0);
+  };
+  double wexcl_c = 0.0;  // sum of earlier waves' totals in tile tc
 
   // One pipeline iteration: finish tc (data in vc), reduce tr (vr), load tn
   // (into vn). False once tc was the workgroup's last tile. The caller
   // rotates the three register buffers instead of copying them.
   auto step = [&](float (&vc)[kPerThread], float (&vr)[kPerThread], float (&vn)[kPerThread])
       __attribute__((always_inline)) -> bool {
-    const bool take = taking, count = counting;
+    const bool take = taking;
     counting = false;
-    // Defined only where it is used (control wave, lane 0): a default value
-    // on the data path would be a register write that must wait for the
-    // pending atomic, i.e. for all of that wave's outstanding memory ops.
-    uint64_t raw;
-    // The first look-back poll for tile tc goes out now, before the barrier:
-    // tc was reduced (and its predecessors' aggregates published) in earlier
-    // iterations, so its round trip overlaps the data waves' reduction.
-    // Defined on the control wave only, like `raw`.
-    Window w;
-    if (ctrl) {
-      if (lane == 0 && (take || count)) {
-        // One atomic either way: the next ticket, or the done count.
-        raw = take ? (uint64_t)fetch_add(&ses.c->counter, 1u) : fetch_add(&ses.c->done, ((uint64_t)tickets << 32) | 1u);
-        tickets += take;
-      }
-      if (tc > 0) poll_window(w, ses, tc - 1, lane);
-    } else if (tr < ntiles) {
-      // ---- reduce tile tr: per-row lane sums (fp64), wave scans, wave total ---
+    if (tr < ntiles) {
+      // ---- reduce tile tr: per-row lane sums (fp64), wave scans, wave total -
       // off[k] = (rows before k) + (lanes before this one in row k); exact,
       // as every partial sum here is.
       double pre = 0.0;
@@ -617,50 +707,14 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
       if (lane == 0) s_wave_total[wave] = pre;
     }
     kh::lds_barrier();  // barrier A
-
+    // ---- tile tn's loads go out now and land during the look-back ----------
+    load_seg<VEC>(vn, span(X, tn), seg, lane);
     double wexcl_r = 0.0;
-    if (ctrl) {
-      // ---- publish tile tr's aggregate (tile 0: it is its inclusive) ---------
-      double agg_r = 0.0;
-      if (tr < ntiles) {
-        agg_r = wave_sum_f64(lane < ndata ? s_wave_total[lane] : 0.0);
-        if (!single && lane == 0 && tr < ntiles - 1) {
-          publish(ses.rec + tr, tr == 0 ? ses.keys.inc : ses.keys.agg, tag_of(ses.base, tr), agg_r);
-        }
-      }
-      // ---- decoupled look-back for tile tc -------------------------------------
-      double excl = 0.0;
-      if (tc > 0) {
-        excl = look_back(ses, tc, lane, w);
-        if (lane == 0 && tc < ntiles - 1) {
-          publish(ses.rec + tc, ses.keys.inc, tag_of(ses.base, tc), excl + agg_c);
-        }
-      }
-      agg_c = agg_r;
-      if (lane == 0) {
-        *s_prefix = excl;
-        s_raw[slot] = take ? raw : 0ull;
-        if (count) {
-          s_done[0] = raw;
-          s_done[1] = tickets;
-        }
-      }
-    } else {
-      // ---- tile tn's loads go out now and land during the look-back ----------
-      // (past the last tile the range is empty: the loads read 0.)
-      load_seg<VEC>(vn, tile_rsrc(X + tn * tile_elems, tn < ntiles ? elems(tn) : 0), seg, lane);
-      if (tr < ntiles)
-        for (int w = 0; w < wave; ++w) wexcl_r += s_wave_total[w];
-    }
+    if (tr < ntiles)
+      for (int w = 0; w < wave; ++w) wexcl_r += s_wave_total[w];
     kh::lds_barrier();  // barrier B
-    const int64_t after = take ? tile_of((uint32_t)s_raw[slot], ses.base, ntiles) : ntiles;
-    if (take && after >= ntiles) {
-      taking = false;  // the workgroup's last ticket is back
-      counting = true;
-    }
-
-    if (!ctrl && tc >= 0) {
-      // ---- y = fl32(prefix + row offset + running sum within the float4) -----
+    // ---- y = fl32(prefix + row offset + running sum within the float4) -----
+    {
       const double prefix = *s_prefix + wexcl_c;
       float o[kPerThread];
 #pragma unroll
@@ -672,25 +726,16 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
           o[4 * k + j] = (float)run;
         }
       }
-      store_seg<VEC>(o, tile_rsrc(Y + tc * tile_elems, elems(tc)), seg, lane);
+      store_seg<VEC>(o, span(Y, tc), seg, lane);
     }
-
-    if (tr >= ntiles) return false;  // tc was this workgroup's last tile
-    tc = tr;
-    tr = tn;
-    tn = after;
     wexcl_c = wexcl_r;
-    // s_raw[slot] was read after barrier B above and is next written two
-    // iterations later. s_wave_total and s_prefix are rewritten only after
-    // every wave has passed the next barrier A, past all their reads. A
-    // thread's row offsets are its own: buffer `slot` holds tile tr's (read
-    // as tile tc's in the next iteration, where slot has flipped).
-    slot ^= 1;
-    return true;
+    return advance(take);
   };
 
   float a[kPerThread], b[kPerThread], c[kPerThread];
-  if (!ctrl) load_seg<VEC>(b, tile_rsrc(X + tr * tile_elems, elems(tr)), seg, lane);
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i) a[i] = c[i] = 0.0f;
+  load_seg<VEC>(b, span(X, tr), seg, lane);
   for (;;) {
     if (!step(a, b, c)) return;
     if (!step(b, c, a)) return;
@@ -747,9 +792,11 @@ scan(KH_MEMREF1(const float, x), KH_MEMREF1(float, y), KH_MEMREF1(float, y_lo),
   const int64_t tile_elems = (int64_t)(bdx - kh::kWave) * kPerThread;
   const int64_t ntiles = shape_ok ? (n + tile_elems - 1) / tile_elems : 0;
   const int64_t lo_bytes = bytes_from_align8(KH_PTR(totals_lo), totals_lo_n0, totals_lo_s0);
-  // (Tickets and tile indices are 32-bit: ntiles < 2^31 always holds for a
-  // device's memory; refused otherwise.)
-  const bool room = ntiles < (int64_t(1) << 31) && (ntiles == 1 ||
+  // (Tickets and tile indices are 32-bit and records are addressed with
+  // 32-bit byte offsets below 2^31: ntiles < 2^27, which always holds for a
+  // device's memory (2^27 tiles of at least 3072 elements); refused
+  // otherwise.)
+  const bool room = ntiles < (int64_t(1) << 27) && (ntiles == 1 ||
                     (lo_bytes >= (int64_t)(sizeof(Header) + sizeof(Counters)) &&
                      bytes_from_align8(KH_PTR(totals_hi), totals_hi_n0, totals_hi_s0) >=
                          (int64_t)sizeof(Record) * (ntiles - 1)));
