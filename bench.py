@@ -52,9 +52,9 @@ METRIC = "GEMM-8192 fp32 TFLOPS + softmax/scan HBM GB/s, % of MI355X roofline"
 # profiles/templates_baseline_sizes_hbm_traffic.md. Constants of that profile
 # (median dispatch), not measured by the run that reports them.
 PMC_TRAFFIC_BYTES = {
-    "vecadd": 201379840, "softmax": 33652736, "layernorm": 33726464, "scan": 539358208, "scan_1e6": 8348672,
-    "fused_gelu": 536952832, "fused_gelu_2^22": 33637376, "gemm": 3747041280, "gemm_8192x8192x256": 380571648,
-    "gemm_2048": 117557248, "gemm_512": 10651648, "attention": 1208264704, "attention_s1024": 302288896,
+    "vecadd": 201380224, "softmax": 33662656, "layernorm": 33725120, "scan": 539465632, "scan_1e6": 8234752,
+    "fused_gelu": 536955520, "fused_gelu_2^22": 33637952, "gemm": 3807616768, "gemm_8192x8192x256": 378323328,
+    "gemm_2048": 117561024, "gemm_512": 10650624, "attention": 1208266240, "attention_s1024": 302303872,
 }
 PMC_TRAFFIC_SOURCE = "profiles/templates_baseline_sizes_hbm_traffic.md (constant, not measured by this run)"
 
