@@ -234,14 +234,19 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
       const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(Vg), (short)0,
                                                                           (int)(seq * vs * 4), 0x00020000);
       float4 kr[4], vr[4];
+      v16f sa[2], sb[2];
       {
         // K0, V0 and K1 go out together (one memory latency before the
-        // first MFMA, not two); the score registers are not live yet.
+        // first MFMA, not two). Only Q and K0 are waited for before tile
+        // 0's S^T (loads complete in issue order; the barrier fences LDS
+        // only): V0 and K1 keep arriving under those MFMAs.
         float4 k1[4];
         load_k(kr, rk, ks, 0, tid);
         load_v(vr, rv, vs, 0, tid);
         load_k(k1, rk, ks, TK, tid);
         store_k(kr, Ks, tid);
+        kh::lds_barrier();
+        qk_tile(sa, q, Ks, lane);
         store_v(vr, Vt, tid);
         store_k(k1, Ks + TK * LDK, tid);
       }
@@ -259,8 +264,6 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
         store_v(vr, Vt + (cur ^ 1) * D * LDV, tid);
         __syncthreads();
       };
-      v16f sa[2], sb[2];
-      qk_tile(sa, q, Ks, lane);
       int64_t t = 0;
       for (; t + 2 < ntiles; t += 2) {
         step(t, sa, sb);
