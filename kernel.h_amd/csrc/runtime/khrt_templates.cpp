@@ -381,8 +381,8 @@ int geometry(const char *name, const Shape &s, khrt_dim3 &grid, khrt_dim3 &block
   } else if (t == "scan" || t == "scan_totals") {
     if (!need(s, "n", n)) return khrt::fail(KHRT_E_INVALID, t + ": shape attribute 'n' is required and must be positive");
     if (t == "scan") {
-      block.x = KH_SCAN_THREADS;
-      grid.x = clamp_grid(ceil_div(n, KH_SCAN_TILE));
+      block.x = n <= KH_SCAN_SMALL_N ? KH_SCAN_SMALL_THREADS : KH_SCAN_THREADS;
+      grid.x = clamp_grid(ceil_div(n, int64_t(KH_SCAN_PER_THREAD) * (block.x - 64)));
     } else {
       grid.x = clamp_grid(std::min<int64_t>(ceil_div(ceil_div(n, 256) + 1, 256), 1024));
     }
