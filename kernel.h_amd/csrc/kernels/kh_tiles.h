@@ -17,10 +17,10 @@
 #define KH_SCAN_THREADS 1024
 #define KH_SCAN_TILE (KH_SCAN_PER_THREAD * (KH_SCAN_THREADS - 64))
 // The launcher's workgroup size up to KH_SCAN_SMALL_N elements: at
-// n = 10^6, 89 tiles of 11,264 ran 11.15 us against 66 of 15,360 in
-// 11.54 us; at 4 * 10^6 1024 threads were faster (21.2 against 22.0 us).
+// n = 10^6, 89 tiles of 11,264 ran 8.35 us against 66 of 15,360 in
+// 8.52 us; at 2 * 10^6 1024 threads were faster (10.1 against 10.6 us).
 #define KH_SCAN_SMALL_THREADS 768
-#define KH_SCAN_SMALL_N (1 << 21)
+#define KH_SCAN_SMALL_N (3 << 19)
 
 // GEMM block tiles (rows of C x columns of C per workgroup of 256 threads).
 #define KH_GEMM_BM 128

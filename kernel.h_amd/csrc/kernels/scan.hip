@@ -233,24 +233,26 @@ __device__ __forceinline__ uint64_t tag_of(uint64_t base, int64_t tile) {
 }
 
 // Run by one thread per workgroup at the start of a multi-tile call. Takes
-// the workgroup's first two tickets (t0 < t1, both >= base) and the
-// session; false if the header could not be established within the bounded
-// wait. The header loads and the ticket atomics go out together, so a
-// recognised header costs one round trip.
+// the workgroup's first two tickets (t0 < t1, both >= base), or only t0
+// when `pair` is false, and the session; false if the header could not be
+// established within the bounded wait. The header loads and the ticket
+// atomics go out together, so a recognised header costs one round trip.
 struct Opened {
   uint64_t base, nonce;
   uint32_t t0, t1;
   bool ok;
 };
 
-__device__ __forceinline__ Opened open_session(Header *h, Counters *c, int64_t ntiles, uint64_t nblocks) {
+__device__ __forceinline__ Opened open_session(Header *h, Counters *c, int64_t ntiles, uint64_t nblocks, bool pair) {
   Opened o;
   o.ok = true;
   o.base = ld(&h->base);
   o.nonce = ld(&h->nonce);
   const uint64_t seen0 = ld(&h->check);
   o.t0 = fetch_add(&c->counter, 1u);
-  o.t1 = fetch_add(&c->counter, 1u);
+  // Without a pair, t1 stands for "no second tile": t0 itself in the checks
+  // below, and the caller ignores it.
+  o.t1 = pair ? fetch_add(&c->counter, 1u) : o.t0;
   // A call takes every ticket below ntiles once and at most two more per
   // workgroup, all >= base: a ticket outside that range means the counter
   // was changed behind the header's back (another kernel wrote it), and the
@@ -303,7 +305,7 @@ __device__ __forceinline__ Opened open_session(Header *h, Counters *c, int64_t n
   // Tickets taken before the session began are not tiles of this call.
   if ((int32_t)(o.t1 - first_ticket(o.base)) < 0) {
     o.t0 = fetch_add(&c->counter, 1u);
-    o.t1 = fetch_add(&c->counter, 1u);
+    o.t1 = pair ? fetch_add(&c->counter, 1u) : o.t0;
   } else if ((int32_t)(o.t0 - first_ticket(o.base)) < 0) {
     o.t0 = o.t1;
     o.t1 = fetch_add(&c->counter, 1u);
@@ -312,8 +314,8 @@ __device__ __forceinline__ Opened open_session(Header *h, Counters *c, int64_t n
 }
 
 // Counts a workgroup as finished with the call's tickets, adding the
-// number it took (`tickets`: its first two plus one per tile-loop step that
-// took one, all >= base). Issued by one thread as soon as the workgroup's
+// number it took (`tickets`: its first one or two plus one per tile-loop
+// step that took one, all >= base). Issued by one thread as soon as the workgroup's
 // last ticket has come back (one at or past the last tile).
 __device__ __forceinline__ uint64_t count_done(Counters *c, uint32_t tickets) {
   return fetch_add(&c->done, ((uint64_t)tickets << 32) | 1u);
@@ -575,16 +577,17 @@ __device__ __forceinline__ int64_t tile_of(uint32_t ticket, uint64_t base, int64
 // Deadlock-free: the lowest tile in look-back only needs aggregates of lower
 // tiles, and each of those is either finished or in the reduce stage of a
 // workgroup that publishes it without waiting on anything.
-// The control wave takes the workgroup's tickets from the third on, so it
-// also counts the workgroup done (count_done), in the step after a ticket at
-// or past the last tile came back: its one atomic of a step then goes to
+// The control wave takes the workgroup's tickets after its first one or two,
+// so it also counts the workgroup done (count_done), in the step after a
+// ticket at or past the last tile came back (the first step when the
+// workgroup started with one ticket): its one atomic of a step then goes to
 // `done` instead of `counter`. The result lands in s_done[0], the
 // workgroup's ticket count in s_done[1], before that step's barrier B.
 template <bool VEC>
 __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *__restrict__ Y, const Session &ses,
                                            int64_t n, int64_t tr, int64_t tn, bool single, uint64_t *s_raw,
                                            double *s_wave_total, double *s_prefix, double *s_off,
-                                           uint64_t *s_done, int bd) {
+                                           uint64_t *s_done, int bd, uint32_t tickets0) {
   const int tid = threadIdx.x;
   const int lane = kh::lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(tid / kh::kWave);
@@ -623,7 +626,7 @@ __device__ __forceinline__ void scan_tiles(const float *__restrict__ X, float *_
 
   if (wave == ndata) {
     // ---- control wave -------------------------------------------------------
-    uint32_t tickets = 2;  // lane 0
+    uint32_t tickets = tickets0;  // lane 0: taken so far
     double agg_c = 0.0;    // aggregate of tile tc
     // The ticket counter as a 64-bit word (its low half is the counter), so
     // that a ticket and the done count are one atomic instruction of one
@@ -807,14 +810,22 @@ scan(KH_MEMREF1(const float, x), KH_MEMREF1(float, y), KH_MEMREF1(float, y_lo),
   Session ses{align8<Header>(KH_PTR(totals_lo)), nullptr, align8<Record>(KH_PTR(totals_hi)), 0, Keys{0, 0}};
   ses.c = counters_of(ses.h, lo_bytes);
   const bool single = ntiles == 1;  // one tile: one workgroup, no look-back state
+  // A workgroup takes two tickets at the start when there are more tiles
+  // than workgroups (the second tile's loads then go out in the first
+  // step), one otherwise: two each would hand every tile of a one-round
+  // launch to the first half of the workgroups to arrive and leave the
+  // rest idle (n = 10^6: 89 tiles on 89 workgroups ran as 48 workgroups of
+  // up to two tiles).
+  const bool pair = ntiles > (int64_t)nblocks;
+  const uint32_t tickets0 = pair ? 2 : 1;
   Opened o{0, 0, 0, 0, true};
   if (!refuse && !single) {
     if (tid == 0) {
-      o = open_session(ses.h, ses.c, ntiles, nblocks);
+      o = open_session(ses.h, ses.c, ntiles, nblocks, pair);
       s_session[0] = o.base;
       s_session[1] = session_key(ses.h, o.nonce);
       s_ticket[0] = tile_of(o.t0, o.base, ntiles);
-      s_ticket[1] = tile_of(o.t1, o.base, ntiles);
+      s_ticket[1] = pair ? tile_of(o.t1, o.base, ntiles) : ntiles;
       s_refuse = !o.ok;
     }
     kh::lds_barrier();
@@ -843,14 +854,16 @@ scan(KH_MEMREF1(const float, x), KH_MEMREF1(float, y), KH_MEMREF1(float, y_lo),
   ses.keys = record_keys(s_session[1]);
   if (first >= ntiles) {
     // No tile for this workgroup: both its tickets are past the end.
-    if (tid == 0) close_session(ses.h, ses.c, ses.base, o.nonce, count_done(ses.c, 2), 2, nblocks);
+    if (tid == 0) close_session(ses.h, ses.c, ses.base, o.nonce, count_done(ses.c, tickets0), tickets0, nblocks);
     return;
   }
   __shared__ uint64_t s_done[2];
   if (kh::aligned16(X) && kh::aligned16(Y) && (n & 3) == 0)
-    scan_tiles<true>(X, Y, ses, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off, s_done, bdx);
+    scan_tiles<true>(X, Y, ses, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off, s_done, bdx,
+                     tickets0);
   else
-    scan_tiles<false>(X, Y, ses, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off, s_done, bdx);
+    scan_tiles<false>(X, Y, ses, n, first, second, single, s_raw, s_wave_total, &s_prefix, s_off, s_done, bdx,
+                      tickets0);
   // s_done was written before the last barrier B; the nonce is in thread 0's
   // registers.
   if (!single && tid == 0)

@@ -260,8 +260,8 @@ def test_kernarg_segment_is_2n_plus_3_slots(name, nslots):
     ("fused_gelu", "rows=4096,cols=1024", (1024, 1, 1), (256, 1, 1)),
     ("softmax", "rows=4096,cols=1024", (1024, 1, 1), (256, 1, 1)),
     ("layernorm", "rows=4097,cols=1024", (1025, 1, 1), (256, 1, 1)),
-    ("scan", "n=1000000", (89, 1, 1), (768, 1, 1)),       # up to 2^21 elements: 768 threads
-    ("scan", "n=2097153", (137, 1, 1), (1024, 1, 1)),
+    ("scan", "n=1000000", (89, 1, 1), (768, 1, 1)),       # up to 1.5 * 2^20 elements: 768 threads
+    ("scan", "n=1572865", (103, 1, 1), (1024, 1, 1)),
     ("scan", "n=67108864", (4370, 1, 1), (1024, 1, 1)),
     # gemm: the grid is the chosen symbol's tile count (rate x last-round fill).
     # gemm (128x256) is persistent: two workgroups per CU loop over its tiles.
