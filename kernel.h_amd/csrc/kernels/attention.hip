@@ -208,8 +208,16 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
   // log2(e)/sqrt(d): S^T comes out in log2 units, so exp(S - m) = 2^(S' - m').
   const float qscale = kh::kLog2e * 0.125f;
 
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(Kg), (short)0,
+                                                                      (int)(seq * ks * 4), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(Vg), (short)0,
+                                                                      (int)(seq * vs * 4), 0x00020000);
   for (int64_t qt = blockIdx.x; qt < nqt; qt += nblocks) {
     const int64_t q_row = qt * rows_per_block + (int64_t)wave * QW + r;
+    // The fast path's K0 goes out before Q: its copy into LDS waits for K0
+    // alone, and tile 0's S^T then takes Q's fragments as they land.
+    float4 kr[4], vr[4];
+    if (fast) load_k(kr, rk, ks, 0, tid);
     float4 q[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
@@ -229,11 +237,6 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
       // MFMAs. Buffer j % 2 of Ks holds K of tile j, of Vt V of tile j. The
       // loop covers the tiles that have a successor (all full); the last
       // tile, the only one that can be partial, is finished after it.
-      const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(Kg), (short)0,
-                                                                          (int)(seq * ks * 4), 0x00020000);
-      const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(Vg), (short)0,
-                                                                          (int)(seq * vs * 4), 0x00020000);
-      float4 kr[4], vr[4];
       v16f sa[2], sb[2];
       {
         // K0, V0 and K1 go out together (one memory latency before the
@@ -241,7 +244,6 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
         // 0's S^T (loads complete in issue order; the barrier fences LDS
         // only): V0 and K1 keep arriving under those MFMAs.
         float4 k1[4];
-        load_k(kr, rk, ks, 0, tid);
         load_v(vr, rv, vs, 0, tid);
         load_k(k1, rk, ks, TK, tid);
         store_k(kr, Ks, tid);
@@ -275,7 +277,11 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
         sa[0] = sb[0];
         sa[1] = sb[1];
       }
-      softmax_pv<true>(o, m, l, sa, Vt + (t & 1) * D * LDV, t * TK, seq, lane);
+      // The last tile is the only one that can be partial.
+      if (seq % TK == 0)
+        softmax_pv<false>(o, m, l, sa, Vt + (t & 1) * D * LDV, t * TK, seq, lane);
+      else
+        softmax_pv<true>(o, m, l, sa, Vt + (t & 1) * D * LDV, t * TK, seq, lane);
     } else {
       for (int64_t t = 0; t < ntiles; ++t) {
         stage_kv_generic(Ks, Vt, Kg, Vg, ks, vs, t * TK, seq, bd);
