@@ -249,10 +249,12 @@ __device__ __forceinline__ Opened open_session(Header *h, Counters *c, int64_t n
   o.base = ld(&h->base);
   o.nonce = ld(&h->nonce);
   const uint64_t seen0 = ld(&h->check);
-  o.t0 = fetch_add(&c->counter, 1u);
-  // Without a pair, t1 stands for "no second tile": t0 itself in the checks
-  // below, and the caller ignores it.
-  o.t1 = pair ? fetch_add(&c->counter, 1u) : o.t0;
+  // A pair is two consecutive tickets from one atomic: the workgroups'
+  // start-up atomics on the counter serialise, one per workgroup instead of
+  // two. Without a pair, t1 stands for "no second tile": t0 itself in the
+  // checks below, and the caller ignores it.
+  o.t0 = fetch_add(&c->counter, pair ? 2u : 1u);
+  o.t1 = o.t0 + (pair ? 1u : 0u);
   // A call takes every ticket below ntiles once and at most two more per
   // workgroup, all >= base: a ticket outside that range means the counter
   // was changed behind the header's back (another kernel wrote it), and the
@@ -304,8 +306,8 @@ __device__ __forceinline__ Opened open_session(Header *h, Counters *c, int64_t n
   }
   // Tickets taken before the session began are not tiles of this call.
   if ((int32_t)(o.t1 - first_ticket(o.base)) < 0) {
-    o.t0 = fetch_add(&c->counter, 1u);
-    o.t1 = pair ? fetch_add(&c->counter, 1u) : o.t0;
+    o.t0 = fetch_add(&c->counter, pair ? 2u : 1u);
+    o.t1 = o.t0 + (pair ? 1u : 0u);
   } else if ((int32_t)(o.t0 - first_ticket(o.base)) < 0) {
     o.t0 = o.t1;
     o.t1 = fetch_add(&c->counter, 1u);
