@@ -52,9 +52,9 @@ METRIC = "GEMM-8192 fp32 TFLOPS + softmax/scan HBM GB/s, % of MI355X roofline"
 # profiles/templates_baseline_sizes_hbm_traffic.md. Constants of that profile
 # (median dispatch), not measured by the run that reports them.
 PMC_TRAFFIC_BYTES = {
-    "vecadd": 201380288, "softmax": 33662144, "layernorm": 33724800, "scan": 539275680, "scan_1e6": 8271712,
-    "fused_gelu": 536954112, "fused_gelu_2^22": 33636160, "gemm": 3786829184, "gemm_8192x8192x256": 378662656,
-    "gemm_2048": 117560576, "gemm_512": 10650624, "attention": 1208261888, "attention_s1024": 302283648,
+    "vecadd": 201380160, "softmax": 33662464, "layernorm": 33725184, "scan": 539207872, "scan_1e6": 8272864,
+    "fused_gelu": 536954176, "fused_gelu_2^22": 33636480, "gemm": 3814877312, "gemm_8192x8192x256": 380331648,
+    "gemm_2048": 117560832, "gemm_512": 10650624, "attention": 1208263040, "attention_s1024": 302283392,
 }
 PMC_TRAFFIC_SOURCE = "profiles/templates_baseline_sizes_hbm_traffic.md (constant, not measured by this run)"
 
