@@ -19,7 +19,10 @@
 //     any grid size).
 //   * Workgroups are persistent and pipelined: the data waves issue the next
 //     tile's loads before the current tile's look-back, and tickets run two
-//     ahead, so load, ticket and look-back latencies overlap.
+//     ahead (when tiles outnumber workgroups; one tile per workgroup
+//     otherwise), so load, ticket and look-back latencies overlap. Control
+//     and data waves run loops of their own, so that each waits only for
+//     its own memory operations.
 //   * Partial sums are carried in fp64. Every fp32 input is exact in fp64
 //     and, for inputs on a common 2^-e grid whose total needs <= 53 bits
 //     (every configuration the reference tests: U[0,1) on 2^-24 or
