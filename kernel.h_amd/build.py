@@ -59,6 +59,10 @@ PRODUCT = ["vecadd", "fused_gelu", "softmax", "layernorm", "scan", "gemm", "atte
 #     and over the reference-side Backend binding.
 TDIR = os.path.join(REPO, "tests")
 PROBES = ["mfma_probe"]
+#   csrc/kernels/<base>.hip with test-only defines -> co/<name>.hsaco, also
+#     loaded by tests only: scan with a short bounded wait, so that a test can
+#     make its give-up paths run (every kernel still exits normally).
+TEST_VARIANTS = {"scan_shortspin": ("scan", ["-DKH_SCAN_SPIN_LIMIT=2048"])}
 CPP_CHECKS = {
     "khrt_raii_check": ["cpp/raii_check.cpp"],
     "khrt_backend_check": ["cpp/backend_check.cpp", "../kernel.h_amd/integration/backend_khrt.cpp"],
@@ -102,7 +106,7 @@ def run(cmd, verbose=False, **kw):
 
 
 def compile_co(name: str, verbose: bool, srcdir: str = "") -> str:
-    base, defs = VARIANTS.get(name, (name, []))
+    base, defs = VARIANTS.get(name) or TEST_VARIANTS.get(name) or (name, [])
     src = os.path.join(srcdir or KDIR, base + ".hip")
     out = os.path.join(CO, name + ".hsaco")
     run([HIPCC, *DEVICE_FLAGS, *EXTRA_DEVICE_FLAGS.get(base, []), *defs, "-c", src, "-o", out], verbose)
@@ -189,6 +193,7 @@ def build(jobs: int = 8, verbose: bool = False) -> None:
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         outs = dict(zip(srcs, ex.map(lambda n: compile_co(n, verbose), srcs)))
         list(ex.map(lambda n: compile_co(n, verbose, fixture_dir), probes))
+        list(ex.map(lambda n: compile_co(n, verbose), TEST_VARIANTS))
         cli_outs = dict(zip(cli_cos, ex.map(lambda n: compile_co(n, verbose, cli_dirs[n]), cli_cos)))
     present = {n: p for n, p in outs.items() if n in PRODUCT}
 

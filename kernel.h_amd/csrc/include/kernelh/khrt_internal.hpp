@@ -52,8 +52,9 @@ std::string check_elf_image(const unsigned char *b, size_t size);
 
 // Per-device set-up of the allocation-free scan entry point (its state
 // array's address, the scan function, a verified launch shape); run by
-// khrt_init_device with the device current.
-int noalloc_setup(int device);
+// khrt_init_device with the device current. Never fails the caller: a
+// failure is kept per device and returned by kh_scan_noalloc there.
+void noalloc_setup(int device);
 
 // Drops the cached occupancy answers and kernel workgroup-size bounds
 // (called when a module is unloaded: a later module's functions can reuse

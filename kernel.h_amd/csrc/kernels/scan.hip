@@ -88,9 +88,19 @@
 // floats always suffice (a tile is at least 3072 elements, 48 B of T).
 // Anything else is refused by writing NaN to y without touching the totals.
 //
-// Every wait is bounded: after kSpinLimit polls a tile gives up, poisons its
-// result with NaN and counts the failure in the header, so a corrupted
-// state can never hang the device.
+// Every wait is bounded (KH_SCAN_SPIN_LIMIT polls), so a corrupted state can
+// never hang the device:
+//   * a look-back that runs out poisons its tile's result (and so every
+//     later tile's) with NaN and counts the failure in the header; the call
+//     still closes, so the next call runs under a new generation;
+//   * a claim left unsigned for the limit (a header that held a claim mark
+//     when the call began) is taken over by one of the waiting workgroups,
+//     so such a header costs one wait and no failure;
+//   * a workgroup whose claims keep stalling (8 limits in all, which needs
+//     claimant waves stalled for seconds) counts the failure and writes NaN
+//     to its share of y.
+// After a call, failed > 0 means y is not to be trusted (NaN, or left as it
+// was where a lost ticket's tile was never reached).
 #include "kh_device.h"
 #include "kh_tiles.h"
 
@@ -103,7 +113,12 @@ constexpr int kPerThread = KH_SCAN_PER_THREAD;
 #define KH_SCAN_WINDOW 2
 #endif
 constexpr int kWindow = KH_SCAN_WINDOW;  // predecessors polled per lane per look-back step
-constexpr uint32_t kSpinLimit = 1u << 22;
+// Polls before a bounded wait gives up (about 1-2 us each: seconds in all).
+// A test build sets a small limit to exercise the give-up paths.
+#ifndef KH_SCAN_SPIN_LIMIT
+#define KH_SCAN_SPIN_LIMIT (1u << 22)
+#endif
+constexpr uint32_t kSpinLimit = KH_SCAN_SPIN_LIMIT;
 constexpr uint64_t kEmpty = ~0ull;
 
 // The header proper, read by every workgroup at its start, and the two
@@ -153,11 +168,13 @@ __device__ __forceinline__ uint64_t header_check(const Header *h, uint64_t base,
   return nonzero(mix64(session_key(h, nonce) ^ mix64(base ^ 0x0c0ffee0ddba11ull)));
 }
 
-// Never a header's check word (only by a random 64-bit coincidence): marks a
-// header being claimed.
+// Claim marks: the check word of a header being claimed, 256 values that
+// differ only in their low byte (the claim's epoch). Never a header's check
+// word but by a random coincidence (2^-56).
 __device__ __forceinline__ uint64_t claim_mark(const Header *h) {
-  return nonzero(mix64(reinterpret_cast<uintptr_t>(h) ^ 0xc1a1bedc1a1bedull));
+  return mix64(reinterpret_cast<uintptr_t>(h) ^ 0xc1a1bedc1a1bedull) & ~0xffull;
 }
+__device__ __forceinline__ bool is_claim_mark(const Header *h, uint64_t v) { return (v & ~0xffull) == claim_mark(h); }
 
 // Record tags of tile i of the call with generation g: a session key XOR
 // t = (g << 32) | i, one key per kind of value. A record holds the tile's
@@ -246,6 +263,19 @@ struct Opened {
   bool ok;
 };
 
+// Takes the workgroup's starting tickets again (one atomic), keeping a
+// second ticket already at or past the session's first: the tickets taken
+// before a session began are not tiles of its call.
+__device__ __forceinline__ void retake_tickets(Opened &o, Counters *c, bool pair) {
+  if ((int32_t)(o.t1 - first_ticket(o.base)) < 0) {
+    o.t0 = fetch_add(&c->counter, pair ? 2u : 1u);
+    o.t1 = o.t0 + (pair ? 1u : 0u);
+  } else if ((int32_t)(o.t0 - first_ticket(o.base)) < 0) {
+    o.t0 = o.t1;
+    o.t1 = fetch_add(&c->counter, 1u);
+  }
+}
+
 __device__ __forceinline__ Opened open_session(Header *h, Counters *c, int64_t ntiles, uint64_t nblocks, bool pair) {
   Opened o;
   o.ok = true;
@@ -263,58 +293,84 @@ __device__ __forceinline__ Opened open_session(Header *h, Counters *c, int64_t n
   // was changed behind the header's back (another kernel wrote it), and the
   // header is not taken as valid even though its check matches.
   const uint64_t span = (uint64_t)ntiles + 2ull * nblocks + 4;
-  const bool signed0 = seen0 == header_check(h, o.base, o.nonce);
-  const bool in_range = (uint32_t)(o.t1 - first_ticket(o.base)) < span;
+  auto in_range = [&]() { return (uint32_t)(o.t1 - first_ticket(o.base)) < span; };
+  bool signed0 = seen0 == header_check(h, o.base, o.nonce);
   // Valid: the header is stable for the whole call (only the last workgroup
   // to finish changes it), so the three words belong together.
-  if (signed0 && in_range) return o;
+  if (signed0 && in_range()) return o;
+  if (signed0 && (int32_t)(o.t1 - first_ticket(o.base)) < 0) {
+    // Signed, but the tickets precede the session's first ticket. The header
+    // loads and the ticket atomic are relaxed and complete in either order,
+    // so this is what a workgroup sees when another workgroup of this call
+    // claimed the header after this one's atomic and signed it before its
+    // loads: the session is open and only the tickets predate it. Take them
+    // again; the acquire fence orders everything that follows after the
+    // claimant's writes (the signature read above is its release store).
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    retake_tickets(o, c, pair);
+    if (in_range()) return o;
+    // Still outside: the counter itself was moved back. Claim afresh.
+  }
   // Not recognised (or read while a claimant was writing it). `check` is
   // read with acquire ordering before base and nonce: when it is a
   // claimant's signature, the base and nonce read after it are the ones it
   // signs. A workgroup claims the header only from a check value that is
   // unsigned (or the signature found with an inconsistent counter), with a
-  // compare-and-swap, so exactly one claims it; the others wait for the new
-  // signature.
+  // compare-and-swap that writes a claim mark, so exactly one claims it; the
+  // others wait for the new signature.
+  //
+  // A claim mark that stays unsigned for kSpinLimit polls (a header that
+  // held a mark when the call began: a claim cut short, or a coincidence) is
+  // claimed in turn, under the next epoch's mark, by one of the waiting
+  // workgroups; every wait counts its polls from the last change of the
+  // check word. (A claimant that is alive signs within microseconds: one
+  // thread, a handful of stores. Only a claimant wave stalled for seconds
+  // could sign after its claim was taken over.)
   const uint64_t mark = claim_mark(h);
-  for (uint32_t spins = 0;; ++spins) {
+  uint64_t last = 0;
+  uint32_t spins = 0;
+  for (uint32_t polls = 0;; ++polls) {
     const uint64_t seen = __hip_atomic_load(&h->check, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
     o.base = ld(&h->base);
     o.nonce = ld(&h->nonce);
     if (seen == header_check(h, o.base, o.nonce) && !(signed0 && seen == seen0)) break;
-    uint64_t expect = seen;
-    if (seen != mark && __hip_atomic_compare_exchange_strong(&h->check, &expect, mark, __ATOMIC_RELAXED,
-                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-      // A read-modify-write, so every ticket before it precedes the
-      // session's first ticket and every ticket after it follows. The
-      // generation may start anywhere: the session key carries the nonce.
-      o.nonce = __builtin_amdgcn_s_memrealtime();
-      o.base = ((uint64_t)(uint32_t)o.nonce << 32) | fetch_add(&c->counter, 0u);
-      st(&h->base, o.base);
-      st(&h->nonce, o.nonce);
-      st(&c->done, uint64_t(0));
-      st(&h->failed, 0u);
-      __hip_atomic_store(&h->check, header_check(h, o.base, o.nonce), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-      break;
+    if (seen != last) {
+      last = seen;
+      spins = 0;
     }
-    if (spins > kSpinLimit) {
-      // The claimant never signed (or the header held the claim mark by
-      // chance): drop the mark so that the next call claims it afresh.
-      uint64_t m = mark;
-      __hip_atomic_compare_exchange_strong(&h->check, &m, uint64_t(0), __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
+    const bool claimed = is_claim_mark(h, seen);
+    if (!claimed || spins > kSpinLimit) {
+      uint64_t expect = seen;
+      const uint64_t mine = claimed ? mark | ((seen + 1) & 0xff) : mark;
+      if (__hip_atomic_compare_exchange_strong(&h->check, &expect, mine, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT)) {
+        // A read-modify-write, so every ticket before it precedes the
+        // session's first ticket and every ticket after it follows. The
+        // generation may start anywhere: the session key carries the nonce.
+        o.nonce = __builtin_amdgcn_s_memrealtime();
+        o.base = ((uint64_t)(uint32_t)o.nonce << 32) | fetch_add(&c->counter, 0u);
+        st(&h->base, o.base);
+        st(&h->nonce, o.nonce);
+        st(&c->done, uint64_t(0));
+        st(&h->failed, 0u);
+        __hip_atomic_store(&h->check, header_check(h, o.base, o.nonce), __ATOMIC_RELEASE,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      continue;  // another workgroup changed the word first: read it again
+    }
+    if (polls > 8 * kSpinLimit) {
+      // Claims kept stalling: give up. The workgroup's tickets are lost
+      // and the call's last workgroup never counts itself done, so the
+      // header is not re-signed by this call.
+      fetch_add(&h->failed, 1u);
       o.ok = false;
       return o;
     }
+    ++spins;
     __builtin_amdgcn_s_sleep(2);
   }
-  // Tickets taken before the session began are not tiles of this call.
-  if ((int32_t)(o.t1 - first_ticket(o.base)) < 0) {
-    o.t0 = fetch_add(&c->counter, pair ? 2u : 1u);
-    o.t1 = o.t0 + (pair ? 1u : 0u);
-  } else if ((int32_t)(o.t0 - first_ticket(o.base)) < 0) {
-    o.t0 = o.t1;
-    o.t1 = fetch_add(&c->counter, 1u);
-  }
+  retake_tickets(o, c, pair);
   return o;
 }
 

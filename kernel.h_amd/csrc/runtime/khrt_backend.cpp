@@ -181,7 +181,9 @@ int khrt_init_device(int ordinal) {
   e = hipSetDevice(ordinal);
   if (e != hipSuccess) return fail_hip(e, "hipSetDevice");
   g_device = ordinal;
-  return noalloc_setup(ordinal);
+  // Optional: a failure here is kept for kh_scan_noalloc and fails nothing else.
+  noalloc_setup(ordinal);
+  return 0;
 }
 
 int khrt_get_device_info(khrt_device_info *out) {

@@ -10,9 +10,11 @@
 // Set-up happens once per device, in khrt_init_device (with that device
 // current): the array's device address is taken with hipGetSymbolAddress
 // and kept per device, the scan code object is loaded, and the launch shape
-// is verified. The entry point itself then only packs its parameters on the
-// stack and launches; it calls no allocating routine, and refuses a device
-// that was not set up that way.
+// is verified. A set-up failure does not fail khrt_init_device (the other
+// entry points do not need it): it is kept per device and returned by every
+// kh_scan_noalloc call on that device. The entry point itself only packs its
+// parameters on the stack and launches; it calls no allocating routine, and
+// refuses a device that was not set up.
 //
 // The scan's state is self-validating (a signed header and tagged records;
 // see the scan kernel), so the zero-filled array needs no clearing before
@@ -47,6 +49,9 @@ constexpr int kMaxDevices = 64;
 
 struct DeviceState {
   bool ready = false;
+  bool tried = false;        // set-up ran (successfully or not)
+  int error_code = 0;        // its failure, returned by every call
+  std::string error;
   float *ptr = nullptr;     // device address of this device's `scratch`
   void *function = nullptr;  // `scan` in this device's module
   int64_t resident = 0;      // workgroups of KH_SCAN_THREADS resident at once
@@ -61,13 +66,9 @@ int bad(const std::string &what) { return khrt::fail(KHRT_E_INVALID, "kh_scan_no
 
 namespace khrt {
 
-int noalloc_setup(int device) {
-  if (device < 0 || device >= kMaxDevices) return 0;  // such devices are refused at call time
-  {
-    std::lock_guard<std::mutex> lock(g_mu);
-    if (g_state[device].ready) return 0;
-  }
-  DeviceState s;
+namespace {
+
+int setup(int device, DeviceState &s) {
   const hipError_t e = hipGetSymbolAddress(reinterpret_cast<void **>(&s.ptr), HIP_SYMBOL(scratch));
   if (e != hipSuccess) return fail_hip(e, "hipGetSymbolAddress(scratch)");
   if (int rc = khrt_template_function("scan", &s.function)) return rc;
@@ -90,9 +91,27 @@ int noalloc_setup(int device) {
     return fail(KHRT_E_REFUSED, std::string("kh_scan_noalloc set-up: scan launch refused: ") + diag);
   }
   s.ready = true;
+  return 0;
+}
+
+}  // namespace
+
+void noalloc_setup(int device) {
+  if (device < 0 || device >= kMaxDevices) return;  // such devices are refused at call time
+  {
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (g_state[device].tried) return;
+  }
+  DeviceState s;
+  s.tried = true;
+  if (int rc = setup(device, s)) {
+    s.ready = false;
+    s.error_code = rc;
+    s.error = khrt_last_error();
+    clear_error();
+  }
   std::lock_guard<std::mutex> lock(g_mu);
   g_state[device] = s;
-  return 0;
 }
 
 }  // namespace khrt
@@ -111,6 +130,8 @@ extern "C" int kh_scan_noalloc(const float *x, float *y, int64_t n, void *stream
     if (device >= 0 && device < kMaxDevices) s = g_state[device];
   }
   if (!s.ready) {
+    if (s.tried) return khrt::fail(s.error_code, "kh_scan_noalloc: set-up on device " + std::to_string(device) +
+                                                     " failed: " + s.error);
     return bad("device " + std::to_string(device) +
                " is not set up: call khrt_init_device on it first (the entry point does no set-up of its own)");
   }

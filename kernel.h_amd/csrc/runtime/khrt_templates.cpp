@@ -694,8 +694,10 @@ int kh_layernorm(const float *x, const float *gamma, const float *beta, float *y
 int kh_scan(const float *x, float *y, float *y_lo, float *totals_hi, float *totals_lo, int64_t n, void *stream) {
   if (n <= 0) return bad("scan: n must be positive");
   if (!x || !y || !totals_hi || !totals_lo) return bad("scan: null buffer");
-  // The look-back state (a 40-byte header in totals_lo, 24 B per tile in
-  // totals_hi) always fits the reference's T = ceil(n/256) floats of each;
+  // The look-back state (in totals_lo a 32-byte header and 16 bytes of
+  // ticket counters, 256 B past it when there is room; in totals_hi 16 B
+  // per tile but the last) always fits the reference's T = ceil(n/256)
+  // floats of each;
   // the kernel establishes it on first use and keeps it valid across calls.
   const int64_t T = ceil_div(n, 256);
   khrt::LaunchArgs args;

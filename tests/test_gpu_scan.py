@@ -11,6 +11,8 @@ through `khrt_launch_raw`: no verification, nothing launched before the
 kernel, totals buffers as the caller left them (never written, zero-filled,
 NaN-filled, or left by an earlier call or by the reference's own protocol).
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -179,7 +181,7 @@ def test_scan_refuses_without_touching_totals(dev, short):
     if short == "totals_hi":
         t_hi = 200
     elif short == "totals_lo":
-        t_lo = 9  # 36 B: the 40-byte header does not fit
+        t_lo = 9  # 36 B: the 32-byte header and 16 B of counters (48 B) do not fit
     else:
         block = 128
     f = kh.GpuModule(kh.code_object("scan")).get_function("scan")
@@ -263,3 +265,100 @@ def test_scan_off_grid_inputs_within_derived_bound(dev, kind):
         f"{int(np.sum(emu != r))} for the template emulator, {int(np.sum(got != emu))} GPU vs emulator; "
         f"worst err/tol {err[worst] / tol[worst]:.3g} at {worst}")
     assert np.all(err <= tol), f"element {worst}: |y - r| = {err[worst]:.3e} > {tol[worst]:.3e}"
+
+
+# The look-back state's layout and hashes, restated on the host so that a
+# test can forge states the kernel must survive (scan.hip: Header, Counters,
+# mix64, header_check, claim_mark). totals_lo holds, from its first 8-byte
+# boundary, base (u64: generation << 32 | first ticket), nonce (u64), check
+# (u64), failed (u32), pad; the ticket counter (u32), pad and done (u64) sit
+# 256 B further on when totals_lo has room.
+_M64 = (1 << 64) - 1
+
+
+def _mix64(z):
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & _M64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & _M64
+    return z ^ (z >> 31)
+
+
+def _header_check(h, base, nonce):
+    key = _mix64(h ^ _mix64(nonce ^ 0x5CA11AB1E5CA4A11))
+    return _mix64(key ^ _mix64(base ^ 0x0C0FFEE0DDBA11)) or 1
+
+
+def _claim_mark(h):
+    return _mix64(h ^ 0xC1A1BEDC1A1BED) & ~0xFF & _M64
+
+
+def _forge_totals_lo(buf, T, base, nonce, check, counter, failed=0, done=0):
+    assert buf.ptr % 8 == 0 and 4 * T >= 256 + 16
+    w = np.zeros(T, np.uint32)
+    w64 = w[:8].view(np.uint64)
+    w64[0], w64[1], w64[2] = base, nonce, check
+    w[6] = failed
+    w[64] = counter
+    w[66:68].view(np.uint64)[0] = done
+    buf.copy_from_host(w)
+
+
+def _failed(buf):
+    return int(buf.to_host(np.uint32, 8)[6])
+
+
+def _shortspin_scan():
+    with open(os.path.join(kh.CO_DIR, "scan_shortspin.hsaco"), "rb") as f:
+        m = kh.GpuModule(f.read())
+    return m, m.get_function("scan")
+
+
+def test_scan_lookback_gives_up_on_a_missing_record(dev):
+    """A signed header whose counter skips tile 0's ticket: tile 0 is never
+    handed out, so tile 1's look-back waits for a record that never comes.
+    With the test build's short bounded wait it gives up: every later tile
+    is NaN, tile 0's elements are untouched, the header counts the failure,
+    every workgroup exits, and the call still closes, so the next call on
+    the same buffers (the product code object) is bit-exact."""
+    n = 10 ** 6
+    T = kh.scan_workspace_floats(n)
+    tile = 15 * 64 * 16  # 1024-thread workgroups: 15 data waves x 64 lanes x 16
+    ntiles = (n + tile - 1) // tile
+    x = O.uniform(n, 0x6173, 0.0, 1.0)
+    ref = np.cumsum(x.astype(np.float64)).astype(np.float32)
+    dx, th, tl = up(x), empty(T, 0.0), empty(T, 0.0)
+    first = 5000
+    base, nonce = (7 << 32) | first, 0x123456789ABC
+    _forge_totals_lo(tl, T, base, nonce, _header_check(tl.ptr, base, nonce), counter=first + 1)
+    _m, f = _shortspin_scan()
+    dy = empty(n, 0.25)
+    say(f"scan short-spin look-back give-up n={n} grid={ntiles}x1024")
+    kh.launch_raw(f, (ntiles, 1, 1), (1024, 1, 1), _scan_args(dx, dy, empty(1, None), th, tl, n, T))
+    got = down(dy, n)
+    assert np.all(got[:tile] == 0.25)
+    assert np.all(np.isnan(got[tile:]))
+    assert _failed(tl) >= 1
+    g = kh.GpuModule(kh.code_object("scan")).get_function("scan")
+    dy = empty(n)
+    say("scan after a give-up: same buffers, product code object")
+    kh.launch_raw(g, (ntiles, 1, 1), (1024, 1, 1), _scan_args(dx, dy, empty(1, None), th, tl, n, T))
+    assert np.array_equal(down(dy, n), ref)
+
+
+def test_scan_takes_over_a_stale_claim(dev):
+    """A header that holds a claim mark when the call begins (a claim that
+    never signs): after the bounded wait one workgroup takes the claim over
+    under the next epoch's mark, so the call is bit-exact with no failure
+    counted, and so is the next one."""
+    n = 10 ** 6
+    T = kh.scan_workspace_floats(n)
+    x = O.uniform(n, 0x6174, 0.0, 1.0)
+    ref = np.cumsum(x.astype(np.float64)).astype(np.float32)
+    dx, th, tl = up(x), empty(T, 3.0), empty(T, 0.0)
+    _forge_totals_lo(tl, T, base=12345, nonce=99, check=_claim_mark(tl.ptr) | 5, counter=777, failed=0, done=31)
+    _m, f = _shortspin_scan()
+    for call in range(2):
+        dy = empty(n)
+        say(f"scan short-spin stale claim call={call}")
+        kh.launch_raw(f, (66, 1, 1), (1024, 1, 1), _scan_args(dx, dy, empty(1, None), th, tl, n, T))
+        assert np.array_equal(down(dy, n), ref)
+        assert _failed(tl) == 0
