@@ -310,11 +310,15 @@ def _median_runs(fn, runs=3, long_s=10.0):
 def cpu_baseline(budget_s: float):
     """The oracle's fp64 references (CPU restatements of the reference's
     e2e checks) timed on this host, built for its widest x86-64 level (the
-    stand-in for -march=native). Each rate is the median of 3 runs (1 when a
-    run exceeds 10 s): the GEMM reference (e2e_gemm_test.cpp:92-110) on a row
-    sample of the 8192^3 problem on all cores via OpenMP (the headline, in
-    `value`'s unit) and on one core; the softmax reference on all cores and
-    one core; the scan prefix (serial) on one core."""
+    stand-in for -march=native), on all cores (OpenMP, the core count from
+    sched_getaffinity) and on one core. Each rate is the median of 3 runs (1
+    when a run exceeds 10 s). The headline, in `value`'s unit, is the GEMM
+    reference (e2e_gemm_test.cpp:92-110) on a row sample of the 8192^3
+    problem; `other_kernels` holds every other reference at its BASELINE
+    configuration: vecadd's fp64 sum, softmax_reference_row, layernorm's
+    reference_row, gelu_reference, the serial scan prefix (one core: it is a
+    recurrence) and attention_reference_row on a row sample of b4 h16 s4096
+    (rates of samples are extrapolated to the whole problem, so labelled)."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle as O
     isa = O.host_isa()
@@ -325,43 +329,83 @@ def cpu_baseline(budget_s: float):
     A = u24(rng, M * M, -1, 1)
     B = u24(rng, M * M, -1, 1)
 
-    def gemm_rate(threads, share):
-        # Size the row sample so that one run takes about share * budget / 3.
+    def sample_size(run, threads, target, first):
+        # Grows a sample (rows or elements) until one run takes >= 50 ms,
+        # then scales it to take about `target` seconds.
         O.set_threads(threads)
-        target = share * budget_s / 3
-        rows = max(threads, 2)
+        size = first
         while True:
             t = time.perf_counter()
-            O.ref_gemm(A, B, M, M, M, row0=0, nrows=rows)
+            run(size)
             dt = time.perf_counter() - t
-            if dt >= 0.05 or rows >= M:
+            if dt >= 0.05:
                 break
-            rows = min(M, rows * 4)
-        rows = int(min(M, max(threads, rows * target / dt)))
+            size *= 4
+        return max(first, int(size * target / dt))
+
+    def gemm_rate(threads, share):
+        rows = min(M, sample_size(lambda r: O.ref_gemm(A, B, M, M, M, row0=0, nrows=min(M, r)), threads,
+                                  share * budget_s / 3, max(threads, 2)))
         med, k = _median_runs(lambda: O.ref_gemm(A, B, M, M, M, row0=0, nrows=rows))
         return 2.0 * rows * M * M / med / 1e12, rows, med, k
 
-    tf_all, rows_all, s_all, k_all = gemm_rate(cores, 0.5)
-    tf_one, rows_one, s_one, k_one = gemm_rate(1, 0.3)
+    tf_all, rows_all, s_all, k_all = gemm_rate(cores, 0.35)
+    tf_one, rows_one, s_one, k_one = gemm_rate(1, 0.2)
     del A, B
-    x = (rng.standard_normal(4096 * 1024) * 4.0).astype(np.float32)
-    O.set_threads(cores)
-    sm_all, _ = _median_runs(lambda: O.ref_softmax(x, 4096, 1024))
-    O.set_threads(1)
-    sm_one, _ = _median_runs(lambda: O.ref_softmax(x, 4096, 1024))
+
+    def both(fn, work):
+        # fn() timed on all cores and on one: work / median seconds.
+        out = {}
+        for label, threads in (("all_cores", cores), ("single_thread", 1)):
+            O.set_threads(threads)
+            med, _ = _median_runs(fn)
+            out[label] = work / med / 1e9
+        return out
+
+    other = {}
+    n = 1 << 24
+    va, vb = u24(rng, n, -1, 1), u24(rng, n, -1, 1)
+    other["vecadd_2^24_gbps"] = both(lambda: O.ref_vecadd(va, vb), 12.0 * n)
+    del va, vb
+    R, C = 4096, 1024
+    x = normal(rng, R * C, 4.0)
+    other["softmax_4096x1024_gbps"] = both(lambda: O.ref_softmax(x, R, C), 8.0 * R * C)
+    g, bt = u24(rng, C, 0.5, 1.5), u24(rng, C, -0.1, 0.1)
+    other["layernorm_4096x1024_gbps"] = both(lambda: O.ref_layernorm(x, g, bt, R, C), 8.0 * R * C + 8.0 * C)
+    ng = 1 << 22
+    xg = normal(rng, ng, 1.0)
+    other["fused_gelu_2^22_gbps"] = both(lambda: O.ref_gelu(xg), 8.0 * ng)
     xs = u24(rng, 1 << 26, 0, 1)
+    O.set_threads(1)
     sc_one, _ = _median_runs(lambda: O.ref_scan(xs))
+    other["scan_2^26_gbps_single_thread"] = 8.0 * xs.size / sc_one / 1e9
+    del xs
+    # attention b4 h16 s4096 d64: a sample of query rows spread over the 64
+    # slices; rate = 4 s d FLOP per row (4 b h s^2 d over b h s rows).
+    b, h, s_, d = 4, 16, 4096, 64
+    Q, K, V = (normal(rng, b * h * s_ * d, 1.0) for _ in range(3))
+    att = {}
+    for label, threads, share in (("all_cores", cores, 0.06), ("single_thread", 1, 0.04)):
+        def rows_run(r):
+            idx = np.arange(r, dtype=np.int64) * 7919 % (b * h * s_)
+            O.ref_attention_rows(Q, K, V, s_, d, idx // s_, idx % s_)
+        rows = min(b * h * s_, sample_size(rows_run, threads, share * budget_s / 3, max(threads, 4)))
+        med, _ = _median_runs(lambda: rows_run(rows))
+        att[label] = 4.0 * s_ * d * rows / med / 1e12
+        att[label + "_rows"] = rows
+    other["attention_b4h16s4096_tflops_extrapolated"] = att
+    del Q, K, V
+    other["note"] = ("fp64 references, same input distributions as the GPU rows; GB/s counts the kernel's "
+                     "algorithmic bytes (fused_gelu 8 B per element: tmp is dead); the scan prefix is serial; "
+                     "medians of 3 runs; attention on a row sample, extrapolated")
     O.set_threads(cores)
     return {"value": tf_all, "unit": "TFLOP/s", "cores": cores, "kind": "port",
             "sample": f"fp64 rank-1 GEMM reference (oracle kho_ref_gemm, built for {isa}): rows 0..{rows_all} of "
-                      f"the 8192^3 problem on {cores} threads, median of {k_all} runs of {s_all:.2f} s",
+                      f"the 8192^3 problem on {cores} threads, median of {k_all} runs of {s_all:.2f} s, "
+                      "extrapolated to the whole problem",
             "single_thread": {"value": tf_one, "unit": "TFLOP/s", "cores": 1,
                               "sample": f"{rows_one} rows, median of {k_one} runs of {s_one:.2f} s"},
-            "other_kernels": {"softmax_4096x1024_gbps": {"all_cores": 8.0 * x.size / sm_all / 1e9,
-                                                         "single_thread": 8.0 * x.size / sm_one / 1e9},
-                              "scan_2^26_gbps_single_thread": 8.0 * xs.size / sc_one / 1e9,
-                              "note": "fp64 references, same input distributions as the GPU rows; the scan "
-                                      "prefix is serial; medians of 3 runs"},
+            "other_kernels": other,
             "isa": isa}
 
 

@@ -357,6 +357,21 @@ KHRT_API int kh_roofline_copy(const float *src, float *dst, int64_t n, void *str
  * blocks * 4 * iters * 8 * 4096. out needs blocks * 256 floats. */
 KHRT_API int kh_roofline_mfma(float *out, int64_t blocks, int64_t iters, void *stream);
 
+/* ---- 7. Bench metrics (bench/harness/metrics.cpp:5-52) ------------------ */
+/* One of the reference's metric formulas by name, with its arguments in
+ * order: gflops_from_ms and gbps_from_ms (work, ms); gemm_flops and
+ * gemm_bytes (m, n, k); elementwise_bytes and layernorm_bytes (rows, cols);
+ * scan_bytes, fused_gelu_bytes and roofline_triad_bytes (n);
+ * attention_flops (batch, heads, seq, head_dim); roofline_fma_flops (fmas).
+ * KHRT_E_INVALID for an unknown name or a wrong argument count. */
+KHRT_API int khrt_bench_metric(const char *formula, const double *args, int nargs, double *out);
+/* The work of one `kernelh bench` row by those formulas: bytes (*is_flops =
+ * 0) or FLOPs (1) per launch of `kernel` (vecadd, fused_gelu, softmax,
+ * layernorm, scan, gemm, attention, roofline_triad) at `shape`. vecadd
+ * counts as the triad (three streams of n floats). The rows' rate column is
+ * work * 1000 / ms / 1e9. */
+KHRT_API int khrt_bench_row_work(const char *kernel, const char *shape, double *work, int *is_flops);
+
 #ifdef __cplusplus
 }
 #endif

@@ -96,8 +96,7 @@ std::function<int()> raw_launcher(void *fn, khrt_dim3 grid, khrt_dim3 block, std
 
 bool prepare_hipref(const std::string &kernel, const std::string &variant,
                     const std::map<std::string, int64_t> &s, Bufs &b, std::function<int()> &launch,
-                    double &work, bool &flops, std::string &error) {
-  flops = false;
+                    std::string &error) {
   const bool vec = variant == "vec4";
   void *fn = nullptr;
   if (kernel == "softmax" || kernel == "layernorm") {
@@ -113,12 +112,10 @@ bool prepare_hipref(const std::string &kernel, const std::string &variant,
       args->add(x).add(y).add(static_cast<int>(r)).add(static_cast<int>(c));
       const int64_t block = std::min<int64_t>((std::min<int64_t>(c, 256) + 63) / 64 * 64, 256);
       launch = raw_launcher(fn, dim(r), dim(block), args);
-      work = 2.0 * r * c * 4.0;  // elementwise_bytes (metrics.cpp:25-27)
     } else {
       float *g = b.alloc(c, 1.0f), *bt = b.alloc(c, 0.0f);
       args->add(x).add(g).add(bt).add(y).add(static_cast<int>(r)).add(static_cast<int>(c));
       launch = raw_launcher(fn, dim(r), dim(256), args);
-      work = 2.0 * r * c * 4.0 + 2.0 * c * 4.0;  // layernorm_bytes (metrics.cpp:29-32)
     }
   } else if (kernel == "fused_gelu") {
     const int64_t n = get(s, "n");
@@ -131,7 +128,6 @@ bool prepare_hipref(const std::string &kernel, const std::string &variant,
     auto args = std::make_shared<RawArgs>();
     args->add(x).add(y).add(static_cast<int>(n));
     launch = raw_launcher(fn, dim((n + 255) / 256), dim(256), args);
-    work = 3.0 * n * 4.0;  // fused_gelu_bytes (metrics.cpp:36-38): counts the dead tmp
   } else if (kernel == "scan") {
     const int64_t n = get(s, "n"), t = (n + 255) / 256;
     void *fn2 = nullptr;
@@ -148,7 +144,6 @@ bool prepare_hipref(const std::string &kernel, const std::string &variant,
       if (int rc = khrt_launch_raw(fn, dim(t), dim(256), 0, nullptr, a1->params())) return rc;
       return khrt_launch_raw(fn2, dim(1), dim(256), 0, nullptr, a2->params());
     };
-    work = 2.0 * n * 4.0;  // scan_bytes (metrics.cpp:34)
   } else if (kernel == "gemm") {
     if (vec) {
       error = "gemm has no hipref-vec variant (only the naive tiled comparator)";
@@ -160,8 +155,6 @@ bool prepare_hipref(const std::string &kernel, const std::string &variant,
     auto args = std::make_shared<RawArgs>();
     args->add(A).add(B).add(C).add(static_cast<int>(m)).add(static_cast<int>(n)).add(static_cast<int>(k));
     launch = raw_launcher(fn, dim((n + 31) / 32, (m + 31) / 32), khrt_dim3{32, 8, 1}, args);
-    work = 2.0 * m * n * k;
-    flops = true;
   } else {
     error = "hipref backend has no comparator for kernel '" + kernel + "'";
     return false;
@@ -175,7 +168,7 @@ bool prepare_hipref(const std::string &kernel, const std::string &variant,
   return true;
 }
 
-bool prepare_roofline_fma(Bufs &b, std::function<int()> &launch, double &work, std::string &error) {
+bool prepare_roofline_fma(Bufs &b, std::function<int()> &launch, double &fmas, std::string &error) {
   constexpr int64_t kElems = 1 << 22;
   constexpr int kIters = 8192;
   void *fn = nullptr;
@@ -188,7 +181,7 @@ bool prepare_roofline_fma(Bufs &b, std::function<int()> &launch, double &work, s
   auto args = std::make_shared<RawArgs>();
   args->add(c).add(static_cast<int>(kElems)).add(kIters);
   launch = raw_launcher(fn, dim((kElems + 255) / 256), dim(256), args);
-  work = 2.0 * static_cast<double>(kElems) * kIters;  // roofline_fma_flops (metrics.cpp:50-52)
+  fmas = static_cast<double>(kElems) * kIters;
   return true;
 }
 
@@ -234,7 +227,7 @@ Rocblas &rocblas() {
 }  // namespace
 
 bool prepare_rocblas_gemm(const std::map<std::string, int64_t> &s, Bufs &b, std::function<int()> &launch,
-                          double &work, std::string &error) {
+                          std::string &error) {
   Rocblas &r = rocblas();
   if (!r.error.empty()) {
     error = r.error;
@@ -256,7 +249,6 @@ bool prepare_rocblas_gemm(const std::map<std::string, int64_t> &s, Bufs &b, std:
                                       static_cast<rocblas_int>(k), &zero, C, static_cast<rocblas_int>(n));
     return st == rocblas_status_success ? 0 : 1;
   };
-  work = 2.0 * m * n * k;
   return true;
 }
 
@@ -326,7 +318,7 @@ Hipblaslt &hipblaslt() {
 }  // namespace
 
 bool prepare_hipblaslt_gemm(const std::map<std::string, int64_t> &s, Bufs &b, std::function<int()> &launch,
-                            double &work, std::string &error) {
+                            std::string &error) {
   Hipblaslt &h = hipblaslt();
   if (!h.error.empty()) {
     error = h.error;
@@ -371,7 +363,6 @@ bool prepare_hipblaslt_gemm(const std::map<std::string, int64_t> &s, Bufs &b, st
                                         result->workspaceSize, nullptr);
     return st == HIPBLAS_STATUS_SUCCESS ? 0 : 1;
   };
-  work = 2.0 * m * n * k;
   return true;
 }
 

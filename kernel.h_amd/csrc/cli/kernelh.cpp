@@ -7,7 +7,10 @@
 //                                                          (main.cpp:649-1420)
 //   kernelh bench   --suite <roofline|kernelh|rocblas|hipblaslt|hipref|all> --out <path>
 //                   [--occupancy] [--kernel <name> --shape ... [--backend <b>]]
-//                                                          (main.cpp:2154-2228)
+//   kernelh bench   --occupancy --kernel <name> --target amdgcn-gfx950
+//                   [--shape ...] [--threads N] --out <dir>   (occupancy only)
+//                                                          (main.cpp:2154-2228,
+//                                                   run_bench.cpp:111-127)
 // Exit codes as in the reference (main.cpp:125-127, run_bench.hpp:9-10):
 // 0 ok, 1 operational failure, 2 usage error, 77 skipped (no GPU).
 //
@@ -29,7 +32,9 @@
 // (bench/harness/csv.cpp:9-10).
 #include "khrt.h"
 
+#include "args.hpp"
 #include "comparators.hpp"
+#include "kernelh/shape_text.hpp"
 #include "tune.hpp"
 
 #include <algorithm>
@@ -69,8 +74,9 @@ void usage(std::ostream &os) {
      << "  --out <dir>           write <dir>/<kernel>.{hsaco,isa} (created if missing)\n"
      << "  --resources           also write <dir>/resources.json\n\n"
      << "tune options (GEMM only): kernelh tune --help\n"
-     << "  --shape m=..,n=..,k=.. --out <dir> [--max-candidates n] [--timeout s]\n"
-     << "  [--cache path]; writes <dir>/tune-results.csv, prints the best config\n\n"
+     << "  --shape m=..,n=..,k=.. --out <dir> [--max-candidates n] [--sample n]\n"
+     << "  [--refine-budget n] [--timeout s] [--cache path]; writes <dir>/tune-results.csv,\n"
+     << "  prints the best config\n\n"
      << "bench options:\n"
      << "  --suite <name>        roofline, kernelh, rocblas, hipblaslt, hipref, all (default: all)\n"
      << "  --backend <name>      with --kernel: kernelh (default), rocblas, hipblaslt,\n"
@@ -80,45 +86,15 @@ void usage(std::ostream &os) {
      << "  --out <path>          results.csv path or directory (required)\n"
      << "  --warmup <n>          warmup launches (default 5)\n"
      << "  --iters <n>           timed launches, median reported (default 20)\n"
-     << "  --occupancy           write occupancy.{json,md} next to results.csv\n\n"
+     << "  --occupancy           write occupancy.{json,md} next to results.csv\n"
+     << "occupancy-only mode (times nothing, needs no device):\n"
+     << "  kernelh bench --occupancy --kernel <name> --target amdgcn-gfx950\n"
+     << "                [--shape k=v,...] [--threads N] --out <dir>\n"
+     << "  writes <dir>/occupancy.{json,md} for the symbol the launcher runs at that\n"
+     << "  shape (default shapes as the reference's); --threads (1..1048576) overrides\n"
+     << "  the launcher's workgroup size\n\n"
      << "info                    print the live device and the gfx950 limits entry\n\n"
      << "--help prints this usage and exits 0.\n";
-}
-
-bool take(int argc, char **argv, int &i, const std::string &arg, const char *flag, std::string &out) {
-  const std::string prefix = std::string(flag) + "=";
-  if (arg.rfind(prefix, 0) == 0) {
-    out = arg.substr(prefix.size());
-    return true;
-  }
-  if (arg == flag) {
-    if (i + 1 >= argc) {
-      std::cerr << "error: " << flag << " requires a value\n";
-      std::exit(kExitUsage);
-    }
-    out = argv[++i];
-    return true;
-  }
-  return false;
-}
-
-bool parse_shape(const std::string &text, std::map<std::string, int64_t> &shape) {
-  size_t start = 0;
-  while (start <= text.size()) {
-    const size_t comma = text.find(',', start);
-    const size_t end = comma == std::string::npos ? text.size() : comma;
-    const std::string item = text.substr(start, end - start);
-    const size_t eq = item.find('=');
-    if (eq == std::string::npos || eq == 0 || eq + 1 >= item.size()) return false;
-    char *vend = nullptr;
-    errno = 0;
-    const long long v = std::strtoll(item.c_str() + eq + 1, &vend, 10);
-    if (errno != 0 || *vend != '\0') return false;
-    shape[item.substr(0, eq)] = v;
-    if (comma == std::string::npos) break;
-    start = comma + 1;
-  }
-  return true;
 }
 
 std::string json_escape(const std::string &s) {
@@ -178,39 +154,33 @@ std::string resources_json(const std::string &kernel, const std::string &shape) 
 
 int run_compile(int argc, char **argv) {
   std::string kernel, shape, target = "amdgcn-gfx950", out;
-  bool resources = false, have_target = false;
-  for (int i = 2; i < argc; ++i) {
-    const std::string arg = argv[i];
-    std::string v;
-    if (arg == "--help" || arg == "-h") {
+  bool resources = false;
+  for (khcli::ArgCursor a(argc, argv, 2); !a.done();) {
+    if (a.flag("--help") || a.flag("-h")) {
       usage(std::cout);
       return kExitOk;
-    } else if (take(argc, argv, i, arg, "--kernel", v)) {
-      kernel = v;
-    } else if (take(argc, argv, i, arg, "--shape", v)) {
-      shape = v;
-    } else if (take(argc, argv, i, arg, "--target", v)) {
-      target = v;
-      have_target = true;
-    } else if (take(argc, argv, i, arg, "--out", v)) {
-      out = v;
-    } else if (arg == "--resources") {
-      resources = true;
-    } else {
-      std::cerr << "error: unknown compile option '" << arg << "'\n";
-      usage(std::cerr);
-      return kExitUsage;
     }
+    if (a.value("--kernel", kernel) || a.value("--shape", shape) || a.value("--target", target) ||
+        a.value("--out", out)) {
+      continue;
+    }
+    if (a.flag("--resources")) {
+      resources = true;
+      continue;
+    }
+    std::cerr << "error: unknown compile option '" << a.word() << "'\n";
+    usage(std::cerr);
+    return kExitUsage;
   }
-  (void)have_target;
   if (kernel.empty() || shape.empty() || out.empty()) {
     std::cerr << "error: compile needs --kernel, --shape and --out\n";
     usage(std::cerr);
     return kExitUsage;
   }
-  std::map<std::string, int64_t> parsed;
-  if (!parse_shape(shape, parsed)) {
-    std::cerr << "error: malformed --shape '" << shape << "'\n";
+  kernelh::ShapeDims parsed;
+  std::string why;
+  if (!kernelh::parse_shape_text(shape, parsed, &why)) {
+    std::cerr << "error: malformed --shape: expected " << why << "\n";
     return kExitUsage;
   }
   const std::string token = target.rfind("amdgcn-", 0) == 0 ? target.substr(7) : target;
@@ -281,90 +251,85 @@ int64_t get(const std::map<std::string, int64_t> &s, const char *k, int64_t dflt
   return it == s.end() ? dflt : it->second;
 }
 
-// Allocates the row's buffers and returns a launcher closure. Rates use the
-// reference's formulas (bench/harness/metrics.cpp), so rows compare across
-// backends: bytes for the bandwidth kernels, 2mnk / 4bhs^2d FLOPs.
-bool prepare(const Row &row, Bufs &b, std::function<int()> &launch, double &work, bool &flops, std::string &error) {
-  std::map<std::string, int64_t> s;
-  if (!parse_shape(row.shape, s)) {
-    error = "malformed shape";
-    return false;
-  }
-  const std::string &k = row.kernel;
-  flops = false;
-  if (row.backend == "hipref-naive" || row.backend == "hipref-vec") {
-    return khcli::prepare_hipref(k, row.backend == "hipref-vec" ? "vec4" : "naive", s, b, launch, work, flops, error);
-  }
-  if (row.backend == "rocblas") {
-    if (k != "gemm") {
-      error = "rocblas backend only benchmarks gemm (got '" + k + "')";
-      return false;
-    }
-    flops = true;
-    return khcli::prepare_rocblas_gemm(s, b, launch, work, error);
-  }
-  if (row.backend == "hipblaslt") {
-    if (k != "gemm") {
-      error = "hipblaslt backend only benchmarks gemm (got '" + k + "')";
-      return false;
-    }
-    flops = true;
-    return khcli::prepare_hipblaslt_gemm(s, b, launch, work, error);
-  }
-  if (k == "roofline_fma") {
-    flops = true;
-    return khcli::prepare_roofline_fma(b, launch, work, error);
-  }
+// Allocates a kernelh row's buffers and returns its launcher closure.
+bool prepare_kernelh(const std::string &k, const kernelh::ShapeDims &s, Bufs &b, std::function<int()> &launch,
+                     std::string &error) {
   error = "unknown kernel or allocation failure";
   if (k == "vecadd") {
     const int64_t n = get(s, "n");
     float *a = b.alloc(n, 1.0f), *bb = b.alloc(n, 2.0f), *c = b.alloc(n, 0.0f);
     launch = [=] { return kh_vecadd(a, bb, c, n, nullptr); };
-    work = 12.0 * n;
   } else if (k == "fused_gelu") {
     const int64_t n = s.count("n") ? get(s, "n") : get(s, "rows") * get(s, "cols");
     float *x = b.alloc(n, 0.25f), *o = b.alloc(n, 0.0f);
     launch = [=] { return kh_fused_gelu(x, nullptr, o, n, nullptr); };
-    work = 12.0 * n;  // fused_gelu_bytes counts the (dead) tmp stream too
   } else if (k == "softmax" || k == "layernorm") {
     const int64_t r = get(s, "rows"), c = get(s, "cols");
     float *x = b.alloc(r * c, 0.5f), *y = b.alloc(r * c, 0.0f);
     if (k == "softmax") {
       launch = [=] { return kh_softmax(x, y, r, c, nullptr); };
-      work = 8.0 * r * c;
     } else {
       float *g = b.alloc(c, 1.0f), *bt = b.alloc(c, 0.0f);
       launch = [=] { return kh_layernorm(x, g, bt, y, r, c, nullptr); };
-      work = 8.0 * r * c + 8.0 * c;
     }
   } else if (k == "scan") {
     const int64_t n = get(s, "n"), T = (n + 255) / 256;
     float *x = b.alloc(n, 0.5f), *y = b.alloc(n, 0.0f), *th = b.alloc(T, 0.0f), *tl = b.alloc(T, 0.0f);
     launch = [=] { return kh_scan(x, y, nullptr, th, tl, n, nullptr); };
-    work = 8.0 * n;
   } else if (k == "gemm") {
     const int64_t m = get(s, "m"), n = get(s, "n"), kk = get(s, "k");
     float *A = b.alloc(m * kk, 1.0f), *B = b.alloc(kk * n, 1.0f), *C = b.alloc(m * n, 0.0f);
     launch = [=] { return kh_gemm(A, B, C, m, n, kk, nullptr); };
-    work = 2.0 * m * n * kk;
-    flops = true;
   } else if (k == "attention") {
     const int64_t bt = get(s, "batch"), h = get(s, "heads"), sq = get(s, "seq"), d = get(s, "head_dim", 64);
     const int64_t e = bt * h * sq * d;
     float *Q = b.alloc(e, 0.01f), *K = b.alloc(e, 0.02f), *V = b.alloc(e, 1.0f), *O = b.alloc(e, 0.0f);
     launch = [=] { return kh_attention(Q, K, V, O, bt, h, sq, d, nullptr); };
-    work = 4.0 * bt * h * sq * sq * d;
-    flops = true;
   } else if (k == "roofline_triad") {
     const int64_t n = get(s, "n");
     float *a = b.alloc(n, 1.0f), *bb = b.alloc(n, 2.0f), *c = b.alloc(n, 0.0f);
     launch = [=] { return kh_roofline_triad(a, bb, c, n, nullptr); };
-    work = 12.0 * n;
   } else {
     return false;
   }
   for (void *p : b.ptrs)
     if (p == nullptr) return false;
+  return true;
+}
+
+// Prepares any row and counts its work with the reference's formulas
+// (bench/harness/metrics.cpp, through khrt_bench_row_work), so rows compare
+// across backends: bytes for the bandwidth kernels, 2mnk / 4bhs^2d FLOPs.
+bool prepare(const Row &row, Bufs &b, std::function<int()> &launch, double &work, bool &flops, std::string &error) {
+  kernelh::ShapeDims s;
+  std::string why;
+  if (!kernelh::parse_shape_text(row.shape, s, &why)) {
+    error = "malformed shape: expected " + why;
+    return false;
+  }
+  const std::string &k = row.kernel;
+  if ((row.backend == "rocblas" || row.backend == "hipblaslt") && k != "gemm") {
+    error = row.backend + " backend only benchmarks gemm (got '" + k + "')";
+    return false;
+  }
+  if (k == "roofline_fma") {
+    double fmas = 0.0;
+    flops = true;
+    return khcli::prepare_roofline_fma(b, launch, fmas, error) &&
+           khrt_bench_metric("roofline_fma_flops", &fmas, 1, &work) == 0;
+  }
+  const bool ok = row.backend == "hipref-naive" || row.backend == "hipref-vec"
+                      ? khcli::prepare_hipref(k, row.backend == "hipref-vec" ? "vec4" : "naive", s, b, launch, error)
+                  : row.backend == "rocblas"   ? khcli::prepare_rocblas_gemm(s, b, launch, error)
+                  : row.backend == "hipblaslt" ? khcli::prepare_hipblaslt_gemm(s, b, launch, error)
+                                               : prepare_kernelh(k, s, b, launch, error);
+  if (!ok) return false;
+  int is_flops = 0;
+  if (khrt_bench_row_work(k.c_str(), row.shape.c_str(), &work, &is_flops) != 0) {
+    error = khrt_last_error();
+    return false;
+  }
+  flops = is_flops != 0;
   return true;
 }
 
@@ -465,85 +430,247 @@ bool known_suite(const std::string &s) {
   return s == "all" || s == "roofline" || s == "kernelh" || s == "rocblas" || s == "hipblaslt" || s == "hipref";
 }
 
-int write_occupancy(const fs::path &dir, const std::vector<std::string> &kernels) {
-  std::ofstream js(dir / "occupancy.json"), md(dir / "occupancy.md");
-  md << "# Occupancy report (gfx950)\n\n"
-     << "achieved_waves = min(VGPR-limited waves, LDS-limited blocks, thread-limited blocks) on the\n"
-     << "gfx950 device-limits entry; measured % from the vendor occupancy API when a device is\n"
-     << "present.\n\n| kernel | vgpr+agpr | lds (B) | block | theoretical % | measured % | limiter |\n"
-     << "| --- | ---: | ---: | ---: | ---: | ---: | --- |\n";
-  js << "{\n  \"reports\": [\n";
-  const char *limiters[] = {"none", "vgpr", "lds", "threads"};
+// ---------------------------------------------------------------- occupancy
+
+// One occupancy report (the reference's OccupancyReport, occupancy.cpp:90-110
+// for its JSON keys): the analytic bound from the symbol the launcher runs at
+// `shape` (its VGPR+AGPR count and static LDS) on the gfx950 limits entry,
+// and, when a device is present, the vendor occupancy API on that loaded
+// function. `threads` 0 takes the launcher's workgroup size at that shape.
+struct OccupancyRow {
+  std::string kernel, config, symbol;
+  int32_t registers = 0, threads = 0;
+  int64_t lds = 0;
+  khrt_occupancy_report rep{};
+};
+
+const char *limiter_name(int32_t l) {
+  static const char *names[] = {"none", "vgpr", "lds", "threads"};
+  return l >= 0 && l <= 3 ? names[l] : "none";
+}
+
+// The reference's default shapes for the occupancy-only mode, used when no
+// --shape is given (kernelh_backend.cpp:447-469); scan_totals as scan.
+std::string default_occupancy_shape(const std::string &kernel) {
+  static const std::map<std::string, std::string> shapes = {
+      {"gemm", "m=512,n=512,k=512"},       {"softmax", "rows=4096,cols=1024"},
+      {"layernorm", "rows=4096,cols=1024"}, {"scan", "n=100000"},
+      {"scan_totals", "n=100000"},          {"fused_gelu", "n=1048576"},
+      {"attention", "batch=2,heads=8,seq=512,head_dim=64"},
+      {"vecadd", "n=1024"}};
+  const auto it = shapes.find(kernel);
+  return it == shapes.end() ? std::string() : it->second;
+}
+
+bool occupancy_row(const std::string &kernel, const std::string &shape, int threads, bool have_device,
+                   OccupancyRow &row, std::string &error) {
+  row.kernel = kernel;
+  row.config = shape;
+  char sym[64] = {0};
+  khrt_kernel_resources r{};
+  khrt_dim3 grid{}, block{};
+  if (khrt_template_launch_symbol(kernel.c_str(), shape.c_str(), sym, sizeof(sym)) != 0 ||
+      khrt_template_resources(sym, &r) != 0 ||
+      khrt_template_geometry(kernel.c_str(), shape.c_str(), &grid, &block) != 0) {
+    error = khrt_last_error();
+    return false;
+  }
+  row.symbol = sym;
+  row.registers = r.vgpr_count + r.agpr_count;
+  row.lds = r.lds_bytes;
+  row.threads = threads > 0 ? threads : static_cast<int32_t>(block.x * block.y * block.z);
   khrt_device_limits lim{};
   khrt_device_limits_for("gfx950", &lim);
-  int dev_count = 0;
-  const bool have_dev = khrt_device_count(&dev_count) == 0 && dev_count > 0;
-  if (have_dev) khrt_live_limits(&lim);
-  for (size_t i = 0; i < kernels.size(); ++i) {
-    const std::string &k = kernels[i];
-    khrt_kernel_resources r{};
-    if (khrt_template_resources(k.c_str(), &r) != 0) continue;
-    const int block = (k == "scan") ? 1024 : 256;
-    void *fn = nullptr;
-    if (have_dev) khrt_template_function(k.c_str(), &fn);
-    khrt_occupancy_input in{k.c_str(), "gfx950", "", r.vgpr_count + r.agpr_count, r.lds_bytes, block};
-    khrt_occupancy_report rep{};
-    khrt_compute_occupancy(&in, &lim, fn, &rep);
-    js << "    {\"kernel\": \"" << k << "\", \"vgpr_count\": " << r.vgpr_count + r.agpr_count
-       << ", \"lds_bytes\": " << r.lds_bytes << ", \"threads_per_workgroup\": " << block
-       << ", \"theoretical_waves\": " << rep.achieved_waves << ", \"theoretical_pct\": " << rep.theoretical_pct
-       << ", \"limiter\": \"" << limiters[rep.limiter] << "\", \"measured_blocks\": " << rep.measured_blocks
-       << ", \"measured_pct\": " << rep.measured_pct << "}" << (i + 1 < kernels.size() ? "," : "") << "\n";
-    md << "| " << k << " | " << r.vgpr_count + r.agpr_count << " | " << r.lds_bytes << " | " << block << " | "
-       << rep.theoretical_pct << " | ";
-    if (rep.measured_blocks >= 0) {
-      md << rep.measured_pct;
+  void *fn = nullptr;
+  if (have_device && khrt_live_limits(&lim) != 0) return (error = khrt_last_error()), false;
+  if (have_device) khrt_template_function(sym, &fn);
+  const khrt_occupancy_input in{kernel.c_str(), "gfx950", shape.c_str(), row.registers, row.lds, row.threads};
+  if (khrt_compute_occupancy(&in, &lim, fn, &row.rep) != 0) {
+    error = khrt_last_error();
+    return false;
+  }
+  return true;
+}
+
+std::string occupancy_json(const OccupancyRow &o, const std::string &indent) {
+  std::ostringstream os;
+  const std::string i2 = indent + "  ";
+  os << "{\n"
+     << i2 << "\"kernel\": \"" << json_escape(o.kernel) << "\",\n"
+     << i2 << "\"target\": \"amdgcn-gfx950\",\n"
+     << i2 << "\"config\": \"" << json_escape(o.config) << "\",\n"
+     << i2 << "\"symbol\": \"" << json_escape(o.symbol) << "\",\n"
+     << i2 << "\"vgpr_count\": " << o.registers << ",\n"
+     << i2 << "\"lds_bytes\": " << o.lds << ",\n"
+     << i2 << "\"threads_per_workgroup\": " << o.threads << ",\n"
+     << i2 << "\"vgpr_limited_waves\": " << o.rep.vgpr_limited_waves << ",\n"
+     << i2 << "\"lds_limited_blocks\": " << o.rep.lds_limited_blocks << ",\n"
+     << i2 << "\"thread_limited_blocks\": " << o.rep.thread_limited_blocks << ",\n"
+     << i2 << "\"theoretical_waves\": " << o.rep.achieved_waves << ",\n"
+     << i2 << "\"theoretical_pct\": " << o.rep.theoretical_pct << ",\n"
+     << i2 << "\"limiter\": \"" << limiter_name(o.rep.limiter) << "\",\n"
+     << i2 << "\"measured_blocks\": " << o.rep.measured_blocks << ",\n"
+     << i2 << "\"measured_pct\": " << o.rep.measured_pct << ",\n"
+     << i2 << "\"measured_note\": \"" << json_escape(o.rep.measured_note) << "\"\n"
+     << indent << "}";
+  return os.str();
+}
+
+// occupancy.json (one report object, or {"reports": [...]} for a suite, as
+// the reference writes them) and occupancy.md in `dir`.
+bool write_occupancy(const fs::path &dir, const std::vector<OccupancyRow> &rows, bool single, std::string &error) {
+  std::error_code ec;
+  fs::create_directories(dir, ec);
+  std::ofstream js(dir / "occupancy.json"), md(dir / "occupancy.md");
+  if (!js || !md) {
+    error = "cannot write occupancy files in '" + dir.string() + "'";
+    return false;
+  }
+  if (single) {
+    js << occupancy_json(rows.front(), "") << "\n";
+  } else {
+    js << "{\n  \"reports\": [\n";
+    for (size_t i = 0; i < rows.size(); ++i)
+      js << "    " << occupancy_json(rows[i], "    ") << (i + 1 < rows.size() ? ",\n" : "\n");
+    js << "  ]\n}\n";
+  }
+  md << "# Occupancy report (gfx950)\n\n"
+     << "Theoretical occupancy from the symbol the launcher runs at each shape (VGPR+AGPR count and\n"
+     << "static LDS from its code-object notes) on the gfx950 device-limits entry; measured occupancy\n"
+     << "from hipModuleOccupancyMaxActiveBlocksPerMultiprocessor on the loaded function when a device\n"
+     << "is present.\n\n"
+     << "| kernel | config | symbol | vgpr+agpr | lds (B) | threads | theoretical % | measured % | limiter |\n"
+     << "| --- | --- | --- | ---: | ---: | ---: | ---: | ---: | --- |\n";
+  for (const OccupancyRow &o : rows) {
+    md << "| " << o.kernel << " | " << o.config << " | " << o.symbol << " | " << o.registers << " | " << o.lds
+       << " | " << o.threads << " | " << o.rep.theoretical_pct << " | ";
+    if (o.rep.measured_blocks >= 0) {
+      md << o.rep.measured_pct;
     } else {
       md << "n/a";
     }
-    md << " | " << limiters[rep.limiter] << " |\n";
+    md << " | " << limiter_name(o.rep.limiter) << " |\n";
   }
-  js << "  ]\n}\n";
-  std::cout << "wrote " << (dir / "occupancy.json").string() << "\nwrote " << (dir / "occupancy.md").string() << "\n";
+  md << "\nNotes:\n"
+     << "- achieved_waves = min(VGPR-limited waves, LDS-limited blocks, thread-limited blocks), the three\n"
+     << "  bounds compared directly as the reference's formula pins them; theoretical % = achieved_waves /\n"
+     << "  waves_per_cu x 100 (waves_per_cu = 32 on gfx950).\n"
+     << "- measured % = resident blocks x waves per block / waves_per_cu x 100 from the vendor API; n/a\n"
+     << "  without a device.\n";
+  std::cout << "wrote " << (dir / "occupancy.json").string() << "\nwrote " << (dir / "occupancy.md").string()
+            << "\n";
+  return true;
+}
+
+// Occupancy of every kernelh row of the given rows (the reference writes
+// one report per kernelh row of the suite, kernelh_backend.cpp:658-698).
+int write_suite_occupancy(const fs::path &dir, const std::vector<Row> &rows, bool have_device) {
+  std::vector<OccupancyRow> out;
+  for (const Row &row : rows) {
+    if (row.backend != "kernelh") continue;
+    OccupancyRow o;
+    std::string error;
+    if (!occupancy_row(row.kernel, row.shape, 0, have_device, o, error)) {
+      std::cerr << "error: occupancy " << row.kernel << " " << row.shape << ": " << error << "\n";
+      return kExitOperational;
+    }
+    out.push_back(o);
+  }
+  if (out.empty()) {
+    std::cerr << "error: no kernelh rows for occupancy\n";
+    return kExitOperational;
+  }
+  std::string error;
+  if (!write_occupancy(dir, out, false, error)) {
+    std::cerr << "error: " << error << "\n";
+    return kExitOperational;
+  }
+  return kExitOk;
+}
+
+bool device_present() {
+  int n = 0;
+  return khrt_device_count(&n) == 0 && n > 0 && khrt_init_device(0) == 0;
+}
+
+// `bench --occupancy --kernel <k> --target amdgcn-gfx950 [--shape ...]
+// [--threads N] --out <dir>`: occupancy.{json,md} for one kernel and shape,
+// timing nothing; no device needed (run_bench.cpp:111-127).
+int run_occupancy_only(const std::string &kernel, const std::string &shape_in, int threads, const fs::path &dir) {
+  const std::string shape = shape_in.empty() ? default_occupancy_shape(kernel) : shape_in;
+  if (shape.empty()) {
+    std::cerr << "error: unknown kernel '" << kernel << "' for --occupancy (no default shape); use --shape k=v,...\n";
+    return kExitOperational;
+  }
+  OccupancyRow o;
+  std::string error;
+  if (!occupancy_row(kernel, shape, threads, device_present(), o, error) || !write_occupancy(dir, {o}, true, error)) {
+    std::cerr << "error: " << error << "\n";
+    return kExitOperational;
+  }
+  std::cout << "wrote " << dir.string() << "/occupancy.json + occupancy.md (" << kernel << ", amdgcn-gfx950)\n";
   return kExitOk;
 }
 
 int run_bench(int argc, char **argv) {
-  std::string suite = "all", out, kernel, shape, backend = "kernelh", v;
-  int warmup = 5, iters = 20;
-  bool occupancy = false;
-  for (int i = 2; i < argc; ++i) {
-    const std::string arg = argv[i];
-    if (arg == "--help" || arg == "-h") {
+  std::string suite = "all", out, kernel, shape, backend = "kernelh", target;
+  long warmup = 5, iters = 20, threads = 0;
+  bool occupancy = false, ok = true;
+  for (khcli::ArgCursor a(argc, argv, 2); !a.done() && ok;) {
+    if (a.flag("--help") || a.flag("-h")) {
       usage(std::cout);
       return kExitOk;
-    } else if (take(argc, argv, i, arg, "--suite", v)) {
-      suite = v;
-    } else if (take(argc, argv, i, arg, "--out", v)) {
-      out = v;
-    } else if (take(argc, argv, i, arg, "--kernel", v)) {
-      kernel = v;
-    } else if (take(argc, argv, i, arg, "--shape", v)) {
-      shape = v;
-    } else if (take(argc, argv, i, arg, "--backend", v)) {
-      backend = v;
-    } else if (take(argc, argv, i, arg, "--warmup", v)) {
-      warmup = std::atoi(v.c_str());
-    } else if (take(argc, argv, i, arg, "--iters", v)) {
-      iters = std::atoi(v.c_str());
-    } else if (arg == "--occupancy") {
+    }
+    if (a.value("--suite", suite) || a.value("--out", out) || a.value("--kernel", kernel) ||
+        a.value("--shape", shape) || a.value("--backend", backend) || a.value("--target", target) ||
+        a.integer("--warmup", 0, 1000000, warmup, ok) || a.integer("--iters", 1, 1000000, iters, ok) ||
+        a.integer("--threads", 1, 1048576, threads, ok)) {
+      continue;
+    }
+    if (a.flag("--occupancy")) {
       occupancy = true;
-    } else {
-      std::cerr << "error: unknown bench option '" << arg << "'\n";
+      continue;
+    }
+    std::cerr << "error: unknown bench option '" << a.word() << "'\n";
+    return kExitUsage;
+  }
+  if (!ok) return kExitUsage;
+  if (out.empty()) {
+    std::cerr << "error: bench requires --out <path> (a .csv file or a dir)\n";
+    return kExitUsage;
+  }
+  kernelh::ShapeDims dims;
+  std::string why;
+  if (!shape.empty() && !kernelh::parse_shape_text(shape, dims, &why)) {
+    std::cerr << "error: malformed --shape: expected " << why << "\n";
+    return kExitUsage;
+  }
+  // The reference's occupancy-only mode (--occupancy --kernel --target);
+  // --target and --threads belong to it alone.
+  if ((!target.empty() || threads != 0) && !(occupancy && !kernel.empty())) {
+    std::cerr << "error: --target/--threads require --occupancy --kernel <name>\n";
+    return kExitUsage;
+  }
+  if (occupancy && !kernel.empty() && !target.empty()) {
+    if (target != "amdgcn-gfx950") {
+      std::cerr << "error: unknown --target '" << target << "' for --occupancy\n"
+                << "error: valid --target values: amdgcn-gfx950\n";
       return kExitUsage;
     }
+    return run_occupancy_only(kernel, shape, static_cast<int>(threads), fs::path(out));
+  }
+  // Otherwise --kernel times one row at --shape (with its occupancy when
+  // --occupancy is given); --occupancy --kernel alone names no shape.
+  if (!kernel.empty() && shape.empty()) {
+    std::cerr << "error: --kernel needs --shape to time a row, or --occupancy --kernel <name> --target "
+                 "amdgcn-gfx950 for its occupancy alone\n";
+    return kExitUsage;
   }
   const bool known_backend = backend == "kernelh" || backend == "rocblas" || backend == "hipblaslt" ||
                              backend == "hipref-naive" || backend == "hipref-vec" || backend == "roofline";
-  if (out.empty() || !known_suite(suite) || !known_backend || iters < 1 || warmup < 0 ||
-      (!kernel.empty() && shape.empty())) {
-    std::cerr << "error: bench needs --out, a suite of roofline|kernelh|rocblas|hipblaslt|hipref|all, a backend of "
-                 "kernelh|rocblas|hipblaslt|hipref-naive|hipref-vec|roofline, and --shape with --kernel\n";
+  if (!known_suite(suite) || !known_backend) {
+    std::cerr << "error: bench takes a suite of roofline|kernelh|rocblas|hipblaslt|hipref|all and a backend of "
+                 "kernelh|rocblas|hipblaslt|hipref-naive|hipref-vec|roofline\n";
     return kExitUsage;
   }
   fs::path csv = out;
@@ -554,17 +681,16 @@ int run_bench(int argc, char **argv) {
   } else if (csv.has_parent_path()) {
     fs::create_directories(csv.parent_path(), ec);
   }
-  int n = 0;
-  if (khrt_device_count(&n) != 0 || n < 1 || khrt_init_device(0) != 0) {
+  const fs::path dir = csv.has_parent_path() ? csv.parent_path() : fs::path(".");
+  std::vector<Row> rows = kernel.empty() ? suite_rows(suite) : std::vector<Row>{{kernel, shape, backend}};
+  if (!device_present()) {
     std::cerr << "skip: no HIP device available (" << khrt_last_error() << ")\n";
-    if (occupancy) write_occupancy(csv.parent_path(), {"vecadd", "gemm", "softmax", "layernorm", "scan", "scan_totals",
-                                                       "fused_gelu", "attention"});
+    if (occupancy) write_suite_occupancy(dir, rows, false);
     return kExitSkip;
   }
   khrt_device_info info{};
   khrt_get_device_info(&info);
   const std::string device = std::string(info.name[0] ? info.name : "AMD Instinct MI355X") + " (" + info.arch + ")";
-  std::vector<Row> rows = kernel.empty() ? suite_rows(suite) : std::vector<Row>{{kernel, shape, backend}};
   const bool fresh = !fs::exists(csv);
   std::ofstream f(csv, std::ios::app);
   if (fresh) f << "kernel,shape,backend,ms_median,gflops_or_gbps,timestamp,device\n";
@@ -581,13 +707,15 @@ int run_bench(int argc, char **argv) {
       ++failures;
       continue;
     }
-    if (!time_row(launch, warmup, iters, ms)) {
+    if (!time_row(launch, static_cast<int>(warmup), static_cast<int>(iters), ms)) {
       std::cerr << "error: " << row.backend << " " << row.kernel << " " << row.shape << ": " << khrt_last_error()
                 << "\n";
       ++failures;
       continue;
     }
-    const double rate = work * 1000.0 / ms / 1e9;  // GFLOP/s or GB/s (metrics.cpp:5-12)
+    double rate = 0.0;
+    const double args[2] = {work, ms};
+    khrt_bench_metric(flops ? "gflops_from_ms" : "gbps_from_ms", args, 2, &rate);
     std::string shp = row.shape;
     std::replace(shp.begin(), shp.end(), ',', ';');
     f << row.kernel << "," << shp << "," << row.backend << "," << ms << "," << rate << "," << now_iso() << ",\""
@@ -596,12 +724,7 @@ int run_bench(int argc, char **argv) {
                 row.shape.c_str(), ms, rate, flops ? "GFLOP/s" : "GB/s");
   }
   std::cout << "wrote " << csv.string() << "\n";
-  if (occupancy) {
-    write_occupancy(csv.parent_path(),
-                    kernel.empty() ? std::vector<std::string>{"vecadd", "gemm", "softmax", "layernorm", "scan",
-                                                              "scan_totals", "fused_gelu", "attention"}
-                                   : std::vector<std::string>{kernel});
-  }
+  if (occupancy && write_suite_occupancy(dir, rows, true) != kExitOk) ++failures;
   return failures ? kExitOperational : kExitOk;
 }
 

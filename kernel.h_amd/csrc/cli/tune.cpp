@@ -17,11 +17,16 @@
 //     reads the same file when pointed at it (KHRT_TUNE_CACHE or
 //     khrt_set_tune_cache) and then runs the cached best for that shape.
 // Differences, each stated in the usage text: the space is a fixed set of
-// precompiled instantiations (no per-candidate compilation), so it is
-// evaluated exhaustively up to --max-candidates instead of sampled and
-// refined, and the cache key is an FNV-1a 64-bit hash (khrt_tune_cache_key).
+// precompiled instantiations (no per-candidate compilation), small enough
+// to evaluate whole, so that is the default (up to --max-candidates); the
+// reference's sampled search runs when --sample or --refine-budget is given
+// (a fixed-seed sample of the space, then single-step refinement around the
+// best accepted candidate, lib/compiler/autotuner.cpp:826-875). The cache key
+// is an FNV-1a 64-bit hash (khrt_tune_cache_key).
 #include "tune.hpp"
 
+#include "args.hpp"
+#include "kernelh/shape_text.hpp"
 #include "khrt.h"
 
 #include <poll.h>
@@ -68,36 +73,40 @@ struct Result {
   std::string reason;
 };
 
-bool take(int argc, char **argv, int &i, const std::string &arg, const char *flag, std::string &out) {
-  if (arg == flag && i + 1 < argc) {
-    out = argv[++i];
-    return true;
+// m, n and k (all positive, and nothing else) from shape text.
+bool parse_mnk(const std::string &text, int64_t &m, int64_t &n, int64_t &k) {
+  kernelh::ShapeDims d;
+  if (!kernelh::parse_shape_text(text, d) || d.size() != 3 || !d.count("m") || !d.count("n") || !d.count("k")) {
+    return false;
   }
-  const std::string pre = std::string(flag) + "=";
-  if (arg.rfind(pre, 0) == 0) {
-    out = arg.substr(pre.size());
-    return true;
-  }
-  return false;
+  m = d["m"], n = d["n"], k = d["k"];
+  return m > 0 && n > 0 && k > 0;
 }
 
-bool parse_mnk(const std::string &text, int64_t &m, int64_t &n, int64_t &k) {
-  m = n = k = 0;
-  std::stringstream ss(text);
-  std::string item;
-  while (std::getline(ss, item, ',')) {
-    const auto eq = item.find('=');
-    if (eq == std::string::npos) return false;
-    char *end = nullptr;
-    const long long v = std::strtoll(item.c_str() + eq + 1, &end, 10);
-    if (*end != '\0') return false;
-    const std::string key = item.substr(0, eq);
-    if (key == "m") m = v;
-    else if (key == "n") n = v;
-    else if (key == "k") k = v;
-    else return false;
-  }
-  return m > 0 && n > 0 && k > 0;
+// The search order of --sample: the candidate list shuffled by a
+// Fisher-Yates pass driven by SplitMix64 from a fixed seed, so a run is
+// reproducible.
+std::vector<int> sample_order(int total, uint64_t seed) {
+  std::vector<int> order(static_cast<size_t>(total));
+  for (int i = 0; i < total; ++i) order[static_cast<size_t>(i)] = i;
+  auto next = [&seed] {
+    uint64_t z = (seed += 0x9e3779b97f4a7c15ull);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+  };
+  for (int i = total - 1; i > 0; --i) std::swap(order[static_cast<size_t>(i)], order[next() % (i + 1)]);
+  return order;
+}
+
+// Candidates one design step away from `c`: the same in every field the
+// space varies but one (bm, bn, bk, waves, unroll, MFMA shape, pipeline,
+// priority, K-split).
+bool one_step_apart(const Candidate &a, const Candidate &b) {
+  const int diffs = (a.bm != b.bm) + (a.bn != b.bn) + (a.bk != b.bk) + (a.waves != b.waves) +
+                    (a.unroll != b.unroll) + (a.mfma != b.mfma) + (std::strcmp(a.pipeline, b.pipeline) != 0) +
+                    (a.prio != b.prio) + (a.k_split != b.k_split);
+  return diffs == 1;
 }
 
 std::string self_exe() {
@@ -237,6 +246,11 @@ void usage_tune(std::ostream &os) {
      << "  --target <t>          amdgcn-gfx950 (default; the local execution target)\n"
      << "  --max-candidates <n>  cap on evaluated candidates (1.." << khrt_gemm_candidate_count()
      << ", default all)\n"
+     << "  --sample <n>          sampled search: n candidates (1..216, default 64) in a\n"
+     << "                        fixed pseudo-random order ...\n"
+     << "  --refine-budget <n>   ... then up to n (0..80, default 16) candidates one\n"
+     << "                        design step from the best; without either flag every\n"
+     << "                        candidate is evaluated in list order\n"
      << "  --timeout <seconds>   wall clock per candidate (1..3600, default 30)\n"
      << "  --cache <path>        cache file (default build/tune-cache.json), keyed\n"
      << "                        FNV-1a(kernel|shape|device)\n"
@@ -244,8 +258,9 @@ void usage_tune(std::ostream &os) {
      << "(gemm_tune_space.py): MFMA 32x32 or 16x16 wave tiles, 4 or 8 waves, BM/BN in\n"
      << "{64,128,256}, BK in {16,32}, unroll 1 or 2 (register-staged, direct-to-LDS\n"
      << "three stages, or two slabs ahead), MFMA wave priority; vec is 4 (dwordx4)\n"
-     << "when k and n are multiples of 4, else 1. The space is precompiled and\n"
-     << "evaluated exhaustively, not sampled. Point the runtime at the cache\n"
+     << "when k and n are multiples of 4, else 1. The space is precompiled; it is\n"
+     << "evaluated whole unless --sample/--refine-budget ask for the sampled search.\n"
+     << "Point the runtime at the cache\n"
      << "(KHRT_TUNE_CACHE=<path> or khrt_set_tune_cache) and kh_gemm runs the\n"
      << "cached best for each tuned shape.\n";
 }
@@ -289,13 +304,15 @@ int eval_print(bool accepted, double ms, double gflops, const std::string &reaso
 }  // namespace
 
 int run_tune_eval(int argc, char **argv) {
-  std::string symbol, shape, v;
+  std::string symbol, shape;
   bool probe = false;
-  for (int i = 2; i < argc; ++i) {
-    const std::string arg = argv[i];
-    if (take(argc, argv, i, arg, "--symbol", v)) symbol = v;
-    else if (take(argc, argv, i, arg, "--shape", v)) shape = v;
-    else if (arg == "--probe") probe = true;
+  for (khcli::ArgCursor a(argc, argv, 2); !a.done();) {
+    if (a.value("--symbol", symbol) || a.value("--shape", shape)) continue;
+    if (a.flag("--probe")) {
+      probe = true;
+      continue;
+    }
+    a.skip();
   }
   int count = 0;
   if (khrt_device_count(&count) != 0 || count < 1 || khrt_init_device(0) != 0) {
@@ -401,42 +418,32 @@ int run_tune_eval(int argc, char **argv) {
 }
 
 int run_tune(int argc, char **argv) {
-  std::string kernel = "gemm", shape, out, target = "amdgcn-gfx950", cache = "build/tune-cache.json", v;
+  std::string kernel = "gemm", shape, out, target = "amdgcn-gfx950", cache = "build/tune-cache.json";
   const std::vector<Candidate> space = candidates();
   const int total = static_cast<int>(space.size());
-  int max_candidates = total, timeout_s = 30;
-  for (int i = 2; i < argc; ++i) {
-    const std::string arg = argv[i];
-    if (arg == "--help" || arg == "-h") {
+  long max_candidates = total, timeout_s = 30, sample = 64, refine = 16;
+  bool searched = false, ok = true;
+  for (khcli::ArgCursor a(argc, argv, 2); !a.done() && ok;) {
+    if (a.flag("--help") || a.flag("-h")) {
       usage_tune(std::cout);
       return 0;
-    } else if (take(argc, argv, i, arg, "--kernel", v)) {
-      kernel = v;
-    } else if (take(argc, argv, i, arg, "--shape", v)) {
-      shape = v;
-    } else if (take(argc, argv, i, arg, "--out", v)) {
-      out = v;
-    } else if (take(argc, argv, i, arg, "--target", v)) {
-      target = v;
-    } else if (take(argc, argv, i, arg, "--cache", v)) {
-      cache = v;
-    } else if (take(argc, argv, i, arg, "--max-candidates", v)) {
-      max_candidates = std::atoi(v.c_str());
-      if (max_candidates < 1 || max_candidates > total) {
-        std::cerr << "error: --max-candidates must be an integer in [1," << total << "]\n";
-        return 2;
-      }
-    } else if (take(argc, argv, i, arg, "--timeout", v)) {
-      timeout_s = std::atoi(v.c_str());
-      if (timeout_s < 1 || timeout_s > 3600) {
-        std::cerr << "error: --timeout must be an integer in [1,3600]\n";
-        return 2;
-      }
-    } else {
-      std::cerr << "error: unknown flag '" << arg << "' for tune\n";
-      return 2;
     }
+    if (a.value("--kernel", kernel) || a.value("--shape", shape) || a.value("--out", out) ||
+        a.value("--target", target) || a.value("--cache", cache) ||
+        a.integer("--max-candidates", 1, total, max_candidates, ok) ||
+        a.integer("--timeout", 1, 3600, timeout_s, ok)) {
+      continue;
+    }
+    // The reference's sampled search (main.cpp:710-723): a sample of the
+    // space, then single-step refinement around the best.
+    if (a.integer("--sample", 1, 216, sample, ok) || a.integer("--refine-budget", 0, 80, refine, ok)) {
+      searched = true;
+      continue;
+    }
+    std::cerr << "error: unknown flag '" << a.word() << "' for tune\n";
+    return 2;
   }
+  if (!ok) return 2;
   int64_t m, n, k;
   if (shape.empty() || out.empty()) {
     std::cerr << "error: tune requires --shape m=...,n=...,k=... and --out <dir>\n";
@@ -458,8 +465,8 @@ int run_tune(int argc, char **argv) {
   int status = 0;
   bool timed_out = false;
   const std::string shape_text = "m=" + std::to_string(m) + ",n=" + std::to_string(n) + ",k=" + std::to_string(k);
-  const std::string probe =
-      run_child({exe, "tune-eval", "--probe", "--shape", shape_text}, timeout_s, status, timed_out);
+  const std::string probe = run_child({exe, "tune-eval", "--probe", "--shape", shape_text},
+                                      static_cast<int>(timeout_s), status, timed_out);
   const auto dev = probe.find("DEVICE ");
   const auto kpos = probe.find("KEY ");
   if (dev == std::string::npos || kpos == std::string::npos) {
@@ -482,12 +489,14 @@ int run_tune(int argc, char **argv) {
   }
 
   std::vector<Result> results;
-  for (int i = 0; i < total && i < max_candidates; ++i) {
-    const Candidate &c = space[i];
+  std::vector<bool> seen(static_cast<size_t>(total), false);
+  auto evaluate = [&](int i) {
+    const Candidate &c = space[static_cast<size_t>(i)];
+    seen[static_cast<size_t>(i)] = true;
     Result r;
     r.c = &c;
-    const std::string outp =
-        run_child({exe, "tune-eval", "--symbol", c.symbol, "--shape", shape_text}, timeout_s, status, timed_out);
+    const std::string outp = run_child({exe, "tune-eval", "--symbol", c.symbol, "--shape", shape_text},
+                                       static_cast<int>(timeout_s), status, timed_out);
     if (timed_out) {
       r.reason = "timeout";
     } else if (WIFSIGNALED(status)) {
@@ -504,6 +513,33 @@ int run_tune(int argc, char **argv) {
                 r.gflops);
     std::fflush(stdout);
     results.push_back(r);
+  };
+  const int budget = static_cast<int>(max_candidates);
+  if (!searched) {
+    // Every candidate in list order (the launcher's own symbols first), up
+    // to --max-candidates: the space is small enough to evaluate whole.
+    for (int i = 0; i < total && i < budget; ++i) evaluate(i);
+  } else {
+    // --sample candidates in a fixed pseudo-random order, then up to
+    // --refine-budget candidates one step from the best accepted one, all
+    // within --max-candidates.
+    const std::vector<int> order = sample_order(total, 0x6b65726e656c68ull);
+    for (int j = 0; j < total && j < sample && static_cast<int>(results.size()) < budget; ++j) evaluate(order[j]);
+    const Result *best = nullptr;
+    for (const Result &r : results)
+      if (r.accepted && (best == nullptr || r.ms < best->ms)) best = &r;
+    if (best == nullptr) {
+      std::printf("no accepted candidate; skipping refinement\n");
+    } else {
+      const Candidate centre = *best->c;
+      std::vector<int> near;
+      for (int i = 0; i < total; ++i)
+        if (!seen[static_cast<size_t>(i)] && one_step_apart(space[static_cast<size_t>(i)], centre)) near.push_back(i);
+      const int n_refine = std::min<int>({static_cast<int>(refine), static_cast<int>(near.size()),
+                                          budget - static_cast<int>(results.size())});
+      std::printf("refining around %s with %d neighbour(s)\n", centre.symbol, std::max(n_refine, 0));
+      for (int j = 0; j < n_refine; ++j) evaluate(near[static_cast<size_t>(j)]);
+    }
   }
 
   // vec: floats per global load the candidate issues at this shape: float4

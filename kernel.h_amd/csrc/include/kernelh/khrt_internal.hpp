@@ -10,6 +10,8 @@
 #include <string>
 #include <vector>
 
+#include "kernelh/shape_text.hpp"
+
 namespace khrt {
 
 // Thread-local last-error message (khrt_last_error).
@@ -24,9 +26,6 @@ int fail_hip(hipError_t e, const char *what);
 // Ensures a device is current (ordinal 0 unless khrt_init_device chose one).
 int ensure_device();
 int current_device();
-
-// "k=v,k=v" -> map; false on any malformed segment (main.cpp:242-266).
-bool parse_shape(const std::string &text, std::map<std::string, int64_t> &out);
 
 // Verified launch used by both khrt_kernel_launch and the kh_* entry points.
 int verified_launch(void *function, khrt_dim3 grid, khrt_dim3 block, size_t shared, void *stream,

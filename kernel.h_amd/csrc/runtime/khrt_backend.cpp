@@ -54,26 +54,6 @@ int ensure_device() {
 
 int current_device() { return g_device < 0 ? 0 : g_device; }
 
-bool parse_shape(const std::string &text, std::map<std::string, int64_t> &out) {
-  size_t start = 0;
-  while (start <= text.size()) {
-    const size_t comma = text.find(',', start);
-    const size_t end = comma == std::string::npos ? text.size() : comma;
-    const std::string item = text.substr(start, end - start);
-    const size_t eq = item.find('=');
-    if (eq == std::string::npos || eq == 0 || eq + 1 >= item.size()) return false;
-    const std::string value = item.substr(eq + 1);
-    char *vend = nullptr;
-    errno = 0;
-    const long long v = std::strtoll(value.c_str(), &vend, 10);
-    if (errno != 0 || vend == value.c_str() || *vend != '\0') return false;
-    out[item.substr(0, eq)] = v;
-    if (comma == std::string::npos) break;
-    start = comma + 1;
-  }
-  return true;
-}
-
 void LaunchArgs::add_memref(const void *ptr, std::vector<int64_t> shape) {
   const uint64_t p = static_cast<uint64_t>(reinterpret_cast<uintptr_t>(ptr));
   slots_.push_back(p);  // allocated

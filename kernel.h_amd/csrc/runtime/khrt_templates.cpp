@@ -533,7 +533,8 @@ int khrt_template_geometry(const char *name, const char *shape, khrt_dim3 *grid,
   if (grid == nullptr || block == nullptr || shape == nullptr) return bad("khrt_template_geometry: null argument");
   if (find_template(name) == nullptr) return unknown_template(name);
   Shape s;
-  if (!khrt::parse_shape(shape, s)) return khrt::fail(KHRT_E_INVALID, std::string("malformed shape '") + shape + "'");
+  std::string why;
+  if (!kernelh::parse_shape_text(shape, s, &why)) return khrt::fail(KHRT_E_INVALID, "malformed shape: expected " + why);
   return geometry(name, s, *grid, *block);
 }
 
@@ -542,7 +543,8 @@ int khrt_template_launch_symbol(const char *name, const char *shape, char *out, 
   const Template *t = find_template(name);
   if (t == nullptr) return unknown_template(name);
   Shape s;
-  if (!khrt::parse_shape(shape, s)) return khrt::fail(KHRT_E_INVALID, std::string("malformed shape '") + shape + "'");
+  std::string why;
+  if (!kernelh::parse_shape_text(shape, s, &why)) return khrt::fail(KHRT_E_INVALID, "malformed shape: expected " + why);
   khrt_dim3 grid, block;
   if (int rc = geometry(name, s, grid, block)) return rc;  // the same shape checks as a launch
   const std::string sym = launch_symbol(t, s);

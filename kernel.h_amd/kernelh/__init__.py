@@ -173,6 +173,9 @@ SIGNATURES = {
     "kh_roofline_triad": (_i, [_vp, _vp, _vp, _i64, _vp]),
     "kh_roofline_copy": (_i, [_vp, _vp, _i64, _vp]),
     "kh_roofline_mfma": (_i, [_vp, _i64, _i64, _vp]),
+    "khrt_bench_metric": (_i, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), _i, ctypes.POINTER(ctypes.c_double)]),
+    "khrt_bench_row_work": (_i, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
+                                 ctypes.POINTER(_i)]),
 }
 
 
@@ -570,6 +573,21 @@ def roofline_mfma(out, blocks: int, iters: int, stream=None) -> float:
     """Launches the MFMA microbenchmark; returns the FLOPs it executes."""
     check(lib.kh_roofline_mfma(_ptr(out), blocks, iters, _ptr(stream)))
     return float(blocks) * 4 * iters * 8 * 4096
+
+
+def bench_metric(formula: str, *args: float) -> float:
+    """One of the reference's bench metric formulas (bench/harness/metrics.cpp)."""
+    a = (ctypes.c_double * max(1, len(args)))(*args)
+    out = ctypes.c_double()
+    check(lib.khrt_bench_metric(formula.encode(), a, len(args), ctypes.byref(out)))
+    return out.value
+
+
+def bench_row_work(kernel: str, shape: str) -> tuple[float, bool]:
+    """(work per launch, is_flops) of a `kernelh bench` row."""
+    w, f = ctypes.c_double(), _i()
+    check(lib.khrt_bench_row_work(kernel.encode(), shape.encode(), ctypes.byref(w), ctypes.byref(f)))
+    return w.value, bool(f.value)
 
 
 def scan_workspace_floats(n: int) -> int:

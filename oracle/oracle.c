@@ -187,6 +187,7 @@ KHO_API void kho_fill_gemm_int(float *A, float *B, long m, long n, long k) {
  * within 29 of each other, and rounds innocuously otherwise (53 >= 2*24+2),
  * so this equals the correctly rounded fp32 sum for all finite inputs. */
 KHO_API void kho_ref_vecadd(const float *a, const float *b, float *c, size_t n) {
+#pragma omp parallel for schedule(static) num_threads(g_threads)
   for (size_t i = 0; i < n; ++i) c[i] = (float)((double)a[i] + (double)b[i]);
 }
 

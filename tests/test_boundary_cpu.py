@@ -472,3 +472,91 @@ def test_gemm_candidate_errors_and_tune_cache_without_device(tmp_path):
             assert kh.launch_symbol("gemm", "m=8192,n=8192,k=8192") == "gemm"
         finally:
             kh.set_tune_cache(None)
+
+
+# ------------------------------------------------------------------ shape text
+
+@pytest.mark.parametrize("shape,why", [
+    ("", "a dimension at offset 0"),
+    ("n", "'=' after the dimension name at offset 1"),
+    ("=5", "a dimension name at offset 0"),
+    ("n=", "a decimal integer"),
+    ("n=5,", "a dimension name at offset 4"),
+    ("n=5x", "',' or the end after the integer at offset 3"),
+    ("n= 5", "a decimal integer"),
+    ("n=+-5", "a decimal integer"),
+    ("n=99999999999999999999", "a decimal integer in int64 range"),
+    ("n=4,,m=2", "a dimension name at offset 4"),
+])
+def test_shape_text_rejections_name_what_was_expected(shape, why):
+    with pytest.raises(kh.KhrtError) as e:
+        kh.geometry("vecadd", shape)
+    assert "malformed shape: expected " + why in e.value.message
+
+
+@pytest.mark.parametrize("shape", ["n=1024", "n=+1024", "m=1,n=1024", "n=7,n=1024"])
+def test_shape_text_accepts(shape):
+    """A sign, other dims, and a later dim replacing an earlier one."""
+    assert kh.geometry("vecadd", shape) == kh.geometry("vecadd", "n=1024")
+
+
+# ------------------------------------------------------------------ bench metrics
+
+# Hand-computed values of test/unit/bench_metrics_test.cpp:16-83, one per
+# REQUIRE, through the formulas the CLI's rate column uses.
+@pytest.mark.parametrize("formula,args,value", [
+    ("gflops_from_ms", (1073741824.0, 1.0), 1073.741824),
+    ("gflops_from_ms", (1e9, 1.0), 1000.0),
+    ("gflops_from_ms", (68719476736.0, 2.0), 34359.738368),
+    ("gbps_from_ms", (3.0 * (1 << 30), 6.0), 536.870912),
+    ("gemm_flops", (512, 512, 512), 268435456.0),
+    ("gemm_flops", (1024, 1024, 1024), 2147483648.0),
+    ("gemm_bytes", (512, 512, 512), 3145728.0),
+    ("elementwise_bytes", (4096, 1024), 33554432.0),
+    ("layernorm_bytes", (4096, 1024), 33562624.0),
+    ("scan_bytes", (100000,), 800000.0),
+    ("fused_gelu_bytes", (1048576,), 12582912.0),
+    ("attention_flops", (2, 8, 512, 64), 1073741824.0),
+    ("roofline_triad_bytes", (1 << 28,), 3221225472.0),
+    ("roofline_fma_flops", (1 << 35,), 68719476736.0),
+])
+def test_bench_metric_formulas_match_the_reference_pins(formula, args, value):
+    assert kh.bench_metric(formula, *args) == pytest.approx(value, rel=1e-12)
+
+
+def test_bench_metric_end_to_end_gemm_rate():
+    # 512^3 in 0.25 ms = 1073.741824 GFLOP/s (bench_metrics_test.cpp:78-83).
+    assert kh.bench_metric("gflops_from_ms", kh.bench_metric("gemm_flops", 512, 512, 512), 0.25) == \
+        pytest.approx(1073.741824, rel=1e-12)
+
+
+def test_bench_metric_errors():
+    with pytest.raises(kh.KhrtError, match="unknown formula"):
+        kh.bench_metric("vecadd_bytes", 1.0)
+    with pytest.raises(kh.KhrtError, match="takes 3 arguments, got 2"):
+        kh.bench_metric("gemm_flops", 1.0, 2.0)
+
+
+# Every kernelh row of the CLI's suites: its work is the reference formula
+# of its kernel at its shape (fused_gelu's 12 B per element counts the dead
+# tmp stream; layernorm adds 8 B per column for gamma and beta).
+@pytest.mark.parametrize("kernel,shape,value,flops", [
+    ("vecadd", "n=16777216", 12.0 * 16777216, False),
+    ("softmax", "rows=4096,cols=1024", 33554432.0, False),
+    ("layernorm", "rows=4096,cols=1024", 33562624.0, False),
+    ("layernorm", "rows=16384,cols=4096", 8.0 * 16384 * 4096 + 8.0 * 4096, False),
+    ("scan", "n=1000000", 8.0e6, False),
+    ("fused_gelu", "n=4194304", 12.0 * 4194304, False),
+    ("fused_gelu", "rows=64,cols=1024", 12.0 * 65536, False),
+    ("gemm", "m=8192,n=8192,k=256", 2.0 * 8192 * 8192 * 256, True),
+    ("attention", "batch=4,heads=16,seq=4096,head_dim=64", 4.0 * 4 * 16 * 4096 * 4096 * 64, True),
+    ("attention", "batch=2,heads=8,seq=512", 1073741824.0, True),
+    ("roofline_triad", "n=268435456", 3221225472.0, False),
+])
+def test_bench_row_work(kernel, shape, value, flops):
+    assert kh.bench_row_work(kernel, shape) == (pytest.approx(value, rel=1e-12), flops)
+
+
+def test_bench_row_work_needs_the_kernels_dims():
+    with pytest.raises(kh.KhrtError, match="no bench row for kernel 'softmax'"):
+        kh.bench_row_work("softmax", "n=1024")

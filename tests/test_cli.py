@@ -221,6 +221,34 @@ def test_tune_evaluates_candidates_and_caches(dev, tmp_path):
 
 
 @pytest.mark.gpu
+def test_tune_sampled_search(dev, tmp_path):
+    """--sample n evaluates n candidates in a fixed pseudo-random order, then
+    --refine-budget r at most r more, each one design step from the best
+    accepted one of the sample; the same flags give the same candidates."""
+    print("[gpu-case] kernelh tune gemm m=n=k=256 --sample 6 --refine-budget 3", flush=True)
+    shape = "m=256,n=256,k=256"
+    symbols = []
+    for rep in range(2):
+        out = tmp_path / f"r{rep}"
+        r = run("tune", "--shape", shape, "--out", str(out), "--sample", "6", "--refine-budget", "3",
+                "--timeout", "60", "--cache", str(tmp_path / f"cache{rep}.json"))
+        assert r.returncode == 0, r.stdout
+        rows = list(csv.DictReader(open(out / "tune-results.csv")))
+        assert 6 <= len(rows) <= 9 and len({row["symbol"] for row in rows}) == len(rows)
+        symbols.append([row["symbol"] for row in rows])
+        sample = rows[:6]
+        centre = min((row for row in sample if row["accepted"] == "true"), key=lambda row: float(row["ms_median"]))
+        assert f"refining around {centre['symbol']} with {len(rows) - 6} neighbour(s)" in r.stdout
+        axes = ("bm", "bn", "bk", "waves", "unroll", "mfma", "pipeline", "prio")
+        cand = {c["symbol"]: c for c in kh.gemm_candidates()}
+        for row in rows[6:]:
+            a, b = cand[row["symbol"]], cand[centre["symbol"]]
+            diffs = sum(a[x] != b[x] for x in axes) + (a["k_split"] != b["k_split"])
+            assert diffs == 1, (row["symbol"], centre["symbol"])
+    assert symbols[0] == symbols[1]
+
+
+@pytest.mark.gpu
 def test_tune_vec_column_follows_the_shape(dev, tmp_path):
     # k not a multiple of 4: every candidate takes its guarded scalar loads.
     print("[gpu-case] kernelh tune gemm m=100,n=100,k=33, 2 candidates", flush=True)
@@ -282,3 +310,98 @@ def test_cli_compiled_code_object_runs_under_reference_geometry(dev, tmp_path, k
         # the reference's HipBackend::launch_kernel does.
         kh.launch_raw(f, (T, 1, 1), (256, 1, 1), args)
         assert np.array_equal(down(dy, n), O.ref_scan(x).astype(np.float32))
+
+
+# ------------------------------------------------------------------ occupancy-only mode
+
+@pytest.mark.parametrize("kernel,shape", [("gemm", None), ("softmax", None), ("scan", None), ("attention", None),
+                                          ("vecadd", None), ("fused_gelu", None), ("layernorm", None),
+                                          ("gemm", "m=8192,n=8192,k=8192")])
+def test_bench_occupancy_only_mode(tmp_path, kernel, shape):
+    """`bench --occupancy --kernel <k> --target <t> [--shape] --out d` times
+    nothing and needs no device: exit 0 and occupancy.{json,md} for that one
+    kernel (run_bench.cpp:111-127), with the reference's report keys
+    (occupancy.cpp:90-110) at the reference's default shapes
+    (kernelh_backend.cpp:447-469) unless --shape names one."""
+    import json
+    args = ["bench", "--occupancy", "--kernel", kernel, "--target", "amdgcn-gfx950", "--out", str(tmp_path)]
+    if shape:
+        args += ["--shape", shape]
+    r = run(*args)
+    assert r.returncode == 0, r.stdout
+    assert f"wrote {tmp_path}/occupancy.json + occupancy.md ({kernel}, amdgcn-gfx950)" in r.stdout
+    rep = json.loads((tmp_path / "occupancy.json").read_text())
+    for key in ("kernel", "target", "config", "vgpr_count", "lds_bytes", "threads_per_workgroup",
+                "vgpr_limited_waves", "lds_limited_blocks", "thread_limited_blocks", "theoretical_waves",
+                "theoretical_pct", "limiter", "measured_blocks", "measured_pct", "measured_note"):
+        assert key in rep, key
+    defaults = {"gemm": "m=512,n=512,k=512", "softmax": "rows=4096,cols=1024", "scan": "n=100000",
+                "attention": "batch=2,heads=8,seq=512,head_dim=64", "vecadd": "n=1024",
+                "fused_gelu": "n=1048576", "layernorm": "rows=4096,cols=1024"}
+    assert rep["kernel"] == kernel and rep["target"] == "amdgcn-gfx950"
+    assert rep["config"] == (shape or defaults[kernel])
+    # The symbol the launcher runs at that shape, with its own resources and
+    # workgroup size, through the pinned formulas.
+    sym = kh.launch_symbol(kernel, rep["config"])
+    res = kh.resources(sym)
+    grid, block = kh.geometry(kernel, rep["config"])
+    assert rep["symbol"] == sym
+    assert rep["vgpr_count"] == res["vgpr_count"] + res["agpr_count"] and rep["lds_bytes"] == res["lds_bytes"]
+    assert rep["threads_per_workgroup"] == block[0] * block[1] * block[2]
+    ref = kh.occupancy(rep["vgpr_count"], rep["lds_bytes"], rep["threads_per_workgroup"])
+    assert rep["theoretical_waves"] == ref.achieved_waves
+    if kh.device_count() == 0:
+        assert rep["measured_blocks"] == -1 and "analytic only" in rep["measured_note"]
+    md = (tmp_path / "occupancy.md").read_text()
+    assert f"| {kernel} | {rep['config']} | {sym} |" in md
+
+
+def test_bench_occupancy_only_threads_override(tmp_path):
+    r = run("bench", "--occupancy", "--kernel", "attention", "--target", "amdgcn-gfx950", "--threads", "64",
+            "--out", str(tmp_path))
+    assert r.returncode == 0, r.stdout
+    import json
+    rep = json.loads((tmp_path / "occupancy.json").read_text())
+    assert rep["threads_per_workgroup"] == 64
+    assert rep["thread_limited_blocks"] == 1024 // 64
+
+
+@pytest.mark.parametrize("args,code,msg", [
+    (["--occupancy", "--kernel", "gemm", "--target", "amdgcn-gfx1101"], 2, "unknown --target 'amdgcn-gfx1101'"),
+    (["--occupancy", "--kernel", "gemm", "--target", "amdgcn-gfx950", "--threads", "0"], 2,
+     "--threads must be an integer in [1,1048576]"),
+    (["--occupancy", "--kernel", "gemm", "--target", "amdgcn-gfx950", "--threads", "1048577"], 2,
+     "--threads must be an integer in [1,1048576]"),
+    (["--occupancy", "--kernel", "gemm", "--target", "amdgcn-gfx950", "--shape", "m=8,n"], 2, "malformed --shape"),
+    (["--target", "amdgcn-gfx950"], 2, "--target/--threads require --occupancy"),
+    (["--threads", "64"], 2, "--target/--threads require --occupancy"),
+    (["--occupancy", "--kernel", "gemm"], 2, "--target amdgcn-gfx950"),
+    (["--occupancy", "--kernel", "conv2d", "--target", "amdgcn-gfx950"], 1, "no default shape"),
+    (["--occupancy", "--kernel", "gemm", "--target", "amdgcn-gfx950", "--shape", "m=8"], 1, "required"),
+])
+def test_bench_occupancy_only_errors(tmp_path, args, code, msg):
+    r = run("bench", *args, "--out", str(tmp_path))
+    assert r.returncode == code, r.stdout
+    assert msg in r.stdout
+
+
+# ------------------------------------------------------------------ tune search flags
+
+@pytest.mark.parametrize("flag,value", [("--sample", "0"), ("--sample", "217"), ("--sample", "x"),
+                                        ("--refine-budget", "-1"), ("--refine-budget", "81"),
+                                        ("--max-candidates", "0"), ("--timeout", "3601")])
+def test_tune_flag_ranges_exit_2(tmp_path, flag, value):
+    r = run("tune", "--shape", "m=64,n=64,k=64", "--out", str(tmp_path), flag, value)
+    assert r.returncode == 2
+    assert f"error: {flag} must be an integer in [" in r.stdout
+
+
+def test_tune_search_flags_accepted(tmp_path):
+    """The reference's documented search flags (main.cpp:704-730) in range:
+    never a usage error; without a device the run skips with 77."""
+    for extra in (["--sample", "1"], ["--sample", "216"], ["--refine-budget", "0"], ["--refine-budget", "80"],
+                  ["--sample", "20", "--refine-budget", "4", "--max-candidates", "24"]):
+        r = run("tune", "--kernel", "gemm", "--shape", "m=64,n=64,k=64", "--out", str(tmp_path), *extra)
+        assert r.returncode in (0, 77), (extra, r.stdout)
+        if kh.device_count() == 0:
+            assert r.returncode == 77 and "skip: no HIP device" in r.stdout
