@@ -315,6 +315,7 @@ def _shortspin_scan():
 def test_scan_lookback_gives_up_on_a_missing_record(dev):
     """A signed header whose counter skips tile 0's ticket: tile 0 is never
     handed out, so tile 1's look-back waits for a record that never comes.
+    (Half as many workgroups as tiles, so that tiles go by ticket.)
     With the test build's short bounded wait it gives up: every later tile
     is NaN, tile 0's elements are untouched, the header counts the failure,
     every workgroup exits, and the call still closes, so the next call on
@@ -331,17 +332,19 @@ def test_scan_lookback_gives_up_on_a_missing_record(dev):
     _forge_totals_lo(tl, T, base, nonce, _header_check(tl.ptr, base, nonce), counter=first + 1)
     _m, f = _shortspin_scan()
     dy = empty(n, 0.25)
-    say(f"scan short-spin look-back give-up n={n} grid={ntiles}x1024")
-    kh.launch_raw(f, (ntiles, 1, 1), (1024, 1, 1), _scan_args(dx, dy, empty(1, None), th, tl, n, T))
+    grid = ntiles // 2
+    say(f"scan short-spin look-back give-up n={n} grid={grid}x1024")
+    kh.launch_raw(f, (grid, 1, 1), (1024, 1, 1), _scan_args(dx, dy, empty(1, None), th, tl, n, T))
     got = down(dy, n)
     assert np.all(got[:tile] == 0.25)
     assert np.all(np.isnan(got[tile:]))
     assert _failed(tl) >= 1
     g = kh.GpuModule(kh.code_object("scan")).get_function("scan")
-    dy = empty(n)
-    say("scan after a give-up: same buffers, product code object")
-    kh.launch_raw(g, (ntiles, 1, 1), (1024, 1, 1), _scan_args(dx, dy, empty(1, None), th, tl, n, T))
-    assert np.array_equal(down(dy, n), ref)
+    for grid in (ntiles // 2, ntiles):  # tiles by ticket, then by workgroup index
+        dy = empty(n)
+        say(f"scan after a give-up: same buffers, product code object, grid={grid}")
+        kh.launch_raw(g, (grid, 1, 1), (1024, 1, 1), _scan_args(dx, dy, empty(1, None), th, tl, n, T))
+        assert np.array_equal(down(dy, n), ref)
 
 
 def test_scan_takes_over_a_stale_claim(dev):
