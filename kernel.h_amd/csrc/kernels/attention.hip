@@ -191,7 +191,7 @@ template <bool VEC4>
 __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, const float *__restrict__ Kg,
                                                 const float *__restrict__ Vg, float *__restrict__ Og, int64_t qs,
                                                 int64_t ks, int64_t vs, int64_t os, int64_t seq, int bd,
-                                                int64_t nblocks, float *Ks, float *Vt) {
+                                                int64_t q0, int64_t qstep, float *Ks, float *Vt) {
   const int tid = threadIdx.x;
   const int lane = kh::lane_id();
   const int wave = tid / kh::kWave;
@@ -212,7 +212,7 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
                                                                       (int)(seq * ks * 4), 0x00020000);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(Vg), (short)0,
                                                                       (int)(seq * vs * 4), 0x00020000);
-  for (int64_t qt = blockIdx.x; qt < nqt; qt += nblocks) {
+  for (int64_t qt = q0; qt < nqt; qt += qstep) {
     const int64_t q_row = qt * rows_per_block + (int64_t)wave * QW + r;
     // The fast path's K0 goes out before Q: its copy into LDS waits for K0
     // alone, and tile 0's S^T then takes Q's fragments as they land.
@@ -366,7 +366,31 @@ attention(KH_MEMREF4(const float, Q), KH_MEMREF4(const float, K), KH_MEMREF4(con
     }
     return;
   }
-  const int64_t hb = blockIdx.y, bb = blockIdx.z;
+  // Which slice and query tiles this workgroup takes: slice (blockIdx.z,
+  // blockIdx.y), query tiles blockIdx.x, + gridDim.x, ... (any grid). Under
+  // the launcher's grid (one workgroup per 128-row query tile of each
+  // slice, slices a multiple of 8), the flat workgroup index L is remapped
+  // instead so that the query tiles of a slice share an XCD: consecutive
+  // workgroups go round-robin to the 8 XCDs, each with its own L2, so with
+  // x the query tile a slice's tiles ran on 8 XCDs and each XCD's L2
+  // fetched the slice's K and V again (HBM reads 5.7x the algorithmic K
+  // and V at seq 1024). Slice = 8 (L / 8 / tiles) + L % 8, tile = (L / 8)
+  // % tiles: workgroups L and L + 8 share an XCD and, mostly, a slice.
+  int64_t hb = blockIdx.y, bb = blockIdx.z, q0 = blockIdx.x, qstep = bcx;
+  {
+    const int64_t tiles = (seq + KH_ATTN_BLOCK_Q - 1) / KH_ATTN_BLOCK_Q;
+    const int64_t slices = heads * Q_n0;
+    const uint32_t gy = kh::grid_blocks_y(), gz = kh::grid_blocks_z();
+    if (kh::threads_x_of(gxy) == kFastThreads && (int64_t)bcx == tiles && (int64_t)gy == heads &&
+        (int64_t)gz == Q_n0 && (slices & 7) == 0 && slices * tiles < (1ll << 31)) {
+      const uint32_t L = (blockIdx.z * gy + blockIdx.y) * bcx + blockIdx.x;
+      const uint32_t j = L >> 3, slice = (uint32_t)(j / tiles) * 8 + (L & 7);
+      q0 = j % tiles;
+      qstep = tiles;  // one tile per workgroup
+      hb = slice % heads;
+      bb = slice / heads;
+    }
+  }
   if (hb >= heads || bb >= Q_n0) return;
   // Row stride of the [s, d] slice is s2 (d contiguous, s3 == 1).
   const float *__restrict__ Qg = Qp + bb * Q_s0 + hb * Q_s1;
@@ -381,7 +405,8 @@ attention(KH_MEMREF4(const float, Q), KH_MEMREF4(const float, K), KH_MEMREF4(con
   const bool vec4 = kh::aligned16(Qp) & kh::aligned16(Kp) & kh::aligned16(Vp) & kh::aligned16(Op) &
                     (((Q_s0 | Q_s1 | Q_s2 | K_s0 | K_s1 | K_s2 | V_s0 | V_s1 | V_s2 | O_s0 | O_s1 | O_s2) & 3) == 0);
   if (vec4)
-    attention_slice<true>(Qg, Kg, Vg, Og, Q_s2, K_s2, V_s2, O_s2, seq, (int)kh::threads_x_of(gxy), bcx, Ks, Vt);
+    attention_slice<true>(Qg, Kg, Vg, Og, Q_s2, K_s2, V_s2, O_s2, seq, (int)kh::threads_x_of(gxy), q0, qstep, Ks, Vt);
   else
-    attention_slice<false>(Qg, Kg, Vg, Og, Q_s2, K_s2, V_s2, O_s2, seq, (int)kh::threads_x_of(gxy), bcx, Ks, Vt);
+    attention_slice<false>(Qg, Kg, Vg, Og, Q_s2, K_s2, V_s2, O_s2, seq, (int)kh::threads_x_of(gxy), q0, qstep, Ks,
+                           Vt);
 }
