@@ -300,29 +300,64 @@ static float acc_round_f32(const uint64_t *acc) {
   }
   return neg ? -r : r;
 }
-KHO_API void kho_ref_scan_exact(const float *x, float *y, size_t n, double *acc_abs) {
+/* The long accumulator's value as a double (rounded once, to nearest). */
+static double acc_to_double(const uint64_t *acc) {
+  uint64_t m[KHO_LIMBS];
+  memcpy(m, acc, sizeof m);
+  const int neg = (int)(m[KHO_LIMBS - 1] >> 63);
+  if (neg) acc_neg(m);
+  /* sum the limbs from the top: the leading ~2 limbs carry the value; the
+     rounding of this sum is far below what the callers resolve */
+  double v = 0.0;
+  for (int i = KHO_LIMBS - 1; i >= 0; --i) v += ldexp((double)m[i], 64 * i - 149);
+  return neg ? -v : v;
+}
+
+/* x as a long-accumulator integer in units of 2^-149 (x finite). */
+static void acc_from_float(float x, uint64_t *t) {
+  uint32_t bits;
+  memcpy(&bits, &x, 4);
+  const uint32_t ebits = (bits >> 23) & 0xffu;
+  uint64_t mant = bits & 0x7fffffu;
+  int shift = 0; /* x = mant * 2^(shift - 149) */
+  if (ebits != 0) {
+    mant |= 0x800000u;
+    shift = (int)ebits - 1;
+  }
+  memset(t, 0, sizeof(uint64_t) * KHO_LIMBS);
+  const int limb = shift >> 6, off = shift & 63;
+  t[limb] = mant << off;
+  if (off > 40 && limb + 1 < KHO_LIMBS) t[limb + 1] = mant >> (64 - off);
+  if (bits >> 31) acc_neg(t);
+}
+
+/* `margin` (optional): for each prefix, how far the exact value P lies from
+ * the nearest boundary where its fp32 rounding r would change,
+ * min(spacing below r, spacing above r) / 2 - |P - r|, in fp64 (relative
+ * error ~2^-52 of |P|). An approximation S of P with |S - P| < margin rounds
+ * to r too. */
+KHO_API void kho_ref_scan_exact(const float *x, float *y, size_t n, double *acc_abs, double *margin) {
   uint64_t acc[KHO_LIMBS] = {0};
   double sabs = 0.0;
   for (size_t i = 0; i < n; ++i) {
-    uint32_t bits;
-    memcpy(&bits, &x[i], 4);
-    const uint32_t ebits = (bits >> 23) & 0xffu;
-    uint64_t mant = bits & 0x7fffffu;
-    int shift = 0;  /* x = mant * 2^(shift - 149) */
-    if (ebits != 0) {
-      mant |= 0x800000u;
-      shift = (int)ebits - 1;
-    }
-    uint64_t t[KHO_LIMBS] = {0};
-    const int limb = shift >> 6, off = shift & 63;
-    t[limb] = mant << off;
-    if (off > 40 && limb + 1 < KHO_LIMBS) t[limb + 1] = mant >> (64 - off);
-    if (bits >> 31) acc_neg(t);
+    uint64_t t[KHO_LIMBS];
+    acc_from_float(x[i], t);
     acc_add(acc, t);
     y[i] = acc_round_f32(acc);
     if (acc_abs) {
       sabs += fabs((double)x[i]);
       acc_abs[i] = sabs;
+    }
+    if (margin) {
+      /* residual P - r, exactly in the accumulator, then as a double */
+      uint64_t res[KHO_LIMBS], r[KHO_LIMBS];
+      memcpy(res, acc, sizeof res);
+      acc_from_float(y[i], r);
+      acc_neg(r);
+      acc_add(res, r);
+      const double below = (double)y[i] - (double)nextafterf(y[i], -INFINITY);
+      const double above = (double)nextafterf(y[i], INFINITY) - (double)y[i];
+      margin[i] = 0.5 * (below < above ? below : above) - fabs(acc_to_double(res));
     }
   }
 }

@@ -81,7 +81,7 @@ def lib():
             "kho_ref_softmax": (None, [_f32p, _f64p, c.c_long, c.c_long, c.c_long]),
             "kho_ref_layernorm": (None, [_f32p, _f32p, _f32p, c.c_double, _f64p, c.c_long, c.c_long, c.c_long]),
             "kho_ref_scan": (None, [_f32p, _f32p, c.c_size_t, c.c_int]),
-            "kho_ref_scan_exact": (None, [_f32p, _f32p, c.c_size_t, c.c_void_p]),
+            "kho_ref_scan_exact": (None, [_f32p, _f32p, c.c_size_t, c.c_void_p, c.c_void_p]),
             "kho_ref_gelu": (None, [_f32p, _f64p, c.c_size_t, c.c_int]),
             "kho_ref_gemm": (None, [_f32p, _f32p, _f64p, c.c_long, c.c_long, c.c_long, c.c_long, c.c_long, c.c_int]),
             "kho_ref_attention_rows": (None, [_f32p, _f32p, _f32p, _f64p, c.c_long, c.c_long, c.c_int, _i64p, _i64p, c.c_long]),
@@ -192,14 +192,20 @@ def ref_scan(x, exclusive: bool = False) -> np.ndarray:
     return y
 
 
-def ref_scan_exact(x, with_abs: bool = False):
+def ref_scan_exact(x, with_abs: bool = False, with_margin: bool = False):
     """Correctly rounded fp32 inclusive prefix (exact long accumulator).
-    With with_abs, also returns the fp64 running sum of |x|."""
+    With with_abs, also returns the fp64 running sum of |x|; with
+    with_margin, each prefix's distance from the nearest point where its
+    fp32 rounding would change (min(spacing below, spacing above)/2 minus
+    |exact - rounded|)."""
     x = _c32(x)
     y = np.empty_like(x)
     a = np.empty(x.size, np.float64) if with_abs else None
-    lib().kho_ref_scan_exact(x, y, x.size, a.ctypes.data if with_abs else None)
-    return (y, a) if with_abs else y
+    m = np.empty(x.size, np.float64) if with_margin else None
+    lib().kho_ref_scan_exact(x, y, x.size, a.ctypes.data if with_abs else None,
+                             m.ctypes.data if with_margin else None)
+    out = (y,) + ((a,) if with_abs else ()) + ((m,) if with_margin else ())
+    return out if len(out) > 1 else y
 
 
 def ref_gelu(x, with_tanh: bool = True) -> np.ndarray:

@@ -203,6 +203,29 @@ def test_scan_exact_reference_vs_rationals():
     assert np.array_equal(O.ref_scan_exact(g), O.ref_scan(g))
 
 
+def test_scan_exact_margin_vs_rationals():
+    """The exact scan's margin (how far each exact prefix P lies from where
+    its fp32 rounding r would change: min(spacing below r, spacing above
+    r) / 2 - |P - r|) against exact rational arithmetic, on wide-exponent
+    inputs, cancellation and hand-made ties (a tie has margin <= 0)."""
+    rng = np.random.default_rng(11)
+    wide = (rng.standard_normal(800) * np.exp2(rng.integers(-30, 40, 800).astype(np.float64))).astype(np.float32)
+    ties = np.array([1.0, 2.0 ** -24, -1.0, -(2.0 ** -24), 3.0, 2.0 ** -22, 2.0 ** -60, -3.0], np.float32)
+    for x in (wide, ties):
+        y, m = O.ref_scan_exact(x, with_margin=True)
+        acc = Fraction(0)
+        for i, v in enumerate(x):
+            acc += Fraction(float(v))
+            r = np.float32(y[i])
+            below = Fraction(float(r)) - Fraction(float(np.nextafter(r, np.float32(-np.inf))))
+            above = Fraction(float(np.nextafter(r, np.float32(np.inf)))) - Fraction(float(r))
+            want = min(below, above) / 2 - abs(acc - Fraction(float(r)))
+            scale = max(abs(acc), min(below, above))
+            assert abs(Fraction(float(m[i])) - want) <= scale * Fraction(1, 2 ** 50), (i, float(m[i]), float(want))
+    _, m = O.ref_scan_exact(ties, with_margin=True)
+    assert m[1] < 0  # 1 + 2^-24: exactly halfway to 1 + 2^-23
+
+
 def test_scan_reference_vs_numpy_and_exclusive():
     x = O.uniform(1 << 20, 42, 0.0, 1.0)
     y = O.ref_scan(x)
