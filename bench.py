@@ -20,8 +20,8 @@ from HBM rather than the 256 MB Infinity Cache.
 Roofline: `achieved` = algorithmic bytes (or FLOPs) per launch / average
 launch duration; `peak` = MI355X published peak (HBM 8 TB/s; fp32 MFMA
 157.3 TFLOP/s). The measured HBM ceiling of a kernel is the best of copy and
-triad streams at 3 GiB and at that kernel's own bytes per launch (rotated
-the same way), each with the product's streaming geometry and with a
+triad streams of 2^28 floats (2 and 3 GiB) and at that kernel's own bytes
+per launch (rotated the same way), each with the product's streaming geometry and with a
 32-workgroups-per-CU grid. The CPU baseline times the oracle's fp64
 references on a bounded sample on this host.
 """
@@ -52,9 +52,9 @@ METRIC = "GEMM-8192 fp32 TFLOPS + softmax/scan HBM GB/s, % of MI355X roofline"
 # profiles/templates_baseline_sizes_hbm_traffic.md. Constants of that profile
 # (median dispatch), not measured by the run that reports them.
 PMC_TRAFFIC_BYTES = {
-    "vecadd": 201380160, "softmax": 33662464, "layernorm": 33725184, "scan": 539207872, "scan_1e6": 8272864,
-    "fused_gelu": 536954176, "fused_gelu_2^22": 33636480, "gemm": 3814877312, "gemm_8192x8192x256": 380331648,
-    "gemm_2048": 117560832, "gemm_512": 10650624, "attention": 1208263040, "attention_s1024": 302283392,
+    "vecadd": 201371645, "softmax": 33660954, "layernorm": 33723990, "scan": 539240514, "scan_1e6": 8202141,
+    "fused_gelu": 536931644, "fused_gelu_2^22": 33639323, "gemm": 3803504387, "gemm_8192x8192x256": 379226985,
+    "gemm_2048": 117554553, "gemm_512": 10650028, "attention": 268723951, "attention_s1024": 67397775,
 }
 PMC_TRAFFIC_SOURCE = "profiles/templates_baseline_sizes_hbm_traffic.md (constant, not measured by this run)"
 
@@ -208,13 +208,14 @@ def measure_ceilings(kh, stream, hbm_cases, prime, steps):
 
     HBM: plain copy (8 B/float) and triad (12 B/float) streams, the
     reference's roofline_triad pattern (bench/refs/roofline.hip:22-30, 2^28
-    floats: 3 GiB per launch, beyond the 256 MB MALL) plus copies and triads
+    floats: 2 GiB per copy launch, 3 GiB per triad launch, beyond the
+    256 MB MALL) plus copies and triads
     of exactly each HBM kernel's bytes per launch, rotated like that
     kernel's buffers. Each runs under two geometries: the product streaming
     kernels' (one unrolled step per thread, ceil(n/4/1024) workgroups of
     256) and 32 grid-strided workgroups per CU, each the best of five
-    sequences. A kernel's ceiling is the best of the 3 GiB streams and its
-    own-size streams.
+    sequences. A kernel's ceiling is the best of the 2^28-float streams and
+    its own-size streams.
 
     fp32 MFMA: independent chains of each fp32 MFMA shape (8 of 32x32x2 or
     16 of 16x16x4 per wave), two waves per SIMD, ~3.5 ms per launch (shorter
@@ -288,7 +289,9 @@ def measure_ceilings(kh, stream, hbm_cases, prime, steps):
         best = min(time_queued(kh, stream, [call] * 10, prime) for _ in range(3))
         mfma_rates[name] = flops / (best * 1e-3) / 1e12
     out.free()
-    return {"hbm_3GiB_best_gbps": big_best, "hbm_3GiB_streams": big_rows, "hbm_per_kernel": per_case,
+    return {"hbm_2e28_floats_best_gbps": big_best, "hbm_2e28_floats_streams": big_rows,
+            "hbm_2e28_floats_note": "copy 2^28 floats (2 GiB per launch) and triad 2^28 floats (3 GiB)",
+            "hbm_per_kernel": per_case,
             "fp32_mfma_tflops": max(mfma_rates.values()), "fp32_mfma_by_instruction": mfma_rates,
             "mfma_config": f"{blocks} workgroups x 4 waves x {iters} rounds of independent chains "
                            "(8 of 32x32x2 or 16 of 16x16x4 per wave), best of 3 sequences of 10 launches"}
@@ -537,7 +540,7 @@ def main() -> int:
     ceilings = None
     if not a.no_ceilings:
         ceilings = measure_ceilings(kh, stream, [c for c in cases if c.bound == "hbm"], prime, a.steps)
-        log(f"[bench] measured ceilings: HBM streams at 3 GiB {ceilings['hbm_3GiB_best_gbps']:.0f} GB/s, "
+        log(f"[bench] measured ceilings: HBM streams of 2^28 floats {ceilings['hbm_2e28_floats_best_gbps']:.0f} GB/s, "
             f"fp32 MFMA {ceilings['fp32_mfma_tflops']:.1f} TFLOP/s")
     vendor = {}
     gemm_cases = [c for c in cases if c.gemm_shape]
@@ -564,7 +567,8 @@ def main() -> int:
             else:
                 pc = ceilings["hbm_per_kernel"][c.name]
                 k["measured_ceiling"] = pc["gbps"]
-                k["measured_ceiling_source"] = ("best of copy/triad streams at 3 GiB and at this kernel's "
+                k["measured_ceiling_source"] = ("best of copy/triad streams of 2^28 floats (2 and 3 GiB) and at "
+                                                "this kernel's "
                                                 f"{int(c.work)} B per launch (own size best {pc['own_size_best']:.0f})")
             k["frac_of_measured"] = rate / k["measured_ceiling"]
         if c.name in PMC_TRAFFIC_BYTES:

@@ -12,8 +12,9 @@
 //   z = 0.7978845608 (t + 0.044715 t^3)
 //   out = 0.5 t (1 + tanh z)
 // tanh is evaluated from the identity 1 + tanh z = 2 - 2 / (1 + e^{2z}),
-// with e^{2z} = 2^{2 z log2 e} on v_exp_f32 and an IEEE reciprocal-based
-// division; e^{2z} overflowing to +inf gives exactly 2, underflowing to 0
+// with e^{2z} = 2^{2 z log2 e} on v_exp_f32 and the division as a multiply
+// by v_rcp_f32 (the hardware's approximate reciprocal, 1 ulp); e^{2z}
+// overflowing to +inf gives exactly 2 (rcp(inf) = 0), underflowing to 0
 // gives exactly 0, so the formula is finite for every finite input. The
 // absolute error of out is a few fp32 ulps of |t|, far inside the 1e-4
 // fp64-reference tolerance (e2e_fused_gelu_test.cpp:63).
