@@ -174,12 +174,27 @@ gemm_wide(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(flo
 // 512^3 28-30 vs 18.0 TFLOP/s, 512x512x2048 37-41 vs 22, 256^3 6.3-6.5 vs
 // 3.8. Four waves per workgroup reached 22 at 512^3; sixteen spilled, and
 // so did loading 8 groups per batch (6 groups: slower at every shape).
+//
+// Where every tile is whole and every wave's K chunk a whole number of
+// batches (M, N multiples of 32, K of 128, 512 threads: the BASELINE 512^3),
+// the kernel takes a path of its own before the general one (ks_interior):
+// buffer loads with one offset register per operand and lane and the k step
+// in the scalar offset, none of them conditional. In the general path the
+// compiler turns each "clamped load, then select 0" into a branch around the
+// load and waits for it where the branches join, so a wave's loads went out
+// one at a time. Kernel trace, rotated inputs, same bits: 512^3 9.8 -> 6.2
+// us, 512x512x1024 16.4 -> 9.0, 256^3 5.7 -> 4.5; and, in the deep symbol,
+// 512x512x2048 25.6 -> 14.4, 512x512x8192 82 -> 49. Batches of 2 groups,
+// two sets in flight, measured best (4 groups: 6.8 us at 512^3, 8: 7.7;
+// three sets: 6.7).
 namespace {
 
 using khg::v16f;
+using kh::u32x4_t;
 constexpr int kKsTile = KH_GEMM_KSPLIT_BM;
 constexpr int kKsMaxWaves = KH_GEMM_KSPLIT_THREADS / 64;
 constexpr int kKsBatch = 4;  // groups of 8 k loaded ahead per batch
+constexpr int kKsFastBatch = 2;  // the same, in ks_interior
 static_assert(KH_GEMM_KSPLIT_BM == 32 && KH_GEMM_KSPLIT_BN == 32, "one 32x32 MFMA accumulator per wave");
 
 // Loads one group of 8 k for this lane: k is the lane's first k of the
@@ -317,6 +332,90 @@ __device__ __forceinline__ void gemm_ksplit_body(const float *__restrict__ A, co
   }
 }
 
+// A uniform pointer, forced into scalar registers: its computation may run
+// on the vector ALU (the 64-bit multiply of a row index), and a buffer
+// resource built from vector registers costs a loop around every load.
+template <typename T>
+__device__ __forceinline__ T *uniform_ptr(T *p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<T *>(((uint64_t)hi << 32) | lo);
+}
+
+// The K split for launches whose tiles are all whole: M, N multiples of 32,
+// K of 8 * kKsFastBatch * 8, eight waves, and every byte offset below 2^31
+// (ks_interior_ok). The operands and groups are those of gemm_ksplit_body;
+// lane (r, h) reads A from one offset register plus 32 bytes per group (the
+// instruction's immediate) and B from one offset register plus a row step
+// in the scalar offset. Same reduction, so the same bits.
+__device__ __forceinline__ bool ks_interior_ok(int bd, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                                               int64_t ldc, const float *A) {
+  constexpr int64_t kLim = int64_t(1) << 29;
+  return bd == KH_GEMM_KSPLIT_THREADS && M > 0 && N > 0 && (M & 31) == 0 && (N & 31) == 0 && K > 0 &&
+         K % (64 * kKsFastBatch) == 0 && (lda & 3) == 0 && kh::aligned16(A) && M <= kLim && N <= kLim &&
+         31 * lda + K / 8 <= kLim && K * ldb <= kLim && ldc <= kLim && (M >> 5) * (N >> 5) < (int64_t(1) << 31);
+}
+
+__device__ __forceinline__ void ks_interior(const float *__restrict__ A, const float *__restrict__ B,
+                                            float *__restrict__ C, int M, int N, int K, int lda, int ldb, int ldc,
+                                            int nblocks, float *red) {
+  constexpr int nw = kKsMaxWaves, NB = kKsFastBatch;
+  const int lane = kh::lane_id(), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kh::kWave);
+  const int r = lane & 31, h = lane >> 5;
+  const int tiles_n = N / kKsTile, total = (M / kKsTile) * tiles_n;
+  const int kc = K / nw, kb = wave * kc, nbat = kc / (8 * NB);
+  const uint32_t va = (uint32_t)(4 * (r * lda + 4 * h)), vb = (uint32_t)(4 * (4 * h * ldb + r));
+  const uint32_t bstep = (uint32_t)(4 * ldb);
+  const uint32_t abytes = (uint32_t)(4 * (31 * lda + kc)), bbytes = (uint32_t)(4 * ((kc - 1) * ldb + kKsTile));
+  struct Set {
+    float4 a[NB];
+    float b[NB][4];
+  };
+  for (int t = blockIdx.x; t < total; t += nblocks) {
+    const int m0 = __builtin_amdgcn_readfirstlane((t / tiles_n) * kKsTile);
+    const int n0 = __builtin_amdgcn_readfirstlane((t % tiles_n) * kKsTile);
+    const __amdgpu_buffer_rsrc_t ra = kh::span_rsrc(uniform_ptr(A + (int64_t)m0 * lda + kb), abytes);
+    const __amdgpu_buffer_rsrc_t rb = kh::span_rsrc(uniform_ptr(B + (int64_t)kb * ldb + n0), bbytes);
+    v16f acc = {};
+    Set s0, s1;
+    auto load = [&](Set &s, int j) {
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const int g = j * NB + i;
+        const u32x4_t u = __builtin_amdgcn_raw_buffer_load_b128(ra, va, (uint32_t)(32 * g), 0);
+        s.a[i] = make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          s.b[i][q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, vb, (uint32_t)(8 * g + q) * bstep, 0));
+      }
+    };
+    auto math = [&](const Set &s) {
+#pragma unroll
+      for (int i = 0; i < NB; ++i) ks_mfma(acc, s.a[i], s.b[i]);
+    };
+    // Two sets in flight: batch j + 1's loads go out before batch j's MFMAs.
+    load(s0, 0);
+    for (int j = 0; j < nbat; j += 2) {
+      if (j + 1 < nbat) load(s1, j + 1);
+      math(s0);
+      if (j + 2 < nbat) load(s0, j + 2);
+      if (j + 1 < nbat) math(s1);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) red[(wave * 16 + i) * kh::kWave + lane] = acc[i];
+    kh::lds_barrier();
+#pragma unroll
+    for (int i = wave; i < 16; i += nw) {
+      float s = red[i * kh::kWave + lane];
+#pragma unroll
+      for (int w = 1; w < nw; ++w) s += red[(16 * w + i) * kh::kWave + lane];
+      C[(int64_t)(m0 + 8 * (i >> 2) + 4 * h + (i & 3)) * ldc + n0 + r] = s;
+    }
+    kh::lds_barrier();
+  }
+}
+
 }  // namespace
 
 template <bool DEEP>
@@ -341,8 +440,14 @@ __device__ __forceinline__ void gemm_ksplit_entry(const float *Ap, const float *
 // at 512^3 the launch is ~10 us, and every serial round trip to
 // kernel-argument memory before the first operand load is part of it.
 #define KH_KSPLIT_ENTRY(DEEP)                                                                                  \
-  const uint32_t gw = kh::group_size_word(), nb = kh::grid_blocks_x();                                       \
-  KH_ARGS_READY(A_base, A_off, A_n0, A_n1, A_s0, B_base, B_off, B_n1, B_s0, C_base, C_off, C_s0, gw, nb);    \
+  const uint32_t gw = kh::group_size_word(), gz = kh::group_size_z_word(), nb = kh::grid_blocks_x();          \
+  KH_ARGS_READY(A_base, A_off, A_n0, A_n1, A_s0, B_base, B_off, B_n1, B_s0, C_base, C_off, C_s0, gw, gz, nb); \
+  if (kh::threads_y_of(gw) == 1 && kh::threads_z_of(gz) == 1 &&                                               \
+      ks_interior_ok((int)kh::threads_x_of(gw), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0, KH_PTR(A))) {             \
+    ks_interior(KH_PTR(A), KH_PTR(B), KH_PTR(C), (int)A_n0, (int)B_n1, (int)A_n1, (int)A_s0, (int)B_s0,       \
+                (int)C_s0, (int)nb, red);                                                                    \
+    return;                                                                                                   \
+  }                                                                                                           \
   gemm_ksplit_entry<DEEP>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0,                \
                           (int)kh::threads_x_of(gw), nb, red)
 

@@ -158,6 +158,41 @@ def test_gemm_symbols_random_shapes_exact(dev):
             assert np.array_equal(down(dC, m * n).reshape(m, n), want), (sym, m, n, k, grid)
 
 
+@pytest.mark.parametrize("sym", ["gemm_ksplit", "gemm_ksplit_deep"])
+@pytest.mark.parametrize("m,n,k,grid", [
+    (32, 32, 128, 1),       # one tile, one batch per wave
+    (96, 64, 384, 5),       # three batches per wave (an odd count)
+    (512, 512, 512, 256),   # the BASELINE launch
+    (256, 480, 1152, 37),   # 120 tiles over 37 workgroups
+    (64, 2048, 2048, 64),   # deep K
+    (512, 512, 192, 256),   # K not a multiple of 128: the general path
+    (500, 512, 512, 256),   # M not a multiple of 32: the general path
+])
+def test_gemm_ksplit_interior_path(dev, sym, m, n, k, grid):
+    """The K-split symbols at 512 threads on shapes whose tiles are all whole
+    (M, N multiples of 32, K of 128: unconditional buffer loads), and on two
+    that are not, with padded rows: A's rows k + 4 floats apart, B's n + 1,
+    C's n + 3, every pad holding NaN. The result must equal the exact
+    integer product bit for bit, and no pad may be read (NaN would reach C)
+    or written."""
+    lda, ldb, ldc = k + 4, n + 1, n + 3
+    A, B = O.gemm_int_inputs(m, n, k)
+    Ap = np.full((m, lda), np.nan, np.float32)
+    Ap[:, :k] = A
+    Bp = np.full((k, ldb), np.nan, np.float32)
+    Bp[:, :n] = B
+    dA, dB = up(Ap.ravel()), up(Bp.ravel())
+    dC = up(np.full(m * ldc, np.nan, np.float32))
+    args = kh.LaunchArgs().add_memref(dA, [m, k]).add_memref(dB, [k, n]).add_memref(dC, [m, n])
+    args.slots[5], args.slots[7 + 5], args.slots[14 + 5] = lda, ldb, ldc
+    f = kh.GpuModule(kh.code_object("gemm")).get_function(sym)
+    say(f"{sym} m={m} n={n} k={k} grid={grid} block=512 lda={lda} ldb={ldb} ldc={ldc}")
+    kh.kernel_launch(f, (grid, 1, 1), (512, 1, 1), args)
+    C = down(dC, m * ldc).reshape(m, ldc)
+    assert np.array_equal(C[:, :n], (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32))
+    assert np.isnan(C[:, n:]).all()
+
+
 @pytest.mark.parametrize("extra", [4, 1])
 def test_gemm_padded_c_rows(dev, extra):
     """C rows `n + extra` floats apart (slot 19 of the 21: C's row stride;
