@@ -12,9 +12,11 @@
 //     MFMA accumulator blocks. Five such symbols, all correct for every
 //     shape; the launcher scores each by its full-occupancy rate times how
 //     busy its last round of workgroups would be (kh_tiles.h) and takes the
-//     best, unless the launch has at most 256 tiles of 32x32 (then
-//     `gemm_ksplit` / `gemm_ksplit_deep`, at the end of this file, split K
-//     over 8 waves instead); a tune cache, when set, overrides the choice:
+//     best, unless the launch has at most 256 tiles of 32x32, or fewer
+//     than 256 tiles of 64x64 that are all whole with K a multiple of 128
+//     (then `gemm_ksplit` / `gemm_ksplit_deep`, at the end of this file,
+//     split K over 8 waves instead); a tune cache, when set, overrides the
+//     choice:
 //       `gemm`        128x256 tiles (64x128 per wave, 128 accumulator registers
 //                     per lane), 16-deep K slabs: the least LDS and L2 traffic
 //                     per MFMA (8192^3, 4096^3, 8192x8192x256); persistent
@@ -22,7 +24,7 @@
 //       `gemm_mid`    128x128 tiles (64x64 per wave), 32-deep slabs (e.g.
 //                     8192x1024x8192);
 //       `gemm_small`  64x64 tiles, for grids the larger tiles would fill
-//                     unevenly (768^3, 1024^3);
+//                     unevenly (1024^3, 960^3);
 //       `gemm_small_pf2` the same tiles on 16x16 MFMAs with two-ahead
 //                     prefetch, when they number more than one per CU
 //                     (1536^3 to 3584^3, 2048x2048x8192);
@@ -352,8 +354,9 @@ __device__ __forceinline__ T *uniform_ptr(T *p) {
 __device__ __forceinline__ bool ks_interior_ok(int bd, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                                                int64_t ldc, const float *A) {
   constexpr int64_t kLim = int64_t(1) << 29;
+  static_assert(KH_GEMM_KSPLIT_INTERIOR_K == 64 * kKsFastBatch, "the launcher's K multiple for this path");
   return bd == KH_GEMM_KSPLIT_THREADS && M > 0 && N > 0 && (M & 31) == 0 && (N & 31) == 0 && K > 0 &&
-         K % (64 * kKsFastBatch) == 0 && (lda & 3) == 0 && kh::aligned16(A) && M <= kLim && N <= kLim &&
+         K % KH_GEMM_KSPLIT_INTERIOR_K == 0 && (lda & 3) == 0 && kh::aligned16(A) && M <= kLim && N <= kLim &&
          31 * lda + K / 8 <= kLim && K * ldb <= kLim && ldc <= kLim && (M >> 5) * (N >> 5) < (int64_t(1) << 31);
 }
 

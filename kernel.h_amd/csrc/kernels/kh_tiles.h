@@ -60,9 +60,19 @@
 // `gemm_ksplit`: 32x32 tiles, K split over the 8 waves of a 512-thread
 // workgroup. The launcher takes it when its tiles fit one round (at most
 // one workgroup per CU): there the larger tiles leave three CUs in four idle.
+// It also takes it where the 64x64 tiles number fewer than the CUs and
+// every 32x32 tile is whole with K a multiple of KH_GEMM_KSPLIT_INTERIOR_K
+// (the K-split symbols' unconditional-load path), from
+// KH_GEMM_KSPLIT_MIN_K on; the workgroups then loop over their tiles.
+// Kernel trace, rotated inputs, against `gemm_small`: 640^3 11.5 vs 18.0
+// us, 768^3 18.0 vs 21.2, 1024x512x512 10.2 vs 15.2, 256x2048x2048 25.5 vs
+// 50.3, 512x1536x1024 21.5 vs 27.4; level at 768x768x256 and 896^3; at
+// 1024^3 (256 tiles of 64x64) level, at 1024x1024x512 slower (17.3 vs 15.9).
 #define KH_GEMM_KSPLIT_BM 32
 #define KH_GEMM_KSPLIT_BN 32
 #define KH_GEMM_KSPLIT_THREADS 512
+#define KH_GEMM_KSPLIT_INTERIOR_K 128
+#define KH_GEMM_KSPLIT_MIN_K 256
 // From this K on, the launcher takes `gemm_ksplit_deep` (three batches of
 // loads in flight per wave) for the same launches.
 #define KH_GEMM_KSPLIT_DEEP_K 2048

@@ -220,6 +220,10 @@ const GemmCandidate *find_gemm_candidate(const char *symbol) {
 // persistent `gemm`, which gets at most two per CU and loops.
 int64_t candidate_grid(const GemmCandidate &c, int64_t m, int64_t n) {
   const int64_t tiles = ceil_div(m, c.bm()) * ceil_div(n, c.bn());
+  // The K-split symbols loop over their tiles as well: one workgroup per CU
+  // (their registers allow no more) measured better than one per tile
+  // beyond a round (768^3 18.0 vs 19.0 us, 512x1024x1024 15.1 vs 15.7).
+  if (c.ksplit()) return std::min<int64_t>(tiles, KH_GEMM_CUS);
   return c.pipe == kPersistent ? std::min<int64_t>(tiles, KH_GEMM_ROUND_BIG) : tiles;
 }
 
@@ -322,7 +326,10 @@ double gemm_score(int64_t tiles, int64_t round, double rate) {
 }
 
 const char *heuristic_gemm_symbol(int64_t m, int64_t n, int64_t k) {
-  if (ceil_div(m, KH_GEMM_KSPLIT_BM) * ceil_div(n, KH_GEMM_KSPLIT_BN) <= KH_GEMM_CUS) {
+  const int64_t tiles64 = ceil_div(m, KH_GEMM_SMALL_BM) * ceil_div(n, KH_GEMM_SMALL_BN);
+  if (ceil_div(m, KH_GEMM_KSPLIT_BM) * ceil_div(n, KH_GEMM_KSPLIT_BN) <= KH_GEMM_CUS ||
+      (tiles64 < KH_GEMM_CUS && m % KH_GEMM_KSPLIT_BM == 0 && n % KH_GEMM_KSPLIT_BN == 0 &&
+       k % KH_GEMM_KSPLIT_INTERIOR_K == 0 && k >= KH_GEMM_KSPLIT_MIN_K)) {
     return k >= KH_GEMM_KSPLIT_DEEP_K ? "gemm_ksplit_deep" : "gemm_ksplit";
   }
   const double big = gemm_score(ceil_div(m, KH_GEMM_BM) * ceil_div(n, KH_GEMM_BN), KH_GEMM_ROUND_BIG,
@@ -336,7 +343,6 @@ const char *heuristic_gemm_symbol(int64_t m, int64_t n, int64_t k) {
   if (big >= mid && big >= wide && big >= small) return "gemm";
   if (mid >= wide && mid > small) return "gemm_mid";
   if (wide > small) return "gemm_wide";
-  const int64_t tiles64 = ceil_div(m, KH_GEMM_SMALL_BM) * ceil_div(n, KH_GEMM_SMALL_BN);
   return tiles64 > KH_GEMM_SMALL_PF2_TILES ? "gemm_small_pf2" : "gemm_small";
 }
 

@@ -275,7 +275,9 @@ def test_kernarg_segment_is_2n_plus_3_slots(name, nslots):
     ("gemm", "m=2048,n=2048,k=2048", (512, 1, 1), (512, 1, 1)),       # gemm_wide: 64x128 on 8 waves, 2 rounds
     ("gemm", "m=1024,n=1024,k=1024", (256, 1, 1), (256, 1, 1)),       # 64x64
     ("gemm", "m=512,n=512,k=512", (256, 1, 1), (512, 1, 1)),        # gemm_ksplit: 256 tiles of 32x32, 8 waves
-    ("gemm", "m=768,n=768,k=768", (144, 1, 1), (256, 1, 1)),        # 576 tiles of 32x32: 64x64 instead
+    ("gemm", "m=768,n=768,k=768", (256, 1, 1), (512, 1, 1)),        # 144 tiles of 64x64: K split, 576 tiles looped
+    ("gemm", "m=960,n=960,k=960", (225, 1, 1), (256, 1, 1)),        # K not a multiple of 128: 64x64
+    ("gemm", "m=768,n=768,k=128", (144, 1, 1), (256, 1, 1)),        # K below 256: 64x64
     ("gemm", "m=512,n=512,k=8192", (256, 1, 1), (512, 1, 1)),       # gemm_ksplit_deep
     ("attention", "batch=4,heads=16,seq=4096,head_dim=64", (32, 16, 4), (256, 1, 1)),
 ])
@@ -294,7 +296,10 @@ def test_launcher_geometry(name, shape, grid, block):
     ("gemm", "m=512,n=512,k=2048", "gemm_ksplit_deep"),   # 256 tiles of 32x32, deep K
     ("gemm", "m=512,n=512,k=1024", "gemm_ksplit"),
     ("gemm", "m=300,n=520,k=100", "gemm_ksplit"),
-    ("gemm", "m=768,n=768,k=768", "gemm_small"),
+    ("gemm", "m=768,n=768,k=768", "gemm_ksplit"),            # fewer 64x64 tiles than CUs, whole 32x32 tiles
+    ("gemm", "m=256,n=2048,k=2048", "gemm_ksplit_deep"),
+    ("gemm", "m=1024,n=1024,k=512", "gemm_small"),           # 256 tiles of 64x64
+    ("gemm", "m=760,n=768,k=768", "gemm_small"),             # an edge tile in m
     ("softmax", "rows=4096,cols=1024", "softmax"),
     ("softmax", "rows=16384,cols=4096", "softmax_wide"),
     ("layernorm", "rows=16,cols=2048", "layernorm_wide"),

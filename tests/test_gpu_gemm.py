@@ -225,6 +225,8 @@ def test_gemm_padded_c_rows(dev, extra):
     (4096, 4096, 4096, 512),    # gemm: one full round of 128x256
     (512, 512, 1024, 256),      # gemm_ksplit: 256 tiles of 32x32 at 512 threads
     (512, 470, 4100, 240),      # gemm_ksplit_deep: edge tiles in n, a partial last K chunk
+    (768, 768, 768, 256),       # gemm_ksplit: 576 whole tiles of 32x32 looped over 256 workgroups
+    (256, 2048, 2048, 256),     # gemm_ksplit_deep: 512 whole tiles looped
 ])
 def test_gemm_launcher_choice_at_scale(dev, m, n, k, grid):
     assert kh.geometry("gemm", f"m={m},n={n},k={k}")[0] == (grid, 1, 1)
