@@ -185,13 +185,34 @@ def rotation_count(bytes_per_set, cap=1024):
     return max(1, min(cap, -(-ROTATE_BYTES // max(1, int(bytes_per_set)))))
 
 
+def issue_ms(launches, sync):
+    """Host time to issue `launches` back to back (an untimed pass; `sync`
+    then waits for them)."""
+    t0 = time.perf_counter()
+    for f in launches:
+        f()
+    t1 = time.perf_counter()
+    sync()
+    return (t1 - t0) * 1e3
+
+
+def prime_for(prime, stream, host_ms):
+    """Queues enough primer copies (~0.35 ms each) ahead of a sequence whose
+    launches take the host `host_ms` to issue: the host then enqueues the
+    whole sequence before its first launch starts, so events around it time
+    the GPU, not the host's submission rate."""
+    for _ in range(max(1, -(-int(1.5 * host_ms * 1000) // 350))):
+        prime(stream)
+
+
 def time_queued(kh, stream, launches, prime):
     """Average GPU duration of `launches` (callables, issued back to back)
-    queued behind `prime(stream)`, a ~0.35 ms copy, so the host has enqueued
-    them all before the first starts: microsecond kernels are timed at the
-    GPU's rate, not the host's submission rate."""
+    queued behind primer copies that outlast the host's time to issue them
+    (measured in an untimed pass first): microsecond kernels are timed at
+    the GPU's rate, not the host's submission rate."""
     e0, e1 = kh.Event(), kh.Event()
-    prime(stream)
+    host = issue_ms(launches, stream.synchronize)
+    prime_for(prime, stream, host)
     e0.record(stream)
     for f in launches:
         f()
@@ -417,8 +438,10 @@ def measure_vendor_gemm(torch, gemm_cases, steps, prime):
     GEMM case's shape, under this bench's own conditions: as many rotated
     buffer sets as the case, U[-1,1] inputs, K back-to-back launches between
     two events on torch's stream (as many as this build's own measurement of
-    the case), queued behind the same ~0.35 ms copy. A reference
-    point for the same shapes, not part of this build's result."""
+    the case), queued behind primer copies that outlast the host's time to
+    issue them (torch.mm's per-call host cost exceeds a 512^3 kernel), so
+    the rate is the vendor kernel's. A reference point for the same shapes,
+    not part of this build's result."""
     dev = torch.device("cuda:0")
     torch.backends.cuda.matmul.allow_tf32 = False
     res = {}
@@ -433,9 +456,12 @@ def measure_vendor_gemm(torch, gemm_cases, steps, prime):
             torch.mm(x, y, out=z)
         best = None
         count = c.gpu_launches  # the same number of launches as this build's measurement
+        calls = [lambda i=i: torch.mm(sets[i % len(sets)][0], sets[i % len(sets)][1], out=sets[i % len(sets)][2])
+                 for i in range(count)]
+        host = issue_ms(calls, torch.cuda.synchronize)
         for _ in range(3):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            prime(st.cuda_stream)
+            prime_for(prime, st.cuda_stream, host)
             e0.record(st)
             for i in range(count):
                 x, y, z = sets[i % len(sets)]
@@ -446,7 +472,8 @@ def measure_vendor_gemm(torch, gemm_cases, steps, prime):
             best = ms if best is None else min(best, ms)
         res[c.name] = {"ms": best, "rate": 2.0 * m * n * k / (best * 1e-3) / 1e12, "unit": "TFLOP/s",
                        "buffer_sets": len(sets), "library": "torch.mm (hipBLASLt/rocBLAS), tf32 off",
-                       "launches_averaged": count, "timing": "best of 3 sequences"}
+                       "launches_averaged": count, "host_issue_ms": host,
+                       "timing": "best of 3 sequences, GPU-paced (queued behind primers that outlast their issue)"}
         del sets
         torch.cuda.empty_cache()
     return res
