@@ -203,8 +203,9 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
   // The fast path's buffer loads address the slices with 32-bit offsets and
   // bound K by seq rows of ks floats and V by seq rows of vs floats, so every
   // row must hold its D floats.
-  const bool fast = VEC4 && bd == kFastThreads && ks >= D && vs >= D &&
-                    (seq + 2 * TK) * (ks > vs ? ks : vs) * 4 < (1ll << 31);
+  const int64_t widest = ks > vs ? (ks > qs ? ks : qs) : (vs > qs ? vs : qs);
+  const bool fast = VEC4 && bd == kFastThreads && ks >= D && vs >= D && qs >= D &&
+                    (seq + 2 * TK) * widest * 4 < (1ll << 31);
   // log2(e)/sqrt(d): S^T comes out in log2 units, so exp(S - m) = 2^(S' - m').
   const float qscale = kh::kLog2e * 0.125f;
 
@@ -212,22 +213,12 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
                                                                       (int)(seq * ks * 4), 0x00020000);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(Vg), (short)0,
                                                                       (int)(seq * vs * 4), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(Qg), (short)0,
+                                                                      (int)(seq * qs * 4), 0x00020000);
   for (int64_t qt = q0; qt < nqt; qt += qstep) {
     const int64_t q_row = qt * rows_per_block + (int64_t)wave * QW + r;
-    // The fast path's K0 goes out before Q: its copy into LDS waits for K0
-    // alone, and tile 0's S^T then takes Q's fragments as they land.
     float4 kr[4], vr[4];
-    if (fast) load_k(kr, rk, ks, 0, tid);
     float4 q[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      float4 v = make_float4(0, 0, 0, 0);
-      if (q_row < seq) {
-        const float *p = Qg + q_row * qs + 8 * c + 4 * h;
-        v = VEC4 ? *reinterpret_cast<const float4 *>(p) : make_float4(p[0], p[1], p[2], p[3]);
-      }
-      q[c] = make_float4(v.x * qscale, v.y * qscale, v.z * qscale, v.w * qscale);
-    }
     v16f o[2] = {v16f{}, v16f{}};
     float m = kNegBig, l = 0.0f;
 
@@ -239,13 +230,23 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
       // tile, the only one that can be partial, is finished after it.
       v16f sa[2], sb[2];
       {
-        // K0, V0 and K1 go out together (one memory latency before the
-        // first MFMA, not two). Only Q and K0 are waited for before tile
-        // 0's S^T (loads complete in issue order; the barrier fences LDS
-        // only): V0 and K1 keep arriving under those MFMAs.
+        // K0, Q, V0 and K1 go out together (one memory latency before the
+        // first MFMA, not two): loads complete in issue order, so scaling Q
+        // (its first use, where the compiler waits for it) after V0 and K1
+        // are issued leaves those two in flight, and the barrier before
+        // tile 0's S^T fences LDS only. Q moves through a range-checked
+        // buffer resource (rows at or past seq read 0): loaded under
+        // `if (q_row < seq)` and scaled at once, it made the compiler wait
+        // for K0 and Q before V0 and K1 went out.
+        load_k(kr, rk, ks, 0, tid);
+        const uint32_t qoff = (uint32_t)(4 * (q_row * qs + 4 * h));
+#pragma unroll
+        for (int c = 0; c < 8; ++c) q[c] = as_f4(__builtin_amdgcn_raw_buffer_load_b128(rq, qoff + 32 * c, 0, 0));
         float4 k1[4];
         load_v(vr, rv, vs, 0, tid);
         load_k(k1, rk, ks, TK, tid);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) q[c] = make_float4(q[c].x * qscale, q[c].y * qscale, q[c].z * qscale, q[c].w * qscale);
         store_k(kr, Ks, tid);
         kh::lds_barrier();
         qk_tile(sa, q, Ks, lane);
@@ -283,6 +284,15 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
       else
         softmax_pv<true>(o, m, l, sa, Vt + (t & 1) * D * LDV, t * TK, seq, lane);
     } else {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        float4 v = make_float4(0, 0, 0, 0);
+        if (q_row < seq) {
+          const float *p = Qg + q_row * qs + 8 * c + 4 * h;
+          v = VEC4 ? *reinterpret_cast<const float4 *>(p) : make_float4(p[0], p[1], p[2], p[3]);
+        }
+        q[c] = make_float4(v.x * qscale, v.y * qscale, v.z * qscale, v.w * qscale);
+      }
       for (int64_t t = 0; t < ntiles; ++t) {
         stage_kv_generic(Ks, Vt, Kg, Vg, ks, vs, t * TK, seq, bd);
         __syncthreads();
