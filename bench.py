@@ -52,9 +52,9 @@ METRIC = "GEMM-8192 fp32 TFLOPS + softmax/scan HBM GB/s, % of MI355X roofline"
 # profiles/templates_baseline_sizes_hbm_traffic.md. Constants of that profile
 # (median dispatch), not measured by the run that reports them.
 PMC_TRAFFIC_BYTES = {
-    "vecadd": 201371645, "softmax": 33660954, "layernorm": 33723990, "scan": 539240514, "scan_1e6": 8202141,
-    "fused_gelu": 536931644, "fused_gelu_2^22": 33639323, "gemm": 3803504387, "gemm_8192x8192x256": 379226985,
-    "gemm_2048": 117554553, "gemm_512": 10650028, "attention": 268723951, "attention_s1024": 67397775,
+    "vecadd": 201359102, "softmax": 33658522, "layernorm": 33720982, "scan": 539456182, "scan_1e6": 8201644,
+    "fused_gelu": 536932348, "fused_gelu_2^22": 33635355, "gemm": 3810297713, "gemm_8192x8192x256": 379223785, "gemm_2048": 117550905,
+    "gemm_512": 10558902, "attention": 268738414, "attention_s1024": 67421901,
 }
 PMC_TRAFFIC_SOURCE = "profiles/templates_baseline_sizes_hbm_traffic.md (constant, not measured by this run)"
 
