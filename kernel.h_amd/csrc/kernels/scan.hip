@@ -99,10 +99,16 @@
 //     when the call began) is taken over by one of the waiting workgroups,
 //     so such a header costs one wait and no failure;
 //   * a workgroup whose claims keep stalling (8 limits in all, which needs
-//     claimant waves stalled for seconds) counts the failure and writes NaN
-//     to its share of y.
+//     claimant waves stalled for seconds) counts the failure, writes NaN
+//     to its share of y and leaves the header unrecognisable: the call
+//     will not close, and the next call then claims a new session rather
+//     than reuse this one's generation and records. (Only a claimant that
+//     resumes after that and signs escapes this; its call's records could
+//     then pass for the next call's.)
 // After a call, failed > 0 means y is not to be trusted (NaN, or left as it
-// was where a lost ticket's tile was never reached).
+// was where a lost ticket's tile was never reached). A claim resets the
+// count, so a call in which another workgroup claimed the header after a
+// failure shows the failure only as NaN in y.
 #include "kh_device.h"
 #include "kh_tiles.h"
 
@@ -383,9 +389,13 @@ __device__ __forceinline__ Opened open_session(Header *h, Counters *c, int64_t n
     }
     if (polls > 8 * kSpinLimit) {
       // Claims kept stalling: give up. The workgroup's tickets are lost
-      // and the call's last workgroup never counts itself done, so the
-      // header is not re-signed by this call.
+      // and the call's last workgroup never counts itself done, so this
+      // call does not re-sign the header. Leave it unrecognisable (0 is
+      // neither a signature nor a claim mark), so that a later call claims
+      // a new session, with new record keys, instead of running under this
+      // call's generation and taking its records for its own.
       fetch_add(&h->failed, 1u);
+      __hip_atomic_store(&h->check, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       o.ok = false;
       return o;
     }
