@@ -346,8 +346,8 @@ __device__ __forceinline__ T *uniform_ptr(T *p) {
 }
 
 // The K split for launches whose tiles are all whole: M, N multiples of 32,
-// K of 8 * kKsFastBatch * 8, eight waves, and every byte offset below 2^31
-// (ks_interior_ok). The operands and groups are those of gemm_ksplit_body;
+// K of 8 * kKsFastBatch * 8, eight waves, and every buffer span below 2^31
+// bytes, the largest record count a buffer resource holds (ks_interior_ok). The operands and groups are those of gemm_ksplit_body;
 // lane (r, h) reads A from one offset register plus 32 bytes per group (the
 // instruction's immediate) and B from one offset register plus a row step
 // in the scalar offset. Same reduction, so the same bits.
@@ -357,7 +357,7 @@ __device__ __forceinline__ bool ks_interior_ok(int bd, int64_t M, int64_t N, int
   static_assert(KH_GEMM_KSPLIT_INTERIOR_K == 64 * kKsFastBatch, "the launcher's K multiple for this path");
   return bd == KH_GEMM_KSPLIT_THREADS && M > 0 && N > 0 && (M & 31) == 0 && (N & 31) == 0 && K > 0 &&
          K % KH_GEMM_KSPLIT_INTERIOR_K == 0 && (lda & 3) == 0 && kh::aligned16(A) && M <= kLim && N <= kLim &&
-         31 * lda + K / 8 <= kLim && K * ldb <= kLim && ldc <= kLim && (M >> 5) * (N >> 5) < (int64_t(1) << 31);
+         31 * lda + K / 8 < kLim && K * ldb < kLim && ldc < kLim && (M >> 5) * (N >> 5) < (int64_t(1) << 31);
 }
 
 __device__ __forceinline__ void ks_interior(const float *__restrict__ A, const float *__restrict__ B,
