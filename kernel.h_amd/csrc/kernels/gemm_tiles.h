@@ -320,14 +320,38 @@ __device__ __forceinline__ void mfma_frag(Acc (&acc)[WTM][WTN], const Frag<WTM, 
     }
 }
 
+// One slab's chunks from LDS. For eight-wave tiles on 16x16 MFMAs
+// (`gemm_wide`), chunk c+1's fragment reads are interleaved with chunk c's
+// MFMAs, one read per two (kernel trace, variants interleaved launch by
+// launch, same bits: 2048^3 142.5 -> 141.3 us, 6144x6144x1024 593.8 ->
+// 586.1). The same change slowed the four-wave tiles (`gemm_small` 8-10%,
+// `gemm_mid` 0.5-1%), which keep one chunk's reads before its MFMAs.
 template <int WTM, int WTN, class T>
 __device__ __forceinline__ void compute_slab(AccOf<T> (&acc)[WTM][WTN], const float *__restrict__ As,
                                              const float *__restrict__ Bs, int wm, int wn, int lane) {
+  constexpr int C = T::BK / Mfma<T::kMF>::CK;
+  if constexpr (T::NT == 512 && T::kMF == 16) {
+    Frag<WTM, WTN> f[2];
+    read_frag<WTM, WTN, T>(f[0], As, Bs, 0, wm, wn, lane);
 #pragma unroll
-  for (int c = 0; c < T::BK / Mfma<T::kMF>::CK; ++c) {
-    Frag<WTM, WTN> f;
-    read_frag<WTM, WTN, T>(f, As, Bs, c, wm, wn, lane);
-    mfma_frag<WTM, WTN>(acc, f);
+    for (int c = 0; c < C; ++c) {
+      if (c + 1 < C) read_frag<WTM, WTN, T>(f[(c + 1) & 1], As, Bs, c + 1, wm, wn, lane);
+      mfma_frag<WTM, WTN>(acc, f[c & 1]);
+      if (c + 1 < C) {
+#pragma unroll
+        for (int g = 0; g < WTM + 2 * WTN; ++g) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // two MFMAs
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      Frag<WTM, WTN> f;
+      read_frag<WTM, WTN, T>(f, As, Bs, c, wm, wn, lane);
+      mfma_frag<WTM, WTN>(acc, f);
+    }
   }
 }
 
