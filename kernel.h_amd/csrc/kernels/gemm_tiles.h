@@ -243,6 +243,42 @@ __device__ __forceinline__ void dma_slab(const float *__restrict__ A, const floa
   }
 }
 
+// Loads L0..L1-1 of dma_slab's (A's NA, then B's NB), so that a slab's
+// loads can be spread between MFMAs.
+template <class T, bool ALN, int L0, int L1>
+__device__ __forceinline__ void dma_part(const float *__restrict__ A, const float *__restrict__ B, int64_t M,
+                                         int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t m0, int64_t n0,
+                                         int64_t k0, float *As, float *Bs, int wave, int lane) {
+  const u32x4 ra = rows_desc(A + m0 * lda, (M - m0) < T::BM ? (M - m0) : T::BM, lda);
+  const u32x4 rb = rows_desc(B + k0 * ldb, (K - k0) < T::BK ? (K - k0) : T::BK, ldb);
+#pragma unroll
+  for (int i = 0; i < T::NA; ++i) {
+    if (i < L0 || i >= L1) continue;
+    const int idx0 = 64 * wave + T::NT * i;  // first float4 of this wave's instruction
+    const int idx = idx0 + lane;
+    const int ar = idx / T::QP, ak = 4 * ((idx % T::QP) ^ T::aswz(ar));
+    uint32_t aoff;
+    if constexpr (ALN)
+      aoff = ((uint32_t)ar * (uint32_t)lda + (uint32_t)ak) * 4u + (uint32_t)k0 * 4u;
+    else
+      aoff = (k0 + ak < K) ? (uint32_t)((ar * lda + k0 + ak) * 4) : kOutside;
+    dma16(ra, aoff, lds_addr(As + 4 * idx0));
+  }
+#pragma unroll
+  for (int i = 0; i < T::NB; ++i) {
+    if (T::NA + i < L0 || T::NA + i >= L1) continue;
+    const int idx0 = 64 * wave + T::NT * i;
+    const int idx = idx0 + lane;
+    const int bk = idx / T::BROW, bn = 4 * (idx % T::BROW);
+    uint32_t boff;
+    if constexpr (ALN)
+      boff = ((uint32_t)bk * (uint32_t)ldb + (uint32_t)bn) * 4u + (uint32_t)n0 * 4u;
+    else
+      boff = (n0 + bn < N) ? (uint32_t)((bk * ldb + n0 + bn) * 4) : kOutside;
+    dma16(rb, boff, lds_addr(Bs + T::b_at(idx0 / T::BROW, 4 * (idx0 % T::BROW))));
+  }
+}
+
 // Wait until at most N vector-memory operations of this wave are in flight
 // and all its LDS operations are done, then meet the workgroup. Loads retire
 // in order, so N = the loads issued after the ones awaited. The wait is the
@@ -307,6 +343,25 @@ template <int WTM, int WTN, class Acc>
 __device__ __forceinline__ void mfma_frag(Acc (&acc)[WTM][WTN], const Frag<WTM, WTN> &f) {
 #pragma unroll
   for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int i = 0; i < WTM; ++i) {
+      const float av = s == 0 ? f.a[i].x : s == 1 ? f.a[i].y : s == 2 ? f.a[i].z : f.a[i].w;
+#pragma unroll
+      for (int j = 0; j < WTN; ++j) {
+        if constexpr (sizeof(Acc) == sizeof(v16f))
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, f.b[j][s], acc[i][j], 0, 0, 0);
+        else
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, f.b[j][s], acc[i][j], 0, 0, 0);
+      }
+    }
+}
+
+// MFMA steps S0..S1-1 of a chunk (mfma_frag is steps 0..3): each
+// accumulator still takes its steps in order, so the same bits.
+template <int WTM, int WTN, int S0, int S1, class Acc>
+__device__ __forceinline__ void mfma_frag_s(Acc (&acc)[WTM][WTN], const Frag<WTM, WTN> &f) {
+#pragma unroll
+  for (int s = S0; s < S1; ++s)
 #pragma unroll
     for (int i = 0; i < WTM; ++i) {
       const float av = s == 0 ? f.a[i].x : s == 1 ? f.a[i].y : s == 2 ? f.a[i].z : f.a[i].w;
@@ -700,14 +755,27 @@ __device__ __forceinline__ void flat_step(AccOf<T> (&acc)[WTM][WTN], Frag<WTM, W
   if constexpr (C > 1) interleave_reads<kReads>();
   if (PRIO) __builtin_amdgcn_s_setprio(0);
   vm_barrier<WAIT>();
-  if (dma)
-    dma_slab<T, ALN>(Ap, Bp, M, N, K, lda, ldb, dm0, dn0, dk0, As + fut * T::A_STAGE, Bs + fut * T::B_STAGE, wv,
-                     lane);
   if (PRIO) __builtin_amdgcn_s_setprio(1);
-  if (read_next) read_frag<WTM, WTN, T>(f0, As + nxt * T::A_STAGE, Bs + nxt * T::B_STAGE, 0, wm, wn, lane);
+  float *const dA = As + fut * T::A_STAGE, *const dB = Bs + fut * T::B_STAGE;
   if constexpr (C > 1) {
-    mfma_frag<WTM, WTN>(acc, f1);
+    // Slab q+1's first fragments, interleaved with this slab's next MFMA
+    // step; the later slab's loads, half after that step and half after
+    // the one after it (each load's inline assembly is a scheduling
+    // boundary, so program order places them). Against all six loads in
+    // one burst before the MFMAs: 8192x8192x256 257.9 -> 253.9 us,
+    // 8192^3 and 4096^3 level (7347 -> 7328, 926.0 -> 927.0 us); a 2+2+2
+    // or 1+2+3 split measured slower at 8192^3 (7413-7416 us).
+    constexpr int kL = T::NA + T::NB;
+    if (read_next) read_frag<WTM, WTN, T>(f0, As + nxt * T::A_STAGE, Bs + nxt * T::B_STAGE, 0, wm, wn, lane);
+    mfma_frag_s<WTM, WTN, 0, 1>(acc, f1);
     interleave_reads<kReads>();
+    if (dma) dma_part<T, ALN, 0, kL / 2>(Ap, Bp, M, N, K, lda, ldb, dm0, dn0, dk0, dA, dB, wv, lane);
+    mfma_frag_s<WTM, WTN, 1, 2>(acc, f1);
+    if (dma) dma_part<T, ALN, kL / 2, kL>(Ap, Bp, M, N, K, lda, ldb, dm0, dn0, dk0, dA, dB, wv, lane);
+    mfma_frag_s<WTM, WTN, 2, 4>(acc, f1);
+  } else {
+    if (dma) dma_slab<T, ALN>(Ap, Bp, M, N, K, lda, ldb, dm0, dn0, dk0, dA, dB, wv, lane);
+    if (read_next) read_frag<WTM, WTN, T>(f0, As + nxt * T::A_STAGE, Bs + nxt * T::B_STAGE, 0, wm, wn, lane);
   }
 #pragma unroll
   for (int c = 2; c < C; ++c) {
