@@ -7,7 +7,7 @@
 // 21 parameters. The reference computes one element per lane with scalar
 // FMAs out of an 8 KiB LDS tile (gemm.cpp:265-296). Here:
 //
-//   * Workgroup = 256 threads (4 wave64s, 2x2; `gemm_wide`: 512, 2x4)
+//   * Workgroup = 256 threads (4 wave64s, 2x2; `gemm_wide`: 512, 4x2)
 //     computing a BM x BN tile of C; each wave owns its part as WTM x WTN
 //     MFMA accumulator blocks. Five such symbols, all correct for every
 //     shape; the launcher scores each by its full-occupancy rate times how
@@ -21,16 +21,19 @@
 //                     per lane), 16-deep K slabs: the least LDS and L2 traffic
 //                     per MFMA (8192^3, 4096^3, 8192x8192x256); persistent
 //                     workgroups, two per CU, each looping over its tiles;
-//       `gemm_mid`    128x128 tiles (64x64 per wave), 32-deep slabs (e.g.
-//                     8192x1024x8192);
+//       `gemm_mid`    128x128 tiles (64x64 per wave), 32-deep slabs (the
+//                     tune cache's; `gemm_wide` outscores it wherever both
+//                     fit);
 //       `gemm_small`  64x64 tiles, for grids the larger tiles would fill
 //                     unevenly (1024^3, 960^3);
 //       `gemm_small_pf2` the same tiles on 16x16 MFMAs with two-ahead
 //                     prefetch, when they number more than one per CU
-//                     (1536^3 to 3584^3, 2048x2048x8192);
-//       `gemm_wide`   64x128 tiles on eight waves of 16x16 MFMAs, one
-//                     workgroup per CU, where its tiles fill whole rounds
-//                     (2048^3, 6144x6144x1024).
+//                     (1536^3 to 3584^3);
+//       `gemm_wide`   128x128 tiles on eight waves of 16x16 MFMAs (32x64
+//                     per wave), 32-deep slabs in `gemm`'s persistent
+//                     direct-to-LDS ring, one workgroup per CU, where its
+//                     tiles fill whole rounds (2048^3, 6144x6144x1024,
+//                     2048x2048x8192, 4096x2048x4096, 8192x1024x8192).
 //     Registers are capped for two waves per SIMD (two workgroups per CU, as
 //     LDS allows), so one workgroup's barrier and slab hand-over overlap the
 //     other's MFMAs. `gemm` and `gemm_mid` raise their waves' priority
@@ -81,9 +84,9 @@ static_assert(Tile<1, 1, 32, false>::BM == KH_GEMM_SMALL_BM && Tile<1, 1, 32, fa
                   Tile<2, 2, 32, false, 2, 2, 16>::BM == KH_GEMM_SMALL_BM &&
                   Tile<2, 2, 32, false, 2, 2, 16>::BN == KH_GEMM_SMALL_BN,
               "launcher tile size (gemm_small and gemm_small_pf2)");
-static_assert(Tile<2, 2, 32, false, 2, 4, 16>::BM == KH_GEMM_WIDE_BM &&
-                  Tile<2, 2, 32, false, 2, 4, 16>::BN == KH_GEMM_WIDE_BN &&
-                  Tile<2, 2, 32, false, 2, 4, 16>::NT == KH_GEMM_WIDE_THREADS,
+static_assert(Tile<2, 4, 32, true, 4, 2, 16>::BM == KH_GEMM_WIDE_BM &&
+                  Tile<2, 4, 32, true, 4, 2, 16>::BN == KH_GEMM_WIDE_BN &&
+                  Tile<2, 4, 32, true, 4, 2, 16>::NT == KH_GEMM_WIDE_THREADS,
               "launcher tile size (gemm_wide)");
 
 // Entry of a symbol whose tile split assumes THREADS one-dimensional
@@ -144,18 +147,23 @@ gemm_small_pf2(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF
                                                                       A_n1, A_s0, B_s0, C_s0);
 }
 
-// Same arguments and results with 64x128 tiles on eight waves (2 x 4, each
-// 32x32 as 2x2 blocks of v_mfma_f32_16x16x4f32), 32-deep register-staged
-// slabs; one workgroup per CU. From the tune space: where its tiles fill
-// whole rounds of 256 it leads the 64x64 tiles (2048^3 124.5 vs 121.5,
-// 6144x6144x1024 129.0 vs 125.0, 2048x2048x8192 125.7 vs 108.1 for the
-// previous choice). The tile split assumes 512 threads: any other launch is
-// refused by writing NaN over C.
+// Same arguments and results with 128x128 tiles on eight waves (4 x 2,
+// each 32x64 as 2x4 blocks of v_mfma_f32_16x16x4f32), 32-deep slabs through
+// `gemm`'s persistent three-stage direct-to-LDS ring (99 KB of LDS: one
+// workgroup per CU, two waves per SIMD). Kernel trace against the previous
+// `gemm_wide` (64x128 tiles, register-staged slabs), variants interleaved
+// launch by launch, same bits: 2048^3 145.2 -> 133.9 us, 6144x6144x1024
+// 586.5 -> 557.1, 2048x2048x8192 528.8 -> 487.1; and against `gemm_mid` at
+// 4096x2048x4096 529.3 -> 496.9, 8192x1024x8192 1018 -> 965. The same tile
+// with the waves 2 x 4 (64x32 each) ran 137.6 us at 2048^3, sixteen waves
+// 140.5, 64x128 tiles two per CU 137.8, without s_setprio 137.0. The tile
+// split assumes 512 threads: any other launch is refused by writing NaN
+// over C.
 extern "C" __global__ void __launch_bounds__(KH_GEMM_WIDE_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_wide(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
   KH_GEMM_ENTRY_CHECK(KH_GEMM_WIDE_THREADS);
-  khg::gemm_entry_pipe<2, 2, 32, true, khg::kPipeRegs, 2, 4, 16>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1,
-                                                                 A_s0, B_s0, C_s0);
+  khg::gemm_entry_flat<2, 4, 32, true, 4, 2, 16>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0,
+                                                 C_s0);
 }
 
 

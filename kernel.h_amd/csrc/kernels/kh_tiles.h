@@ -29,8 +29,9 @@
 #define KH_GEMM_MID_BN 128
 #define KH_GEMM_SMALL_BM 64
 #define KH_GEMM_SMALL_BN 64
-// `gemm_wide`: 64x128 tiles on eight waves (512 threads), one workgroup per CU.
-#define KH_GEMM_WIDE_BM 64
+// `gemm_wide`: 128x128 tiles on eight waves (512 threads), one workgroup per
+// CU, persistent.
+#define KH_GEMM_WIDE_BM 128
 #define KH_GEMM_WIDE_BN 128
 #define KH_GEMM_WIDE_THREADS 512
 
@@ -44,6 +45,11 @@
 // are counted per CU. Fitted on 20 shapes from 1024^3 to 8192^3 (square,
 // skinny, rectangular, deep K) timed with rotated U[-1,1] inputs and warm
 // clocks: the choice is the measured best or within 3% of it on all of them.
+// `gemm_wide`'s rate was refitted when it became the persistent 128x128
+// ring: 3.3% below `gemm` at 4096^3 (both in whole rounds), level with the
+// 64x64 tiles at 2560^3. Its round divides `gemm_mid`'s and its rate is
+// higher, so it outscores `gemm_mid` at every shape (measured 5-6% faster
+// at 4096x2048x4096 and 8192x1024x8192).
 #define KH_GEMM_CUS 256
 #define KH_GEMM_ROUND_BIG (2 * KH_GEMM_CUS)
 #define KH_GEMM_ROUND_MID (2 * KH_GEMM_CUS)
@@ -51,7 +57,7 @@
 #define KH_GEMM_ROUND_SMALL KH_GEMM_CUS
 #define KH_GEMM_RATE_BIG 142
 #define KH_GEMM_RATE_MID 135
-#define KH_GEMM_RATE_WIDE 129
+#define KH_GEMM_RATE_WIDE 137
 #define KH_GEMM_RATE_SMALL 126
 // Where the 64x64 tiles are chosen and number more than this (one per CU),
 // the launcher takes `gemm_small_pf2` (16x16 MFMAs, two-ahead prefetch)

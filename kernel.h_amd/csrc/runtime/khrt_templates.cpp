@@ -200,7 +200,7 @@ const GemmCandidate kGemmCandidates[] = {
     {"gemm_mid", "gemm", 32, 2, 2, 2, 2, 32, 1, kRegs, true},
     {"gemm_small", "gemm", 32, 2, 2, 1, 1, 32, 0, kRegs, true},
     {"gemm_small_pf2", "gemm", 16, 2, 2, 2, 2, 32, 1, kPf2, true},
-    {"gemm_wide", "gemm", 16, 2, 4, 2, 2, 32, 1, kRegs, true},
+    {"gemm_wide", "gemm", 16, 4, 2, 2, 4, 32, 1, kPersistent, true},
     {"gemm_ksplit", "gemm", 32, 1, 1, 1, 1, 8, 0, kKsplit, true},
     {"gemm_ksplit_deep", "gemm", 32, 1, 1, 1, 1, 8, 0, kKsplitDeep, true},
     KH_GEMM_TUNE_CONFIGS(KH_TUNE_CANDIDATE)};
@@ -217,14 +217,17 @@ const GemmCandidate *find_gemm_candidate(const char *symbol) {
 }
 
 // Grid of a candidate at m x n: one workgroup per tile, except the
-// persistent `gemm`, which gets at most two per CU and loops.
+// persistent symbols, which get one round of resident workgroups and loop:
+// two per CU for `gemm` (four waves), one per CU for `gemm_wide` (eight
+// waves, 99 KB of LDS).
 int64_t candidate_grid(const GemmCandidate &c, int64_t m, int64_t n) {
   const int64_t tiles = ceil_div(m, c.bm()) * ceil_div(n, c.bn());
   // The K-split symbols loop over their tiles as well: one workgroup per CU
   // (their registers allow no more) measured better than one per tile
   // beyond a round (768^3 18.0 vs 19.0 us, 512x1024x1024 15.1 vs 15.7).
   if (c.ksplit()) return std::min<int64_t>(tiles, KH_GEMM_CUS);
-  return c.pipe == kPersistent ? std::min<int64_t>(tiles, KH_GEMM_ROUND_BIG) : tiles;
+  if (c.pipe == kPersistent) return std::min<int64_t>(tiles, c.waves() > 4 ? KH_GEMM_ROUND_WIDE : KH_GEMM_ROUND_BIG);
+  return tiles;
 }
 
 // The tune cache `kernelh tune` writes: one JSON object per line,

@@ -18,10 +18,13 @@ def up(a) -> kh.Buffer:
 
 def empty(count: int, poison: float | None = float("nan")) -> kh.Buffer:
     """A float buffer pre-filled on the device (NaN by default) so an output
-    element the kernel fails to write cannot pass a comparison by luck."""
+    element the kernel fails to write cannot pass a comparison by luck. The
+    fill runs on the null stream, which does not order against the
+    non-blocking streams kh.Stream creates, so it is waited for here."""
     b = kh.Buffer(max(1, count) * 4)
     if poison is not None:
         b.fill(poison)
+        kh.synchronize()
     return b
 
 

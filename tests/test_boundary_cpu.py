@@ -269,10 +269,10 @@ def test_kernarg_segment_is_2n_plus_3_slots(name, nslots):
     ("gemm", "m=8192,n=8192,k=256", (512, 1, 1), (256, 1, 1)),       # skinny K
     ("gemm", "m=4096,n=4096,k=64", (512, 1, 1), (256, 1, 1)),         # exactly one round
     ("gemm", "m=12288,n=12288,k=1024", (512, 1, 1), (256, 1, 1)),    # 4608 tiles: 9 per workgroup
-    ("gemm", "m=8192,n=1024,k=8192", (512, 1, 1), (256, 1, 1)),       # 128x128 (gemm_mid): 512 tiles
-    ("gemm", "m=6144,n=6144,k=1024", (4608, 1, 1), (512, 1, 1)),      # gemm_wide: 64x128, 18 full rounds
+    ("gemm", "m=8192,n=1024,k=8192", (256, 1, 1), (512, 1, 1)),       # gemm_wide: 512 tiles of 128x128, 2 each
+    ("gemm", "m=6144,n=6144,k=1024", (256, 1, 1), (512, 1, 1)),       # gemm_wide: 2304 tiles of 128x128, 9 each
     ("gemm", "m=3072,n=3072,k=3072", (2304, 1, 1), (256, 1, 1)),      # 64x64 (gemm_small_pf2)
-    ("gemm", "m=2048,n=2048,k=2048", (512, 1, 1), (512, 1, 1)),       # gemm_wide: 64x128 on 8 waves, 2 rounds
+    ("gemm", "m=2048,n=2048,k=2048", (256, 1, 1), (512, 1, 1)),       # gemm_wide: 256 tiles of 128x128, one round
     ("gemm", "m=1024,n=1024,k=1024", (256, 1, 1), (256, 1, 1)),       # 64x64
     ("gemm", "m=512,n=512,k=512", (256, 1, 1), (512, 1, 1)),        # gemm_ksplit: 256 tiles of 32x32, 8 waves
     ("gemm", "m=768,n=768,k=768", (256, 1, 1), (512, 1, 1)),        # 144 tiles of 64x64: K split, 576 tiles looped
@@ -288,7 +288,10 @@ def test_launcher_geometry(name, shape, grid, block):
 @pytest.mark.parametrize("name,shape,symbol", [
     ("gemm", "m=8192,n=8192,k=8192", "gemm"),
     ("gemm", "m=8192,n=8192,k=256", "gemm"),
-    ("gemm", "m=8192,n=1024,k=8192", "gemm_mid"),
+    ("gemm", "m=8192,n=1024,k=8192", "gemm_wide"),       # outscores gemm_mid (same tile, one round per CU)
+    ("gemm", "m=4096,n=2048,k=4096", "gemm_wide"),
+    ("gemm", "m=4096,n=4096,k=4096", "gemm"),            # one round of 128x256 against four of 128x128
+    ("gemm", "m=2560,n=2560,k=2560", "gemm_small_pf2"),  # 400 tiles of 128x128: a partial second round
     ("gemm", "m=1024,n=1024,k=1024", "gemm_small"),
     ("gemm", "m=3072,n=3072,k=3072", "gemm_small_pf2"),   # >= 1024 tiles of 64x64
     ("gemm", "m=2048,n=2048,k=2048", "gemm_wide"),
@@ -454,7 +457,9 @@ def test_gemm_candidate_table():
     ("gemm", 256, 512, 64, 4, 256),                  # fewer tiles than slots
     ("gemm_mid", 1000, 1000, 8, 64, 256),
     ("gemm_ksplit", 512, 512, 512, 256, 512),
-    ("gemm_wide", 2048, 2048, 2048, 512, 512),
+    ("gemm_wide", 2048, 2048, 2048, 256, 512),      # persistent: one per CU
+    ("gemm_wide", 6144, 6144, 1024, 256, 512),
+    ("gemm_wide", 1000, 1000, 64, 64, 512),         # fewer tiles than CUs
     ("gemm_m16_w2x4_t4x2_k16_p1_dma", 1000, 1000, 64, 64, 512),   # 128 x 128 tiles, 8 waves
 ])
 def test_gemm_candidate_geometry(symbol, m, n, k, grid, block):

@@ -218,10 +218,10 @@ def test_gemm_padded_c_rows(dev, extra):
 
 @pytest.mark.parametrize("m,n,k,grid", [
     (8192, 8192, 256, 512),     # gemm: 2048 tiles of 128x256 over 512 persistent workgroups
-    (6144, 6144, 1024, 4608),   # gemm_wide: 4608 tiles of 64x128 at 512 threads, 18 full rounds
-    (2048, 2048, 8192, 512),    # gemm_wide, deep K
+    (6144, 6144, 1024, 256),    # gemm_wide: 2304 tiles of 128x128 over 256 persistent workgroups
+    (2048, 2048, 8192, 256),    # gemm_wide, deep K: one tile per workgroup
     (3072, 3072, 3072, 2304),   # gemm_small_pf2 (2304 tiles of 64x64)
-    (8192, 1024, 8192, 512),    # gemm_mid: 512 tiles of 128x128
+    (8192, 1024, 8192, 256),    # gemm_wide: 512 tiles of 128x128, two per workgroup
     (4096, 4096, 4096, 512),    # gemm: one full round of 128x256
     (512, 512, 1024, 256),      # gemm_ksplit: 256 tiles of 32x32 at 512 threads
     (512, 470, 4100, 240),      # gemm_ksplit_deep: edge tiles in n, a partial last K chunk
