@@ -93,6 +93,25 @@ __device__ __forceinline__ void qk_tile(v16f (&s)[2], const float4 (&q)[8], cons
   }
 }
 
+// Asks the scheduler to place the 16 fragment reads of the MFMA block just
+// issued (qk_tile's K rows, or the PV block's V^T rows) one by one among
+// its first 16 MFMAs. Left to itself it issued them as a burst ahead of the
+// MFMAs, and a wave waited on LDS about once per LDS instruction. Same
+// instructions, same MFMA order per accumulator, so the same bits. Kernel
+// trace, variants interleaved launch by launch over rotated inputs: 1024
+// keys 142.7 -> 139.5 us, 4096 keys 2029 -> 2022 (level); after the S^T
+// block alone, or with the softmax's VALU work interleaved with the S^T
+// block's last 48 MFMAs, the same. One read per two or four MFMAs, or
+// reads issued one or two chunks ahead, measured slower (they also took
+// the registers to 253-256).
+__device__ __forceinline__ void interleave_reads() {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+  }
+}
+
 // Online-softmax update of one tile's S^T (into P, in place), then O^T += V^T P^T.
 template <bool MASK>
 __device__ __forceinline__ void softmax_pv(v16f (&o)[2], float &m, float &l, v16f (&s)[2],
@@ -262,7 +281,9 @@ __device__ __forceinline__ void attention_slice(const float *__restrict__ Qg, co
         load_k(kr, rk, ks, (t + 2) * TK, tid);
         load_v(vr, rv, vs, (t + 1) * TK, tid);
         qk_tile(sn, q, Ks + (cur ^ 1) * TK * LDK, lane);
+        interleave_reads();
         softmax_pv<false>(o, m, l, sc, Vt + cur * D * LDV, t * TK, seq, lane);
+        interleave_reads();
         store_k(kr, Ks + cur * TK * LDK, tid);
         store_v(vr, Vt + (cur ^ 1) * D * LDV, tid);
         __syncthreads();
