@@ -52,9 +52,9 @@ METRIC = "GEMM-8192 fp32 TFLOPS + softmax/scan HBM GB/s, % of MI355X roofline"
 # profiles/templates_baseline_sizes_hbm_traffic.md. Constants of that profile
 # (median dispatch), not measured by the run that reports them.
 PMC_TRAFFIC_BYTES = {
-    "vecadd": 201358958, "softmax": 33658486, "layernorm": 33720946, "scan": 539056269, "scan_1e6": 8200868,
-    "fused_gelu": 536931260, "fused_gelu_2^22": 33632503, "gemm": 3638696788, "gemm_8192x8192x256": 371620843, "gemm_2048": 117554965,
-    "gemm_512": 10558899, "attention": 268738270, "attention_s1024": 67421865,
+    "vecadd": 201358990, "softmax": 33658494, "layernorm": 33720954, "scan": 539336957, "scan_1e6": 8203430,
+    "fused_gelu": 536932028, "fused_gelu_2^22": 33633535, "gemm": 3634428880, "gemm_8192x8192x256": 371291006, "gemm_2048": 117639960,
+    "gemm_512": 10543541, "attention": 268738430, "attention_s1024": 67421873,
 }
 PMC_TRAFFIC_SOURCE = "profiles/templates_baseline_sizes_hbm_traffic.md (constant, not measured by this run)"
 
