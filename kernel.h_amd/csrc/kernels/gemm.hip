@@ -24,11 +24,12 @@
 //       `gemm_mid`    128x128 tiles (64x64 per wave), 32-deep slabs (the
 //                     tune cache's; `gemm_wide` outscores it wherever both
 //                     fit);
-//       `gemm_small`  64x64 tiles, for grids the larger tiles would fill
-//                     unevenly (1024^3, 960^3);
-//       `gemm_small_pf2` the same tiles on 16x16 MFMAs with two-ahead
-//                     prefetch, when they number more than one per CU
-//                     (1536^3 to 3584^3);
+//       `gemm_small`  64x64 tiles on eight waves of 16x16 MFMAs (16x32 per
+//                     wave) in the persistent direct-to-LDS ring, two
+//                     workgroups per CU, for grids the larger tiles would
+//                     fill unevenly (1024^3, 960^3, 1536^3 to 3584^3);
+//       `gemm_small_pf2` 64x64 tiles on four waves of 16x16 MFMAs with
+//                     two-ahead register prefetch (the tune cache's);
 //       `gemm_wide`   128x128 tiles on eight waves of 16x16 MFMAs (32x64
 //                     per wave), 32-deep slabs in `gemm`'s persistent
 //                     direct-to-LDS ring, one workgroup per CU, where its
@@ -45,7 +46,7 @@
 //     after the slab's first 8-deep chunk, so the next slab's first fragments
 //     are read while the rest of this one feeds the MFMAs. Against staging the
 //     slab through registers and ds_write (still used by `gemm_mid` and
-//     `gemm_small`, where it measured as fast) that is +2% at 8192^3: the
+//     `gemm_small_pf2`) that is +2% at 8192^3: the
 //     stores and the wait for them sat between a wave's last MFMA of one slab
 //     and its first of the next.
 //   * LDS holds A as [m][k] (one ds_read_b128 per lane delivers four k
@@ -80,7 +81,9 @@ using khg::kThreads;
 static_assert(Tile<2, 4, 16, true>::BM == KH_GEMM_BM && Tile<2, 4, 16, true>::BN == KH_GEMM_BN, "launcher tile size");
 static_assert(Tile<2, 2, 32, false>::BM == KH_GEMM_MID_BM && Tile<2, 2, 32, false>::BN == KH_GEMM_MID_BN,
               "launcher tile size");
-static_assert(Tile<1, 1, 32, false>::BM == KH_GEMM_SMALL_BM && Tile<1, 1, 32, false>::BN == KH_GEMM_SMALL_BN &&
+static_assert(Tile<1, 2, 32, true, 4, 2, 16>::BM == KH_GEMM_SMALL_BM &&
+                  Tile<1, 2, 32, true, 4, 2, 16>::BN == KH_GEMM_SMALL_BN &&
+                  Tile<1, 2, 32, true, 4, 2, 16>::NT == KH_GEMM_SMALL_THREADS &&
                   Tile<2, 2, 32, false, 2, 2, 16>::BM == KH_GEMM_SMALL_BM &&
                   Tile<2, 2, 32, false, 2, 2, 16>::BN == KH_GEMM_SMALL_BN,
               "launcher tile size (gemm_small and gemm_small_pf2)");
@@ -125,11 +128,22 @@ gemm_mid(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(floa
   gemm_entry<2, 2, 32, true, false>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
 }
 
-// Same arguments and results with 64x64 tiles.
-extern "C" __global__ void __launch_bounds__(kThreads)
+// Same arguments and results with 64x64 tiles on eight waves (4 x 2, each
+// 16x32 as 1x2 blocks of v_mfma_f32_16x16x4f32), 32-deep slabs through
+// `gemm`'s persistent direct-to-LDS ring; 49.5 KB of LDS and 86 VGPRs, so
+// two workgroups per CU. Kernel trace, interleaved launches, same bits,
+// against the 64x64 tiles it replaced (four waves, register-staged
+// slabs; and `gemm_small_pf2` where that was the launcher's choice):
+// 1024^3 28.2 -> 23.7 us, 1024x1024x512 16.3 -> 13.5-14.9,
+// 1024x1024x8192 201.5 -> 160.9, 1536^3 86.8 -> 83.6, 2048x1024x1024 45.0
+// -> 41.9, 2560^3-3584^3 within 1.3%. One workgroup per CU: 1536^3 91.0.
+// The tile split assumes 512 threads: any other launch is refused by
+// writing NaN over C.
+extern "C" __global__ void __launch_bounds__(KH_GEMM_SMALL_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_small(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
-  KH_GEMM_ENTRY_CHECK(kThreads);
-  gemm_entry<1, 1, 32, false, false>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0, C_s0);
+  KH_GEMM_ENTRY_CHECK(KH_GEMM_SMALL_THREADS);
+  khg::gemm_entry_flat<1, 2, 32, true, 4, 2, 16>(KH_PTR(A), KH_PTR(B), KH_PTR(C), A_n0, B_n1, A_n1, A_s0, B_s0,
+                                                 C_s0);
 }
 
 // Same arguments and results with 64x64 tiles on v_mfma_f32_16x16x4f32 (each
@@ -138,8 +152,9 @@ gemm_small(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(fl
 // The tune space found the 16x16 form faster than the same tiles on 32x32
 // MFMAs at every shape timed (rotated U[-1,1] inputs, warm clocks): 2048^3
 // 121.5 vs 117.0, 3072^3 123.4 vs 114.2, 2048x2048x8192 127.6 vs 108.1,
-// 6144x6144x1024 125.0 vs 121.1 TFLOP/s; level at 1536^3. With one tile per
-// CU the fewer barriers of `gemm_small` still win (1024^3: 73.9 vs 68.1).
+// 6144x6144x1024 125.0 vs 121.1 TFLOP/s; level at 1536^3. The persistent
+// eight-wave `gemm_small` has since matched or beaten it at every shape
+// timed, so the launcher no longer picks it; a tune cache can.
 extern "C" __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_small_pf2(KH_MEMREF2(const float, A), KH_MEMREF2(const float, B), KH_MEMREF2(float, C)) {
   KH_GEMM_ENTRY_CHECK(kThreads);

@@ -29,6 +29,8 @@
 #define KH_GEMM_MID_BN 128
 #define KH_GEMM_SMALL_BM 64
 #define KH_GEMM_SMALL_BN 64
+// `gemm_small` runs eight waves (512 threads), two workgroups per CU.
+#define KH_GEMM_SMALL_THREADS 512
 // `gemm_wide`: 128x128 tiles on eight waves (512 threads), one workgroup per
 // CU, persistent.
 #define KH_GEMM_WIDE_BM 128
@@ -41,8 +43,8 @@
 // take the best. `gemm` and `gemm_mid` run two workgroups per CU, so a round
 // is 2 x KH_GEMM_CUS tiles and a half-empty last round costs a full one;
 // `gemm_wide` runs one per CU (a round of KH_GEMM_CUS tiles); the 64x64
-// tiles are light enough that a partial round costs little, so their rounds
-// are counted per CU. Fitted on 20 shapes from 1024^3 to 8192^3 (square,
+// tiles (`gemm_small`, persistent, two per CU) are light enough that a
+// partial round costs little, so their rounds are counted per CU. Fitted on 20 shapes from 1024^3 to 8192^3 (square,
 // skinny, rectangular, deep K) timed with rotated U[-1,1] inputs and warm
 // clocks: the choice is the measured best or within 3% of it on all of them.
 // `gemm_wide`'s rate was refitted when it became the persistent 128x128
@@ -59,10 +61,6 @@
 #define KH_GEMM_RATE_MID 135
 #define KH_GEMM_RATE_WIDE 137
 #define KH_GEMM_RATE_SMALL 126
-// Where the 64x64 tiles are chosen and number more than this (one per CU),
-// the launcher takes `gemm_small_pf2` (16x16 MFMAs, two-ahead prefetch)
-// instead of `gemm_small`.
-#define KH_GEMM_SMALL_PF2_TILES 256
 // `gemm_ksplit`: 32x32 tiles, K split over the 8 waves of a 512-thread
 // workgroup. The launcher takes it when its tiles fit one round (at most
 // one workgroup per CU): there the larger tiles leave three CUs in four idle.
@@ -70,10 +68,13 @@
 // every 32x32 tile is whole with K a multiple of KH_GEMM_KSPLIT_INTERIOR_K
 // (the K-split symbols' unconditional-load path), from
 // KH_GEMM_KSPLIT_MIN_K on; the workgroups then loop over their tiles.
-// Kernel trace, rotated inputs, against `gemm_small`: 640^3 11.5 vs 18.0
-// us, 768^3 18.0 vs 21.2, 1024x512x512 10.2 vs 15.2, 256x2048x2048 25.5 vs
-// 50.3, 512x1536x1024 21.5 vs 27.4; level at 768x768x256 and 896^3; at
-// 1024^3 (256 tiles of 64x64) level, at 1024x1024x512 slower (17.3 vs 15.9).
+// Kernel trace, rotated inputs, against the four-wave register-staged
+// 64x64 tiles `gemm_small` then had: 640^3 11.5 vs 18.0 us, 768^3 18.0 vs
+// 21.2, 1024x512x512 10.2 vs 15.2, 256x2048x2048 25.5 vs 50.3,
+// 512x1536x1024 21.5 vs 27.4; level at 768x768x256 and 896^3; at 1024^3
+// (256 tiles of 64x64) level, at 1024x1024x512 slower (17.3 vs 15.9).
+// Against the persistent eight-wave `gemm_small`: 768^3 level (18.0 vs
+// 17.8), 512x512x2048 14.6 vs 40.4.
 #define KH_GEMM_KSPLIT_BM 32
 #define KH_GEMM_KSPLIT_BN 32
 #define KH_GEMM_KSPLIT_THREADS 512

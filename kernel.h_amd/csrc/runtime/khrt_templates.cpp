@@ -198,7 +198,7 @@ struct GemmCandidate {
 const GemmCandidate kGemmCandidates[] = {
     {"gemm", "gemm", 32, 2, 2, 2, 4, 16, 1, kPersistent, true},
     {"gemm_mid", "gemm", 32, 2, 2, 2, 2, 32, 1, kRegs, true},
-    {"gemm_small", "gemm", 32, 2, 2, 1, 1, 32, 0, kRegs, true},
+    {"gemm_small", "gemm", 16, 4, 2, 1, 2, 32, 1, kPersistent, true},
     {"gemm_small_pf2", "gemm", 16, 2, 2, 2, 2, 32, 1, kPf2, true},
     {"gemm_wide", "gemm", 16, 4, 2, 2, 4, 32, 1, kPersistent, true},
     {"gemm_ksplit", "gemm", 32, 1, 1, 1, 1, 8, 0, kKsplit, true},
@@ -218,15 +218,17 @@ const GemmCandidate *find_gemm_candidate(const char *symbol) {
 
 // Grid of a candidate at m x n: one workgroup per tile, except the
 // persistent symbols, which get one round of resident workgroups and loop:
-// two per CU for `gemm` (four waves), one per CU for `gemm_wide` (eight
-// waves, 99 KB of LDS).
+// two per CU for `gemm` and `gemm_small`, one per CU for `gemm_wide` (99 KB
+// of LDS).
 int64_t candidate_grid(const GemmCandidate &c, int64_t m, int64_t n) {
   const int64_t tiles = ceil_div(m, c.bm()) * ceil_div(n, c.bn());
   // The K-split symbols loop over their tiles as well: one workgroup per CU
   // (their registers allow no more) measured better than one per tile
   // beyond a round (768^3 18.0 vs 19.0 us, 512x1024x1024 15.1 vs 15.7).
   if (c.ksplit()) return std::min<int64_t>(tiles, KH_GEMM_CUS);
-  if (c.pipe == kPersistent) return std::min<int64_t>(tiles, c.waves() > 4 ? KH_GEMM_ROUND_WIDE : KH_GEMM_ROUND_BIG);
+  if (c.pipe == kPersistent) {
+    return std::min<int64_t>(tiles, std::strcmp(c.symbol, "gemm_wide") == 0 ? KH_GEMM_CUS : 2 * KH_GEMM_CUS);
+  }
   return tiles;
 }
 
@@ -346,7 +348,7 @@ const char *heuristic_gemm_symbol(int64_t m, int64_t n, int64_t k) {
   if (big >= mid && big >= wide && big >= small) return "gemm";
   if (mid >= wide && mid > small) return "gemm_mid";
   if (wide > small) return "gemm_wide";
-  return tiles64 > KH_GEMM_SMALL_PF2_TILES ? "gemm_small_pf2" : "gemm_small";
+  return "gemm_small";
 }
 
 // The launcher's GEMM candidate: the tune cache's choice for this shape when

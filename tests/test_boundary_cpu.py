@@ -271,13 +271,13 @@ def test_kernarg_segment_is_2n_plus_3_slots(name, nslots):
     ("gemm", "m=12288,n=12288,k=1024", (512, 1, 1), (256, 1, 1)),    # 4608 tiles: 9 per workgroup
     ("gemm", "m=8192,n=1024,k=8192", (256, 1, 1), (512, 1, 1)),       # gemm_wide: 512 tiles of 128x128, 2 each
     ("gemm", "m=6144,n=6144,k=1024", (256, 1, 1), (512, 1, 1)),       # gemm_wide: 2304 tiles of 128x128, 9 each
-    ("gemm", "m=3072,n=3072,k=3072", (2304, 1, 1), (256, 1, 1)),      # 64x64 (gemm_small_pf2)
+    ("gemm", "m=3072,n=3072,k=3072", (512, 1, 1), (512, 1, 1)),       # 2304 tiles of 64x64 (gemm_small), 4.5 each
     ("gemm", "m=2048,n=2048,k=2048", (256, 1, 1), (512, 1, 1)),       # gemm_wide: 256 tiles of 128x128, one round
-    ("gemm", "m=1024,n=1024,k=1024", (256, 1, 1), (256, 1, 1)),       # 64x64
+    ("gemm", "m=1024,n=1024,k=1024", (256, 1, 1), (512, 1, 1)),       # 64x64 (gemm_small), one each
     ("gemm", "m=512,n=512,k=512", (256, 1, 1), (512, 1, 1)),        # gemm_ksplit: 256 tiles of 32x32, 8 waves
     ("gemm", "m=768,n=768,k=768", (256, 1, 1), (512, 1, 1)),        # 144 tiles of 64x64: K split, 576 tiles looped
-    ("gemm", "m=960,n=960,k=960", (225, 1, 1), (256, 1, 1)),        # K not a multiple of 128: 64x64
-    ("gemm", "m=768,n=768,k=128", (144, 1, 1), (256, 1, 1)),        # K below 256: 64x64
+    ("gemm", "m=960,n=960,k=960", (225, 1, 1), (512, 1, 1)),        # K not a multiple of 128: 64x64
+    ("gemm", "m=768,n=768,k=128", (144, 1, 1), (512, 1, 1)),        # K below 256: 64x64
     ("gemm", "m=512,n=512,k=8192", (256, 1, 1), (512, 1, 1)),       # gemm_ksplit_deep
     ("attention", "batch=4,heads=16,seq=4096,head_dim=64", (32, 16, 4), (256, 1, 1)),
 ])
@@ -291,11 +291,11 @@ def test_launcher_geometry(name, shape, grid, block):
     ("gemm", "m=8192,n=1024,k=8192", "gemm_wide"),       # outscores gemm_mid (same tile, one round per CU)
     ("gemm", "m=4096,n=2048,k=4096", "gemm_wide"),
     ("gemm", "m=4096,n=4096,k=4096", "gemm"),            # one round of 128x256 against four of 128x128
-    ("gemm", "m=2560,n=2560,k=2560", "gemm_small_pf2"),  # 400 tiles of 128x128: a partial second round
+    ("gemm", "m=2560,n=2560,k=2560", "gemm_small"),      # 400 tiles of 128x128: a partial second round
     ("gemm", "m=1024,n=1024,k=1024", "gemm_small"),
-    ("gemm", "m=3072,n=3072,k=3072", "gemm_small_pf2"),   # >= 1024 tiles of 64x64
+    ("gemm", "m=3072,n=3072,k=3072", "gemm_small"),       # 2304 tiles of 64x64
     ("gemm", "m=2048,n=2048,k=2048", "gemm_wide"),
-    ("gemm", "m=1536,n=1536,k=1536", "gemm_small_pf2"),  # 576 tiles of 64x64: more than one per CU
+    ("gemm", "m=1536,n=1536,k=1536", "gemm_small"),      # 576 tiles of 64x64: more than one per CU
     ("gemm", "m=512,n=512,k=2048", "gemm_ksplit_deep"),   # 256 tiles of 32x32, deep K
     ("gemm", "m=512,n=512,k=1024", "gemm_ksplit"),
     ("gemm", "m=300,n=520,k=100", "gemm_ksplit"),

@@ -9,12 +9,13 @@
 * Ragged shapes, the reference launch geometry, and the A*B^T negative
   control (e2e_gemm_test.cpp:289-375).
 * Every tile symbol (`gemm` 128x256 persistent, `gemm_mid` 128x128,
-  `gemm_small` and `gemm_small_pf2` 64x64, `gemm_ksplit` and
-  `gemm_ksplit_deep` 32x32 with K split over the workgroup's waves, at any
-  64..512 threads) gives the same results
-  at every shape and grid, whichever the launcher would pick; and the
-  launcher's own grid (one workgroup per tile, or at most two per CU for
-  `gemm`; XCD-remapped) is checked at a shape it sends to each symbol.
+  `gemm_wide` 128x128 persistent on 8 waves, `gemm_small` 64x64 persistent
+  on 8 waves, `gemm_small_pf2` 64x64, `gemm_ksplit` and `gemm_ksplit_deep`
+  32x32 with K split over the workgroup's waves, at any 64..512 threads)
+  gives the same results at every shape and grid, whichever the launcher
+  would pick; and the launcher's own grid (one workgroup per tile, or one
+  round of resident workgroups for the persistent symbols; XCD-remapped)
+  is checked at a shape it sends to each symbol.
 """
 import json
 
@@ -121,7 +122,7 @@ def test_every_gemm_symbol_at_every_shape(dev, symbol, m, n, k):
     dA, dB, dC = up(A), up(B), empty(m * n)
     args = kh.LaunchArgs().add_memref(dA, [m, k]).add_memref(dB, [k, n]).add_memref(dC, [m, n])
     say(f"{symbol} m={m} n={n} k={k}")
-    block = 512 if symbol == "gemm_wide" else 256  # gemm_wide's tile split is for 8 waves
+    block = 512 if symbol in ("gemm_wide", "gemm_small") else 256  # their tile split is for 8 waves
     kh.kernel_launch(f, (37, 1, 1), (block, 1, 1), args)  # grid-strided: any grid
     C = down(dC, m * n).reshape(m, n)
     if k <= 4096:
@@ -152,7 +153,7 @@ def test_gemm_symbols_random_shapes_exact(dev):
         for sym, f in fns.items():
             grid = int(rng.choice([1, 3, 8, 37, 512]))
             block = (int(rng.choice([64, 192, 512])) if sym.startswith("gemm_ksplit")  # 1, 3 or 8 waves
-                     else 512 if sym == "gemm_wide" else 256)
+                     else 512 if sym in ("gemm_wide", "gemm_small") else 256)
             say(f"{sym} m={m} n={n} k={k} grid={grid} block={block}")
             kh.kernel_launch(f, (grid, 1, 1), (block, 1, 1), args)
             assert np.array_equal(down(dC, m * n).reshape(m, n), want), (sym, m, n, k, grid)
@@ -220,7 +221,7 @@ def test_gemm_padded_c_rows(dev, extra):
     (8192, 8192, 256, 512),     # gemm: 2048 tiles of 128x256 over 512 persistent workgroups
     (6144, 6144, 1024, 256),    # gemm_wide: 2304 tiles of 128x128 over 256 persistent workgroups
     (2048, 2048, 8192, 256),    # gemm_wide, deep K: one tile per workgroup
-    (3072, 3072, 3072, 2304),   # gemm_small_pf2 (2304 tiles of 64x64)
+    (3072, 3072, 3072, 512),    # gemm_small: 2304 tiles of 64x64 over 512 persistent workgroups
     (8192, 1024, 8192, 256),    # gemm_wide: 512 tiles of 128x128, two per workgroup
     (4096, 4096, 4096, 512),    # gemm: one full round of 128x256
     (512, 512, 1024, 256),      # gemm_ksplit: 256 tiles of 32x32 at 512 threads
@@ -284,11 +285,12 @@ def test_tune_candidate_refuses_another_block_size(dev):
         assert np.all(np.isnan(down(dC, m * n))), sym
 
 
-@pytest.mark.parametrize("sym,block", [("gemm", 128), ("gemm_mid", 192), ("gemm_small", 64), ("gemm_small_pf2", 128)])
+@pytest.mark.parametrize("sym,block", [("gemm", 128), ("gemm_mid", 192), ("gemm_small", 256), ("gemm_small_pf2", 128)])
 def test_product_symbols_refuse_another_block_size(dev, sym, block):
-    # The 256-thread symbols' tile split assumes four waves: a smaller
-    # workgroup writes NaN over C, never part of each tile. (A larger one is
-    # refused by the launch itself: test_launch_above_the_kernel_bound_is_refused.)
+    # Each symbol's tile split assumes its own wave count (four; eight for
+    # `gemm_small`): a smaller workgroup writes NaN over C, never part of
+    # each tile. (A larger one is refused by the launch itself:
+    # test_launch_above_the_kernel_bound_is_refused.)
     m = n = k = 64
     A, B = O.gemm_int_inputs(m, n, k)
     dA, dB, dC = up(A), up(B), empty(m * n, 0.0)
