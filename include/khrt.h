@@ -231,8 +231,8 @@ KHRT_API int khrt_template_geometry(const char *name, const char *shape, khrt_di
                                     khrt_dim3 *block);
 /* The kernel symbol the launcher runs for a template at a shape ("k=v,k=v"):
  * the template name itself or a variant in the same code object with the
- * same arguments and results (gemm_mid, gemm_small, gemm_small_pf2,
- * softmax_wide, layernorm_wide). Writes a NUL-terminated name of at most cap
+ * same arguments and results (gemm_small, gemm_wide, gemm_ksplit,
+ * gemm_ksplit_deep, softmax_wide, layernorm_wide). Writes a NUL-terminated name of at most cap
  * bytes. No reference counterpart: the reference compiles one symbol per
  * template and shape (emitter.cpp:733-736); callers that report resources
  * for a launch (kernelh compile --resources) need the symbol it runs. */
