@@ -1,5 +1,5 @@
 // fp32 MFMA GEMM building blocks for gfx950, shared by the product kernels
-// (gemm.hip: `gemm`, `gemm_mid`, `gemm_small`, `gemm_small_pf2`) and the tune candidates
+// (gemm.hip: `gemm`, `gemm_mid`, `gemm_small`, `gemm_small_pf2`, `gemm_wide`) and the tune candidates
 // (gemm_tune.hip, used by `kernelh tune`). The design is described at the
 // top of gemm.hip.
 #pragma once
@@ -211,40 +211,9 @@ __device__ __forceinline__ uint32_t lds_addr(const float *p) { return (uint32_t)
 // 32-bit term plus a wave-uniform one (k0 for A, n0 for B), which keeps the
 // offsets of every load of a slab in registers even where the tile's
 // accumulators leave few (rows past M still read 0 through the resource).
-template <class T, bool ALN = false>
-__device__ __forceinline__ void dma_slab(const float *__restrict__ A, const float *__restrict__ B, int64_t M,
-                                         int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t m0, int64_t n0,
-                                         int64_t k0, float *As, float *Bs, int wave, int lane) {
-  const u32x4 ra = rows_desc(A + m0 * lda, (M - m0) < T::BM ? (M - m0) : T::BM, lda);
-  const u32x4 rb = rows_desc(B + k0 * ldb, (K - k0) < T::BK ? (K - k0) : T::BK, ldb);
-#pragma unroll
-  for (int i = 0; i < T::NA; ++i) {
-    const int idx0 = 64 * wave + T::NT * i;  // first float4 of this wave's instruction
-    const int idx = idx0 + lane;
-    const int ar = idx / T::QP, ak = 4 * ((idx % T::QP) ^ T::aswz(ar));
-    uint32_t aoff;
-    if constexpr (ALN)
-      aoff = ((uint32_t)ar * (uint32_t)lda + (uint32_t)ak) * 4u + (uint32_t)k0 * 4u;
-    else
-      aoff = (k0 + ak < K) ? (uint32_t)((ar * lda + k0 + ak) * 4) : kOutside;
-    dma16(ra, aoff, lds_addr(As + 4 * idx0));
-  }
-#pragma unroll
-  for (int i = 0; i < T::NB; ++i) {
-    const int idx0 = 64 * wave + T::NT * i;
-    const int idx = idx0 + lane;
-    const int bk = idx / T::BROW, bn = 4 * (idx % T::BROW);
-    uint32_t boff;
-    if constexpr (ALN)
-      boff = ((uint32_t)bk * (uint32_t)ldb + (uint32_t)bn) * 4u + (uint32_t)n0 * 4u;
-    else
-      boff = (n0 + bn < N) ? (uint32_t)((bk * ldb + n0 + bn) * 4) : kOutside;
-    dma16(rb, boff, lds_addr(Bs + T::b_at(idx0 / T::BROW, 4 * (idx0 % T::BROW))));
-  }
-}
-
-// Loads L0..L1-1 of dma_slab's (A's NA, then B's NB), so that a slab's
-// loads can be spread between MFMAs.
+//
+// dma_part issues loads L0..L1-1 of a slab (A's NA, then B's NB), so that a
+// slab's loads can be spread between MFMAs; dma_slab issues all of them.
 template <class T, bool ALN, int L0, int L1>
 __device__ __forceinline__ void dma_part(const float *__restrict__ A, const float *__restrict__ B, int64_t M,
                                          int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t m0, int64_t n0,
@@ -277,6 +246,13 @@ __device__ __forceinline__ void dma_part(const float *__restrict__ A, const floa
       boff = (n0 + bn < N) ? (uint32_t)((bk * ldb + n0 + bn) * 4) : kOutside;
     dma16(rb, boff, lds_addr(Bs + T::b_at(idx0 / T::BROW, 4 * (idx0 % T::BROW))));
   }
+}
+
+template <class T, bool ALN = false>
+__device__ __forceinline__ void dma_slab(const float *__restrict__ A, const float *__restrict__ B, int64_t M,
+                                         int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t m0, int64_t n0,
+                                         int64_t k0, float *As, float *Bs, int wave, int lane) {
+  dma_part<T, ALN, 0, T::NA + T::NB>(A, B, M, N, K, lda, ldb, m0, n0, k0, As, Bs, wave, lane);
 }
 
 // Wait until at most N vector-memory operations of this wave are in flight
