@@ -52,9 +52,9 @@ METRIC = "GEMM-8192 fp32 TFLOPS + softmax/scan HBM GB/s, % of MI355X roofline"
 # profiles/templates_baseline_sizes_hbm_traffic.md. Constants of that profile
 # (median dispatch), not measured by the run that reports them.
 PMC_TRAFFIC_BYTES = {
-    "vecadd": 201358990, "softmax": 33658494, "layernorm": 33720954, "scan": 539336957, "scan_1e6": 8203430,
-    "fused_gelu": 536932028, "fused_gelu_2^22": 33633535, "gemm": 3634428880, "gemm_8192x8192x256": 371291006, "gemm_2048": 117639960,
-    "gemm_512": 10543541, "attention": 268738430, "attention_s1024": 67421873,
+    "vecadd": 201358270, "softmax": 33658314, "layernorm": 33720774, "scan": 539174466, "scan_1e6": 8198139,
+    "fused_gelu": 536929788, "fused_gelu_2^22": 33632843, "gemm": 3636852993, "gemm_8192x8192x256": 371314749, "gemm_2048": 117641828,
+    "gemm_512": 10544554, "attention": 268738094, "attention_s1024": 67421693,
 }
 PMC_TRAFFIC_SOURCE = "profiles/templates_baseline_sizes_hbm_traffic.md (constant, not measured by this run)"
 
