@@ -184,6 +184,9 @@ struct GemmCandidate {
   const char *co;
   int mfma, wgm, wgn, wtm, wtn, bk, prio, pipe;
   bool product;
+  // Persistent symbols: workgroups resident per CU (their LDS and
+  // registers), so the launcher's grid is one round of them.
+  int per_cu = 2;
   bool ksplit() const { return pipe == kKsplit || pipe == kKsplitDeep; }
   // K-split: each of the 8 waves holds the whole 32x32 tile for its K range.
   int waves() const { return ksplit() ? KH_GEMM_KSPLIT_THREADS / 64 : wgm * wgn; }
@@ -200,7 +203,7 @@ const GemmCandidate kGemmCandidates[] = {
     {"gemm_mid", "gemm", 32, 2, 2, 2, 2, 32, 1, kRegs, true},
     {"gemm_small", "gemm", 16, 4, 2, 1, 2, 32, 1, kPersistent, true},
     {"gemm_small_pf2", "gemm", 16, 2, 2, 2, 2, 32, 1, kPf2, true},
-    {"gemm_wide", "gemm", 16, 4, 2, 2, 4, 32, 1, kPersistent, true},
+    {"gemm_wide", "gemm", 16, 4, 2, 2, 4, 32, 1, kPersistent, true, 1},
     {"gemm_ksplit", "gemm", 32, 1, 1, 1, 1, 8, 0, kKsplit, true},
     {"gemm_ksplit_deep", "gemm", 32, 1, 1, 1, 1, 8, 0, kKsplitDeep, true},
     KH_GEMM_TUNE_CONFIGS(KH_TUNE_CANDIDATE)};
@@ -217,18 +220,16 @@ const GemmCandidate *find_gemm_candidate(const char *symbol) {
 }
 
 // Grid of a candidate at m x n: one workgroup per tile, except the
-// persistent symbols, which get one round of resident workgroups and loop:
-// two per CU for `gemm` and `gemm_small`, one per CU for `gemm_wide` (99 KB
-// of LDS).
+// persistent symbols, which get one round of resident workgroups and loop
+// (per_cu: two for `gemm` and `gemm_small`, one for `gemm_wide`, whose
+// 99 KB of LDS allow no more).
 int64_t candidate_grid(const GemmCandidate &c, int64_t m, int64_t n) {
   const int64_t tiles = ceil_div(m, c.bm()) * ceil_div(n, c.bn());
   // The K-split symbols loop over their tiles as well: one workgroup per CU
   // (their registers allow no more) measured better than one per tile
   // beyond a round (768^3 18.0 vs 19.0 us, 512x1024x1024 15.1 vs 15.7).
   if (c.ksplit()) return std::min<int64_t>(tiles, KH_GEMM_CUS);
-  if (c.pipe == kPersistent) {
-    return std::min<int64_t>(tiles, std::strcmp(c.symbol, "gemm_wide") == 0 ? KH_GEMM_CUS : 2 * KH_GEMM_CUS);
-  }
+  if (c.pipe == kPersistent) return std::min<int64_t>(tiles, int64_t(c.per_cu) * KH_GEMM_CUS);
   return tiles;
 }
 
