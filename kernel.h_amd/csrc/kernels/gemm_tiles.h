@@ -315,25 +315,9 @@ __device__ __forceinline__ void read_frag(Frag<WTM, WTN> &f, const float *__rest
   }
 }
 
-template <int WTM, int WTN, class Acc>
-__device__ __forceinline__ void mfma_frag(Acc (&acc)[WTM][WTN], const Frag<WTM, WTN> &f) {
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-#pragma unroll
-    for (int i = 0; i < WTM; ++i) {
-      const float av = s == 0 ? f.a[i].x : s == 1 ? f.a[i].y : s == 2 ? f.a[i].z : f.a[i].w;
-#pragma unroll
-      for (int j = 0; j < WTN; ++j) {
-        if constexpr (sizeof(Acc) == sizeof(v16f))
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, f.b[j][s], acc[i][j], 0, 0, 0);
-        else
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, f.b[j][s], acc[i][j], 0, 0, 0);
-      }
-    }
-}
-
-// MFMA steps S0..S1-1 of a chunk (mfma_frag is steps 0..3): each
-// accumulator still takes its steps in order, so the same bits.
+// MFMA steps S0..S1-1 of a chunk: a chunk's four steps can be split around
+// other work, each accumulator still taking its steps in order (the same
+// bits).
 template <int WTM, int WTN, int S0, int S1, class Acc>
 __device__ __forceinline__ void mfma_frag_s(Acc (&acc)[WTM][WTN], const Frag<WTM, WTN> &f) {
 #pragma unroll
@@ -351,12 +335,19 @@ __device__ __forceinline__ void mfma_frag_s(Acc (&acc)[WTM][WTN], const Frag<WTM
     }
 }
 
-// One slab's chunks from LDS. For eight-wave tiles on 16x16 MFMAs
-// (`gemm_wide`), chunk c+1's fragment reads are interleaved with chunk c's
-// MFMAs, one read per two (kernel trace, variants interleaved launch by
-// launch, same bits: 2048^3 142.5 -> 141.3 us, 6144x6144x1024 593.8 ->
-// 586.1). The same change slowed the four-wave tiles (`gemm_small` 8-10%,
-// `gemm_mid` 0.5-1%), which keep one chunk's reads before its MFMAs.
+template <int WTM, int WTN, class Acc>
+__device__ __forceinline__ void mfma_frag(Acc (&acc)[WTM][WTN], const Frag<WTM, WTN> &f) {
+  mfma_frag_s<WTM, WTN, 0, 4>(acc, f);
+}
+
+// One slab's chunks from LDS (the register-staged pipelines). For eight-wave
+// tiles on 16x16 MFMAs (the tune space's; `gemm_wide` was one before it
+// moved to the persistent ring), chunk c+1's fragment reads are interleaved
+// with chunk c's MFMAs, one read per two (kernel trace, variants
+// interleaved launch by launch, same bits: 2048^3 142.5 -> 141.3 us,
+// 6144x6144x1024 593.8 -> 586.1). The same change slowed the four-wave
+// tiles (the then four-wave `gemm_small` 8-10%, `gemm_mid` 0.5-1%), which
+// keep one chunk's reads before its MFMAs.
 template <int WTM, int WTN, class T>
 __device__ __forceinline__ void compute_slab(AccOf<T> (&acc)[WTM][WTN], const float *__restrict__ As,
                                              const float *__restrict__ Bs, int wm, int wn, int lane) {
